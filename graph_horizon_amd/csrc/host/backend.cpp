@@ -1,0 +1,764 @@
+// gfx950 backend: the C ABI of include/gh_backend.h over the HIP runtime.
+// Kernels come from gfx950 code objects loaded with hipModuleLoad and are launched with
+// hipModuleLaunchKernel on the backend's single stream.
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+namespace {
+
+struct KernelName {
+    GhKernel id;
+    const char* name;
+};
+
+const KernelName kKernels[] = {
+    {K_REPACK_Q4K, "gh_repack_q4k"},       {K_REPACK_Q6K, "gh_repack_q6k"},
+    {K_DEQUANT_Q4K, "gh_dequant_q4k"},     {K_DEQUANT_Q6K, "gh_dequant_q6k"},
+    {K_GEMV_Q4K_R1, "gh_gemv_q4k_r1"},     {K_GEMV_Q4K_R2, "gh_gemv_q4k_r2"},
+    {K_GEMV_Q4K_R4, "gh_gemv_q4k_r4"},     {K_GEMV_Q6K_R1, "gh_gemv_q6k_r1"},
+    {K_GEMV_Q6K_R2, "gh_gemv_q6k_r2"},     {K_GEMV_Q6K_R4, "gh_gemv_q6k_r4"},
+    {K_RMSNORM, "gh_rmsnorm_x"},           {K_ROPE, "gh_rope"},
+    {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
+    {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
+    {K_ARGMAX_FINAL, "gh_argmax_final"},   {K_ATTN_SPLIT_G1, "gh_attn_split_g1"},
+    {K_ATTN_SPLIT_G2, "gh_attn_split_g2"}, {K_ATTN_SPLIT_G4, "gh_attn_split_g4"},
+    {K_ATTN_SPLIT_G8, "gh_attn_split_g8"}, {K_ATTN_MERGE, "gh_attn_merge"},
+    {K_STEP_ADVANCE, "gh_step_advance"},
+};
+
+const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention"};
+
+constexpr uint32_t kArgmaxBlocks = 256;
+// argmax scratch at the front of the workspace: f32[256] values, u32[256] indices, u32 result
+constexpr size_t kArgmaxBytes = 256 * 4 * 2 + 256;
+
+std::string library_dir() {
+    Dl_info info{};
+    if (dladdr((void*)&gh_create, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t s = p.find_last_of('/');
+        return s == std::string::npos ? std::string(".") : p.substr(0, s);
+    }
+    return ".";
+}
+
+inline uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+bool is_weight(const gh_buf* w) {
+    return w && w->kind == GH_BUF_WEIGHT && (w->format == GH_FMT_Q4_K || w->format == GH_FMT_Q6_K);
+}
+
+int check_enc(gh_backend* b, gh_encoder* enc) {
+    if (!b) return GH_E_INVALID;
+    if (!enc || enc != &b->enc || !b->enc_open) return gh::fail(b, GH_E_STATE, "no open encoder");
+    return GH_OK;
+}
+
+// Record an op's status in the encoder (errors surface again at gh_submit).
+int latch(gh_encoder* enc, int rc) {
+    if (rc != GH_OK && enc && enc->latched == GH_OK) enc->latched = rc;
+    return rc;
+}
+
+bool fits(const gh_buf* buf, uint64_t bytes) { return buf && buf->addr && buf->bytes >= bytes; }
+
+// Yarn::pair / post_scale (backend/rope.rs:60-133) evaluated on the host in FP32 with the same
+// libm calls, so the device rotation table holds the reference's values.
+constexpr float kPi = 3.14159265358979323846f;
+float corr_dim(uint32_t rope_dim, uint32_t original_context, float rotations, float base) {
+    float denom = rotations * 2.0f * kPi;
+    return (float)rope_dim * std::log((float)original_context / denom) / (2.0f * std::log(base));
+}
+void yarn_pair(const gh_yarn* y, uint32_t pair, uint32_t position, float* c, float* s) {
+    float freq_scale = 1.0f / y->factor;
+    float theta_extrap =
+        (float)position * std::pow(y->freq_base, -(2.0f * (float)pair) / (float)y->rope_dim);
+    float theta_interp = freq_scale * theta_extrap;
+    float start = std::fmax(
+        std::floor(corr_dim(y->rope_dim, y->original_context, y->beta_fast, y->freq_base)), 0.0f);
+    float end =
+        std::fmin(std::ceil(corr_dim(y->rope_dim, y->original_context, y->beta_slow, y->freq_base)),
+                  (float)(y->rope_dim - 1));
+    float yv = ((float)pair - start) / std::fmax(end - start, 0.001f);
+    float cl = yv < 0.0f ? 0.0f : (yv > 1.0f ? 1.0f : yv);
+    float ramp = 1.0f - cl;
+    float theta = theta_interp * (1.0f - ramp) + theta_extrap * ramp;
+    *c = std::cos(theta) * 1.0f;
+    *s = std::sin(theta) * 1.0f;
+}
+float yarn_post_query(const gh_yarn* y, uint32_t position) {
+    float bucket = (float)(position / y->original_context);
+    return std::log(bucket + 1.0f) * y->q_temperature_scale + 1.0f;
+}
+
+// IEEE binary32 -> binary16, round to nearest even (overflow to infinity, NaN stays NaN).
+uint16_t f32_to_f16_rne(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u);
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);  // rounds to >= 65520
+    if (ax < 0x38800000u) {  // result is subnormal (or zero) in binary16
+        if (ax < 0x33000000u) return (uint16_t)sign;  // below half the smallest subnormal
+        const uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+        const uint32_t shift = 126u - (ax >> 23);  // 14 + (112 - e) with e the f32 exponent
+        const uint32_t q = m >> shift, rem = m & ((1u << shift) - 1), halfway = 1u << (shift - 1);
+        return (uint16_t)(sign | (q + (rem > halfway || (rem == halfway && (q & 1)))));
+    }
+    const uint32_t q = (ax - 0x38000000u) >> 13, rem = ax & 0x1FFFu;
+    return (uint16_t)(sign | (q + (rem > 0x1000u || (rem == 0x1000u && (q & 1)))));
+}
+
+int total_key(float f) {
+    int32_t b;
+    std::memcpy(&b, &f, 4);
+    b ^= (int32_t)(((uint32_t)(b >> 31)) >> 1);
+    return b;
+}
+
+}  // namespace
+
+namespace gh {
+
+int fail(gh_backend* b, int code, const std::string& msg) {
+    if (b) b->err = msg;
+    return code;
+}
+
+int hip_check(gh_backend* b, hipError_t e, const char* what) {
+    if (e == hipSuccess) return GH_OK;
+    return fail(b, e == hipErrorOutOfMemory ? GH_E_OOM : GH_E_HIP,
+                std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int launch(gh_backend* b, GhKernel k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
+           const void* args) {
+    if (gx == 0 || gy == 0 || gz == 0) return GH_OK;
+    void* params[] = {const_cast<void*>(args)};
+    return hip_check(b, hipModuleLaunchKernel(b->fn[k], gx, gy, gz, bx, 1, 1, 0, b->stream, params,
+                                              nullptr),
+                     "hipModuleLaunchKernel");
+}
+
+int ensure_workspace(gh_backend* b, size_t bytes) {
+    bytes += kArgmaxBytes;
+    if (b->ws_bytes >= bytes) return GH_OK;
+    if (b->capturing) return fail(b, GH_E_STATE, "workspace growth during graph capture");
+    int rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    if (b->ws) (void)hipFree(b->ws);
+    b->ws = nullptr;
+    b->ws_bytes = 0;
+    size_t want = std::max(bytes, (size_t)(4u << 20));
+    rc = hip_check(b, hipMalloc(&b->ws, want), "hipMalloc(workspace)");
+    if (rc) return rc;
+    b->ws_bytes = want;
+    ++b->gen;
+    return GH_OK;
+}
+
+bool yarn_valid(const gh_yarn* y) {
+    if (!y || y->rope_dim == 0 || y->rope_dim % 2 != 0 || y->original_context == 0) return false;
+    const float v[6] = {y->freq_base, y->factor,         y->beta_fast,
+                        y->beta_slow, y->log_multiplier, y->q_temperature_scale};
+    for (float x : v)
+        if (!std::isfinite(x) || x <= 0.0f) return false;
+    return true;
+}
+
+int ensure_rope(gh_backend* b, const gh_yarn* y, uint32_t positions) {
+    GhRopeTable& t = b->rope;
+    bool same = t.table && std::memcmp(&t.yarn, y, sizeof(gh_yarn)) == 0;
+    if (same && t.positions >= positions) return GH_OK;
+    if (b->capturing) return fail(b, GH_E_STATE, "rope table growth during graph capture");
+    uint32_t n = std::max<uint32_t>(positions, 4096);
+    if (same) n = std::max(n, t.positions * 2);
+    const uint32_t pairs = y->rope_dim / 2;
+    std::vector<float> table((size_t)n * pairs * 2), post(n);
+    for (uint32_t p = 0; p < n; ++p) {
+        for (uint32_t j = 0; j < pairs; ++j)
+            yarn_pair(y, j, p, &table[((size_t)p * pairs + j) * 2], &table[((size_t)p * pairs + j) * 2 + 1]);
+        post[p] = yarn_post_query(y, p);
+    }
+    int rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    if (t.table) (void)hipFree(t.table);
+    if (t.post) (void)hipFree(t.post);
+    t.table = t.post = nullptr;
+    t.positions = 0;
+    rc = hip_check(b, hipMalloc(&t.table, table.size() * 4), "hipMalloc(rope)");
+    if (!rc) rc = hip_check(b, hipMalloc(&t.post, post.size() * 4), "hipMalloc(rope)");
+    if (!rc) rc = hip_check(b, hipMemcpy(t.table, table.data(), table.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(rope)");
+    if (!rc) rc = hip_check(b, hipMemcpy(t.post, post.data(), post.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(rope)");
+    if (rc) return rc;
+    t.yarn = *y;
+    t.positions = n;
+    ++b->gen;
+    return GH_OK;
+}
+
+int op_rope(gh_backend* b, const gh_buf* x, uint32_t heads, uint32_t head_dim, uint32_t base,
+            uint32_t rows, uint32_t role, const void* pos_ptr) {
+    GhRopeArgs a{};
+    a.x = x->addr;
+    a.table = (uint64_t)b->rope.table;
+    a.post = role == GH_ROPE_QUERY ? (uint64_t)b->rope.post : 0;
+    a.pos_ptr = (uint64_t)pos_ptr;
+    a.heads = heads;
+    a.head_dim = head_dim;
+    a.pairs = b->rope.yarn.rope_dim / 2;
+    a.base = base;
+    a.rows = rows;
+    uint64_t total = (uint64_t)rows * heads * a.pairs;
+    return launch(b, K_ROPE, ceil_div(total, 256), 1, 1, 256, &a);
+}
+
+int op_kv_write(gh_backend* b, const gh_kv* kv, const gh_buf* k, const gh_buf* v,
+                uint64_t k_elem_off, uint64_t v_elem_off, uint32_t vectors, const void* pos_ptr) {
+    GhKvWriteArgs a{};
+    a.kc = kv->k.addr;
+    a.vc = kv->v.addr;
+    a.k = k->addr;
+    a.v = v->addr;
+    a.pos_ptr = (uint64_t)pos_ptr;
+    a.k_off = k_elem_off;
+    a.v_off = v_elem_off;
+    a.k_count = vectors * kv->head_dim;
+    a.v_count = vectors * kv->value_dim;
+    a.k_stride = kv->kv_heads * kv->head_dim;
+    a.v_stride = kv->kv_heads * kv->value_dim;
+    return launch(b, K_KV_WRITE, ceil_div(std::max(a.k_count, a.v_count), 256), 1, 1, 256, &a);
+}
+
+uint32_t attention_split_len(uint32_t max_len) {
+    uint32_t sl = ceil_div(max_len, 512);
+    sl = ((sl + 63) / 64) * 64;
+    return std::min<uint32_t>(std::max<uint32_t>(sl, 64), 256);
+}
+
+size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits) {
+    size_t n = (size_t)rows * q_heads * splits;
+    return n * 4 * 2 + n * 128 * 4 + 1024;
+}
+
+// Causal GQA attention for `rows` query rows at positions base + r (+ *pos_ptr);
+// max_pos bounds the positions the launch can see (sizes the split grid).
+int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
+                 uint32_t q_heads, uint32_t base, uint32_t rows, uint32_t layer,
+                 const void* pos_ptr, uint32_t max_pos) {
+    const uint32_t group = q_heads / kv->kv_heads;
+    GhKernel k;
+    switch (group) {
+        case 1: k = K_ATTN_SPLIT_G1; break;
+        case 2: k = K_ATTN_SPLIT_G2; break;
+        case 4: k = K_ATTN_SPLIT_G4; break;
+        case 8: k = K_ATTN_SPLIT_G8; break;
+        default: return fail(b, GH_E_UNSUPPORTED, "attention: GQA group must be 1, 2, 4 or 8");
+    }
+    const uint32_t split_len = attention_split_len(max_pos + 1);
+    const uint32_t splits = ceil_div((uint64_t)max_pos + 1, split_len);
+    // bound the partials: process rows in groups that fit a 256 MiB workspace
+    const size_t per_row = attention_workspace(1, q_heads, splits);
+    uint32_t group_rows = (uint32_t)std::max<size_t>(1, ((size_t)256 << 20) / per_row);
+    group_rows = std::min(group_rows, rows);
+    int rc = ensure_workspace(b, attention_workspace(group_rows, q_heads, splits));
+    if (rc) return rc;
+    char* ws = (char*)b->ws + kArgmaxBytes;
+    for (uint32_t r0 = 0; r0 < rows; r0 += group_rows) {
+        const uint32_t nr = std::min(group_rows, rows - r0);
+        const size_t n = (size_t)nr * q_heads * splits;
+        GhAttnArgs a{};
+        a.q = q->addr + (uint64_t)r0 * q_heads * kv->head_dim * 2;
+        a.kc = kv->k.addr;
+        a.vc = kv->v.addr;
+        a.out = out->addr + (uint64_t)r0 * q_heads * kv->value_dim * 2;
+        a.part_m = (uint64_t)ws;
+        a.part_l = (uint64_t)(ws + n * 4);
+        a.part_acc = (uint64_t)(ws + n * 8);
+        a.pos_ptr = (uint64_t)pos_ptr;
+        a.key_dim = kv->head_dim;
+        a.value_dim = kv->value_dim;
+        a.kv_heads = kv->kv_heads;
+        a.q_heads = q_heads;
+        a.layer = layer;
+        a.context = kv->context;
+        a.base = base + r0;
+        a.rows = nr;
+        a.splits = splits;
+        a.split_len = split_len;
+        a.scale = 1.0f / std::sqrt((float)kv->head_dim);
+        rc = launch(b, k, kv->kv_heads, splits, nr, 256, &a);
+        if (!rc) rc = launch(b, K_ATTN_MERGE, q_heads, nr, 1, 128, &a);
+        if (rc) return rc;
+    }
+    return GH_OK;
+}
+
+int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, uint32_t embd,
+             const void* token_ptr) {
+    GhDequantArgs a{};
+    a.w = w->addr;
+    a.out = x->addr;
+    a.row_ptr = (uint64_t)token_ptr;
+    a.wrows = w->rows;
+    a.nb = embd / 256;
+    a.row0 = token;
+    a.rows = 1;
+    return launch(b, w->format == GH_FMT_Q4_K ? K_DEQUANT_Q4K : K_DEQUANT_Q6K,
+                  ceil_div(embd, 256), 1, 1, 256, &a);
+}
+
+int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2) {
+    int rc = ensure_workspace(b, 0);
+    if (rc) return rc;
+    GhArgmaxArgs a{};
+    a.logits = logits->addr;
+    a.part_v = (uint64_t)b->ws;
+    a.part_i = (uint64_t)((char*)b->ws + 1024);
+    a.out = out ? (uint64_t)out : (uint64_t)((char*)b->ws + 2048);
+    a.out2 = (uint64_t)out2;
+    a.n = (uint32_t)vocab;
+    a.blocks = std::min<uint32_t>(kArgmaxBlocks, ceil_div(vocab, 256));
+    rc = launch(b, K_ARGMAX_PARTIAL, a.blocks, 1, 1, 256, &a);
+    if (!rc) rc = launch(b, K_ARGMAX_FINAL, 1, 1, 1, 256, &a);
+    return rc;
+}
+
+int op_step_advance(gh_backend* b, void* scalars, void* history) {
+    GhStepArgs a{(uint64_t)scalars, (uint64_t)history};
+    return launch(b, K_STEP_ADVANCE, 1, 1, 1, 64, &a);
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+extern "C" {
+
+int gh_create(const gh_config* cfg, gh_backend** out) {
+    if (!out) return GH_E_INVALID;
+    *out = nullptr;
+    int dev = cfg ? cfg->device : 0;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= dev || dev < 0) return GH_E_NO_DEVICE;
+    hipDeviceProp_t prop{};
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return GH_E_NO_DEVICE;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return GH_E_NO_DEVICE;
+    if (hipSetDevice(dev) != hipSuccess) return GH_E_NO_DEVICE;
+    auto* b = new gh_backend();
+    b->device = dev;
+    b->enc.b = b;
+    int rc = hip_check(b, hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking), "hipStreamCreate");
+    if (!rc) rc = hip_check(b, hipEventCreate(&b->ev_start), "hipEventCreate");
+    if (!rc) rc = hip_check(b, hipEventCreate(&b->ev_stop), "hipEventCreate");
+    std::string dir = cfg && cfg->code_object_path ? std::string(cfg->code_object_path) : library_dir();
+    for (const char* m : kModules) {
+        if (rc) break;
+        hipModule_t mod = nullptr;
+        std::string path = dir + "/" + m + "_gfx950.co";
+        if (hipModuleLoad(&mod, path.c_str()) != hipSuccess) {
+            rc = fail(b, GH_E_MODULE, "hipModuleLoad failed: " + path);
+            break;
+        }
+        b->modules.push_back(mod);
+    }
+    for (const KernelName& kn : kKernels) {
+        if (rc) break;
+        hipFunction_t f = nullptr;
+        for (hipModule_t mod : b->modules)
+            if (hipModuleGetFunction(&f, mod, kn.name) == hipSuccess) break;
+        if (!f) rc = fail(b, GH_E_MODULE, std::string("kernel not found: ") + kn.name);
+        b->fn[kn.id] = f;
+    }
+    if (!rc) rc = ensure_workspace(b, 0);
+    if (rc) {
+        gh_destroy(b);
+        return rc;
+    }
+    *out = b;
+    return GH_OK;
+}
+
+void gh_destroy(gh_backend* b) {
+    if (!b) return;
+    if (b->stream) (void)hipStreamSynchronize(b->stream);
+    if (b->ws) (void)hipFree(b->ws);
+    if (b->rope.table) (void)hipFree(b->rope.table);
+    if (b->rope.post) (void)hipFree(b->rope.post);
+    for (hipModule_t m : b->modules) (void)hipModuleUnload(m);
+    if (b->ev_start) (void)hipEventDestroy(b->ev_start);
+    if (b->ev_stop) (void)hipEventDestroy(b->ev_stop);
+    if (b->stream) (void)hipStreamDestroy(b->stream);
+    delete b;
+}
+
+const char* gh_last_error(const gh_backend* b) { return b ? b->err.c_str() : "no backend"; }
+
+int gh_alloc_buffer(gh_backend* b, uint64_t bytes, gh_buf* out) {
+    if (!b || !out || bytes == 0) return fail(b, GH_E_INVALID, "alloc: zero size");
+    void* p = nullptr;
+    int rc = hip_check(b, hipMalloc(&p, bytes), "hipMalloc");
+    if (rc) return rc;
+    *out = gh_buf{(uint64_t)p, bytes, GH_FMT_F16, GH_BUF_ALLOC, 0, 0};
+    return GH_OK;
+}
+
+int gh_free_buffer(gh_backend* b, gh_buf* buf) {
+    if (!b || !buf) return GH_E_INVALID;
+    if (buf->kind != GH_BUF_ALLOC && buf->kind != GH_BUF_WEIGHT)
+        return fail(b, GH_E_INVALID, "free_buffer: a view never owns its storage");
+    int rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (!rc) rc = hip_check(b, hipFree((void*)buf->addr), "hipFree");
+    *buf = gh_buf{};
+    return rc;
+}
+
+int gh_view(gh_backend* b, const gh_buf* buf, uint64_t off, uint64_t len, gh_buf* out) {
+    if (!b || !buf || !out) return GH_E_INVALID;
+    if (buf->kind == GH_BUF_WEIGHT) return fail(b, GH_E_INVALID, "view of a packed weight");
+    if (off > buf->bytes || len > buf->bytes - off) return fail(b, GH_E_RANGE, "view beyond buffer");
+    *out = gh_buf{buf->addr + off, len, buf->format, GH_BUF_VIEW, 0, 0};
+    return GH_OK;
+}
+
+uint64_t gh_min_buffer_offset_alignment(const gh_backend*) { return 4; }
+
+int gh_upload(gh_backend* b, const gh_buf* dst, uint64_t off, const void* src, uint64_t len) {
+    if (!b || !dst || (!src && len)) return GH_E_INVALID;
+    if (off > dst->bytes || len > dst->bytes - off) return fail(b, GH_E_RANGE, "upload beyond buffer");
+    if (len == 0) return GH_OK;
+    int rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    return hip_check(b, hipMemcpy((void*)(dst->addr + off), src, len, hipMemcpyHostToDevice), "hipMemcpy H2D");
+}
+
+int gh_download(gh_backend* b, const gh_buf* src, uint64_t off, void* dst, uint64_t len) {
+    if (!b || !src || (!dst && len)) return GH_E_INVALID;
+    if (off > src->bytes || len > src->bytes - off) return fail(b, GH_E_RANGE, "download beyond buffer");
+    if (len == 0) return GH_OK;
+    int rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    return hip_check(b, hipMemcpy(dst, (const void*)(src->addr + off), len, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+}
+
+int gh_load_weight(gh_backend* b, uint32_t format, const void* bytes, uint64_t len,
+                   uint32_t in_dim, uint32_t out_dim, gh_buf* out) {
+    if (!b || !bytes || !out || in_dim == 0 || out_dim == 0) return fail(b, GH_E_INVALID, "load_weight: bad argument");
+    *out = gh_buf{};
+    if (format == GH_FMT_F32 || format == GH_FMT_F16) {
+        const uint64_t n = (uint64_t)in_dim * out_dim;
+        if (len != n * (format == GH_FMT_F32 ? 4 : 2)) return fail(b, GH_E_INVALID, "load_weight: length mismatch");
+        std::vector<uint16_t> h(n);
+        if (format == GH_FMT_F32) {
+            // cpu/weights.rs:151-174: F32 norms are narrowed RNE to F16 at load
+            const float* f = (const float*)bytes;
+            for (uint64_t i = 0; i < n; ++i) h[i] = f32_to_f16_rne(f[i]);
+        } else {
+            std::memcpy(h.data(), bytes, len);
+        }
+        gh_buf buf;
+        int rc = gh_alloc_buffer(b, n * 2, &buf);
+        if (rc) return rc;
+        rc = gh_upload(b, &buf, 0, h.data(), n * 2);
+        if (rc) {
+            gh_free_buffer(b, &buf);
+            return rc;
+        }
+        buf.format = GH_FMT_F16;
+        buf.rows = out_dim;
+        buf.cols = in_dim;
+        *out = buf;
+        return GH_OK;
+    }
+    if (format != GH_FMT_Q4_K && format != GH_FMT_Q6_K)
+        return fail(b, GH_E_UNSUPPORTED, "load_weight: format outside the Q4_K_M profile");
+    if (in_dim % 256 != 0) return fail(b, GH_E_INVALID, "load_weight: in_dim not a multiple of 256");
+    const uint64_t bl = format == GH_FMT_Q4_K ? 144 : 210;
+    const uint64_t nb = in_dim / 256;
+    if (len % bl != 0 || len != (uint64_t)out_dim * nb * bl)
+        return fail(b, GH_E_INVALID, "load_weight: malformed quantized weight (not whole blocks of the shape)");
+    void* staging = nullptr;
+    void* dst = nullptr;
+    int rc = hip_check(b, hipMalloc(&staging, len), "hipMalloc(staging)");
+    if (!rc) rc = hip_check(b, hipMalloc(&dst, len), "hipMalloc(weight)");
+    if (!rc) rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (!rc) rc = hip_check(b, hipMemcpy(staging, bytes, len, hipMemcpyHostToDevice), "hipMemcpy(weight)");
+    if (!rc) {
+        GhRepackArgs a{(uint64_t)staging, (uint64_t)dst, out_dim, (uint32_t)nb};
+        uint64_t threads = format == GH_FMT_Q4_K ? (uint64_t)out_dim * nb * 9 : len;
+        rc = launch(b, format == GH_FMT_Q4_K ? K_REPACK_Q4K : K_REPACK_Q6K, ceil_div(threads, 256), 1, 1, 256, &a);
+    }
+    if (!rc) rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (staging) (void)hipFree(staging);
+    if (rc) {
+        if (dst) (void)hipFree(dst);
+        return rc;
+    }
+    *out = gh_buf{(uint64_t)dst, len, format, GH_BUF_WEIGHT, out_dim, in_dim};
+    return GH_OK;
+}
+
+int gh_dequant_rows(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* w,
+                    uint32_t row0, uint32_t rows) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (!is_weight(w)) return latch(enc, fail(b, GH_E_INVALID, "dequant: not a quantized weight"));
+    if ((uint64_t)row0 + rows > w->rows) return latch(enc, fail(b, GH_E_RANGE, "dequant: rows beyond weight"));
+    if (!fits(out, (uint64_t)rows * w->cols * 4)) return latch(enc, fail(b, GH_E_RANGE, "dequant: output too small"));
+    GhDequantArgs a{};
+    a.w = w->addr;
+    a.out = out->addr;
+    a.wrows = w->rows;
+    a.nb = w->cols / 256;
+    a.row0 = row0;
+    a.rows = rows;
+    return latch(enc, launch(b, w->format == GH_FMT_Q4_K ? K_DEQUANT_Q4K : K_DEQUANT_Q6K,
+                             ceil_div((uint64_t)rows * w->cols, 256), 1, 1, 256, &a));
+}
+
+int gh_begin(gh_backend* b, gh_encoder** enc) {
+    if (!b || !enc) return GH_E_INVALID;
+    if (b->enc_open) return fail(b, GH_E_STATE, "begin: encoder already open");
+    b->enc_open = true;
+    b->enc.latched = GH_OK;
+    *enc = &b->enc;
+    return GH_OK;
+}
+
+int gh_submit(gh_backend* b, gh_encoder* enc) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    b->enc_open = false;
+    rc = hip_check(b, hipStreamSynchronize(b->stream), "submit");
+    return enc->latched != GH_OK ? enc->latched : rc;
+}
+
+void gh_no_barrier(gh_backend*) {}
+
+int gh_kv_write(gh_backend* b, gh_encoder* enc, const gh_kv* kv, const gh_buf* k,
+                const gh_buf* v, uint64_t k_payload_offset, uint64_t v_payload_offset,
+                uint64_t, uint64_t, uint32_t vectors) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (!kv || !k || !v) return latch(enc, fail(b, GH_E_INVALID, "kv_write: null"));
+    if (kv->scheme != GH_KV_F16) return latch(enc, fail(b, GH_E_UNSUPPORTED, "kv_write: only the f16 scheme"));
+    const uint64_t kb = (uint64_t)vectors * kv->head_dim * 2, vb = (uint64_t)vectors * kv->value_dim * 2;
+    if (!fits(k, kb) || !fits(v, vb) || k_payload_offset % 2 || v_payload_offset % 2 ||
+        k_payload_offset + kb > kv->k.bytes || v_payload_offset + vb > kv->v.bytes)
+        return latch(enc, fail(b, GH_E_RANGE, "kv_write: beyond cache"));
+    return latch(enc, op_kv_write(b, kv, k, v, k_payload_offset / 2, v_payload_offset / 2, vectors, nullptr));
+}
+
+int gh_embed(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* w, uint32_t token,
+             uint32_t embd) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (!is_weight(w) || w->cols != embd) return latch(enc, fail(b, GH_E_UNSUPPORTED, "embed: token_embd must be a Q4_K/Q6_K weight of width embd"));
+    if (token >= w->rows) return latch(enc, fail(b, GH_E_RANGE, "embed: token beyond vocabulary"));
+    if (!fits(x, (uint64_t)embd * 4)) return latch(enc, fail(b, GH_E_RANGE, "embed: x too small"));
+    return latch(enc, op_embed(b, x, w, token, embd, nullptr));
+}
+
+static int gemv_launch(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w,
+                       uint32_t in_dim, uint32_t out_dim, uint32_t n, bool f32) {
+    if (!is_weight(w)) return fail(b, GH_E_UNSUPPORTED, "matmul: weight must be Q4_K or Q6_K");
+    if (w->cols != in_dim || w->rows != out_dim) return fail(b, GH_E_INVALID, "matmul: weight shape mismatch");
+    if (!fits(a, (uint64_t)n * in_dim * 2) || !fits(out, (uint64_t)n * out_dim * (f32 ? 4 : 2)))
+        return fail(b, GH_E_RANGE, "matmul: buffer too small");
+    GhGemvArgs g{};
+    g.w = w->addr;
+    g.x = a->addr;
+    g.y = out->addr;
+    g.in_dim = in_dim;
+    g.out_dim = out_dim;
+    g.n = n;
+    g.out_f32 = f32 ? 1 : 0;
+    // rows per wavefront: keep >= 2048 wavefronts in flight where the matrix allows it
+    const bool q4 = w->format == GH_FMT_Q4_K;
+    uint32_t r = out_dim >= 16384 ? 4 : (out_dim >= 8192 ? 2 : 1);
+    GhKernel k = q4 ? (r == 4 ? K_GEMV_Q4K_R4 : r == 2 ? K_GEMV_Q4K_R2 : K_GEMV_Q4K_R1)
+                    : (r == 4 ? K_GEMV_Q6K_R4 : r == 2 ? K_GEMV_Q6K_R2 : K_GEMV_Q6K_R1);
+    return launch(b, k, ceil_div(out_dim, 4 * r), 1, 1, 256, &g);
+}
+
+int gh_matmul(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* a,
+              const gh_buf* w, uint32_t in_dim, uint32_t out_dim) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    return latch(enc, gemv_launch(b, out, a, w, in_dim, out_dim, 1, false));
+}
+
+int gh_matmul_batched(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* a,
+                      const gh_buf* w, uint32_t in_dim, uint32_t out_dim, uint32_t n) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (n == 0) return latch(enc, fail(b, GH_E_INVALID, "matmul_batched: n == 0"));
+    return latch(enc, gemv_launch(b, out, a, w, in_dim, out_dim, n, false));
+}
+
+int gh_logits(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* x,
+              const gh_buf* w, uint32_t in_dim, uint32_t out_dim) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    return latch(enc, gemv_launch(b, out, x, w, in_dim, out_dim, 1, true));
+}
+
+int gh_rmsnorm_x(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* x,
+                 const gh_buf* w, uint32_t dim, float eps, uint32_t rows) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (dim == 0 || !fits(x, (uint64_t)rows * dim * 4) || !fits(out, (uint64_t)rows * dim * 2) || !fits(w, (uint64_t)dim * 2))
+        return latch(enc, fail(b, GH_E_RANGE, "rmsnorm_x: buffer too small"));
+    GhRmsnormArgs a{out->addr, x->addr, w->addr, dim, rows, eps, 0};
+    return latch(enc, launch(b, K_RMSNORM, rows, 1, 1, 256, &a));
+}
+
+int gh_rope_yarn(gh_backend* b, gh_encoder* enc, const gh_buf* x, uint32_t heads,
+                 uint32_t head_dim, uint32_t pos, const gh_yarn* yarn, uint32_t role) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (!yarn_valid(yarn) || role > 1 || yarn->rope_dim > head_dim)
+        return latch(enc, fail(b, GH_E_INVALID, "rope: invalid YaRN parameters"));
+    if (!fits(x, (uint64_t)heads * head_dim * 2)) return latch(enc, fail(b, GH_E_RANGE, "rope: buffer too small"));
+    rc = ensure_rope(b, yarn, pos + 1);
+    if (rc) return latch(enc, rc);
+    return latch(enc, op_rope(b, x, heads, head_dim, pos, 1, role, nullptr));
+}
+
+int gh_rope_yarn_batched(gh_backend* b, gh_encoder* enc, const gh_buf* q, const gh_buf* k,
+                         uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t base,
+                         uint32_t rows, const gh_yarn* yarn) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (rows == 0) return latch(enc, fail(b, GH_E_INVALID, "rope: empty batch"));
+    if (!yarn_valid(yarn) || yarn->rope_dim > head_dim) return latch(enc, fail(b, GH_E_INVALID, "rope: invalid YaRN parameters"));
+    if ((uint64_t)base + rows > 0xFFFFFFFFull) return latch(enc, fail(b, GH_E_RANGE, "rope: position overflow"));
+    if (!fits(q, (uint64_t)rows * q_heads * head_dim * 2) || !fits(k, (uint64_t)rows * kv_heads * head_dim * 2))
+        return latch(enc, fail(b, GH_E_RANGE, "rope: buffer too small"));
+    rc = ensure_rope(b, yarn, base + rows);
+    if (!rc) rc = op_rope(b, q, q_heads, head_dim, base, rows, GH_ROPE_QUERY, nullptr);
+    if (!rc) rc = op_rope(b, k, kv_heads, head_dim, base, rows, GH_ROPE_KEY, nullptr);
+    return latch(enc, rc);
+}
+
+int gh_silu_mul(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* gate,
+                const gh_buf* up, uint32_t n) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (!fits(out, (uint64_t)n * 2) || !fits(gate, (uint64_t)n * 2) || !fits(up, (uint64_t)n * 2))
+        return latch(enc, fail(b, GH_E_RANGE, "silu_mul: buffer too small"));
+    GhEltArgs a{out->addr, gate->addr, up->addr, n, 0};
+    return latch(enc, launch(b, K_SILU_MUL, ceil_div(n, 256), 1, 1, 256, &a));
+}
+
+int gh_residual_add(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* y,
+                    uint32_t n) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (!fits(x, (uint64_t)n * 4) || !fits(y, (uint64_t)n * 2))
+        return latch(enc, fail(b, GH_E_RANGE, "residual_add: buffer too small"));
+    GhEltArgs a{x->addr, 0, y->addr, n, 0};
+    return latch(enc, launch(b, K_RESIDUAL_ADD, ceil_div(n, 256), 1, 1, 256, &a));
+}
+
+static int check_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
+                           uint32_t q_heads, uint32_t last_pos, uint32_t rows, uint32_t layer) {
+    if (!kv || kv->scheme != GH_KV_F16) return fail(b, GH_E_UNSUPPORTED, "attention: only the f16 KV scheme");
+    if (kv->head_dim != 128 || kv->value_dim != 128) return fail(b, GH_E_UNSUPPORTED, "attention: head_dim 128 only");
+    if (kv->kv_heads == 0 || q_heads % kv->kv_heads) return fail(b, GH_E_INVALID, "attention: q_heads not a multiple of kv_heads");
+    if (layer >= kv->block_count || last_pos >= kv->context) return fail(b, GH_E_RANGE, "attention: position beyond context");
+    const uint64_t cache = (uint64_t)kv->block_count * kv->context * kv->kv_heads * 128 * 2;
+    if (!fits(&kv->k, cache) || !fits(&kv->v, cache)) return fail(b, GH_E_RANGE, "attention: cache too small");
+    if (!fits(q, (uint64_t)rows * q_heads * 256) || !fits(out, (uint64_t)rows * q_heads * 256))
+        return fail(b, GH_E_RANGE, "attention: buffer too small");
+    return GH_OK;
+}
+
+int gh_attention_decode(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* q,
+                        const gh_kv* kv, uint32_t q_heads, uint32_t pos, uint32_t layer) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    rc = check_attention(b, out, q, kv, q_heads, pos, 1, layer);
+    if (!rc) rc = op_attention(b, out, q, kv, q_heads, pos, 1, layer, nullptr, pos);
+    return latch(enc, rc);
+}
+
+int gh_attention_prefill(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* q,
+                         const gh_kv* kv, uint32_t q_heads, uint32_t base, uint32_t n,
+                         uint32_t layer) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (n == 0) return latch(enc, fail(b, GH_E_INVALID, "attention_prefill: n == 0"));
+    rc = check_attention(b, out, q, kv, q_heads, base + n - 1, n, layer);
+    if (!rc) rc = op_attention(b, out, q, kv, q_heads, base, n, layer, nullptr, base + n - 1);
+    return latch(enc, rc);
+}
+
+int gh_read_logits(gh_backend* b, const gh_buf* logits, uint64_t vocab, float* dst) {
+    if (!b || !logits) return GH_E_INVALID;
+    if (!fits(logits, vocab * 4)) return fail(b, GH_E_RANGE, "read_logits: buffer smaller than vocab");
+    return gh_download(b, logits, 0, dst, vocab * 4);
+}
+
+int gh_read_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, uint32_t* out) {
+    if (!b || !logits || !out) return GH_E_INVALID;
+    if (vocab == 0) return fail(b, GH_E_INVALID, "read_argmax on empty logits");
+    if (!fits(logits, vocab * 4)) return fail(b, GH_E_RANGE, "read_argmax: buffer smaller than vocab");
+    int rc = op_argmax(b, logits, vocab, nullptr, nullptr);
+    if (rc) return rc;
+    rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    return hip_check(b, hipMemcpy(out, (char*)b->ws + 2048, 4, hipMemcpyDeviceToHost), "hipMemcpy argmax");
+}
+
+int gh_read_topk(gh_backend* b, const gh_buf* logits, uint64_t vocab, uint64_t k, uint32_t* idx,
+                 float* val, uint64_t* count) {
+    if (!b || !logits || !count) return GH_E_INVALID;
+    if (vocab == 0) return fail(b, GH_E_INVALID, "read_topk on empty logits");
+    std::vector<float> l(vocab);
+    int rc = gh_read_logits(b, logits, vocab, l.data());
+    if (rc) return rc;
+    k = std::min<uint64_t>(k, vocab);
+    std::vector<uint32_t> cand(vocab);
+    for (uint64_t i = 0; i < vocab; ++i) cand[i] = (uint32_t)i;
+    auto order = [&](uint32_t x, uint32_t y) {
+        int kx = total_key(l[x]), ky = total_key(l[y]);
+        return kx != ky ? kx > ky : x < y;
+    };
+    std::partial_sort(cand.begin(), cand.begin() + (ptrdiff_t)k, cand.end(), order);
+    for (uint64_t i = 0; i < k; ++i) {
+        if (idx) idx[i] = cand[i];
+        if (val) val[i] = l[cand[i]];
+    }
+    *count = k;
+    return GH_OK;
+}
+
+int gh_timer_start(gh_backend* b) {
+    if (!b) return GH_E_INVALID;
+    return hip_check(b, hipEventRecord(b->ev_start, b->stream), "hipEventRecord");
+}
+
+int gh_timer_stop(gh_backend* b, float* ms) {
+    if (!b || !ms) return GH_E_INVALID;
+    int rc = hip_check(b, hipEventRecord(b->ev_stop, b->stream), "hipEventRecord");
+    if (!rc) rc = hip_check(b, hipEventSynchronize(b->ev_stop), "hipEventSynchronize");
+    if (!rc) rc = hip_check(b, hipEventElapsedTime(ms, b->ev_start, b->ev_stop), "hipEventElapsedTime");
+    return rc;
+}
+
+int gh_synchronize(gh_backend* b) {
+    if (!b) return GH_E_INVALID;
+    return hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+}
+
+}  // extern "C"

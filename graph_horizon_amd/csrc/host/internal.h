@@ -1,0 +1,95 @@
+// Host-side internals of the gfx950 backend (C++17, HIP runtime API, no device code).
+#ifndef GH_HOST_INTERNAL_H
+#define GH_HOST_INTERNAL_H
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../../include/gh_backend.h"
+#include "../kernels/gh_kargs.h"
+
+enum GhKernel : int {
+    K_REPACK_Q4K,
+    K_REPACK_Q6K,
+    K_DEQUANT_Q4K,
+    K_DEQUANT_Q6K,
+    K_GEMV_Q4K_R1,
+    K_GEMV_Q4K_R2,
+    K_GEMV_Q4K_R4,
+    K_GEMV_Q6K_R1,
+    K_GEMV_Q6K_R2,
+    K_GEMV_Q6K_R4,
+    K_RMSNORM,
+    K_ROPE,
+    K_SILU_MUL,
+    K_RESIDUAL_ADD,
+    K_KV_WRITE,
+    K_ARGMAX_PARTIAL,
+    K_ARGMAX_FINAL,
+    K_ATTN_SPLIT_G1,
+    K_ATTN_SPLIT_G2,
+    K_ATTN_SPLIT_G4,
+    K_ATTN_SPLIT_G8,
+    K_ATTN_MERGE,
+    K_STEP_ADVANCE,
+    K_COUNT
+};
+
+// Device-resident YaRN rotation table: (cos, sin) per (position, pair) and the query
+// post-scale per position, computed on the host with Yarn::pair's formula.
+struct GhRopeTable {
+    gh_yarn yarn{};
+    uint32_t positions = 0;
+    void* table = nullptr;  // float2 [positions][pairs]
+    void* post = nullptr;   // float [positions]
+};
+
+struct gh_encoder {
+    gh_backend* b = nullptr;
+    int latched = GH_OK;
+};
+
+struct gh_backend {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<hipModule_t> modules;
+    hipFunction_t fn[K_COUNT] = {};
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    gh_encoder enc;
+    bool enc_open = false;
+    bool capturing = false;  // a graph capture is recording on `stream`
+    std::string err;
+    // growable device workspace (attention partials, argmax partials)
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    GhRopeTable rope;
+    uint64_t gen = 0;  // bumped whenever the workspace or rope table moves (captured graphs hold them)
+};
+
+namespace gh {
+int fail(gh_backend* b, int code, const std::string& msg);
+int hip_check(gh_backend* b, hipError_t e, const char* what);
+int launch(gh_backend* b, GhKernel k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
+           const void* args);
+int ensure_workspace(gh_backend* b, size_t bytes);
+int ensure_rope(gh_backend* b, const gh_yarn* y, uint32_t positions);
+bool yarn_valid(const gh_yarn* y);
+// Graph-capturable op variants used by the model driver: positions/tokens read from device.
+int op_rope(gh_backend* b, const gh_buf* x, uint32_t heads, uint32_t head_dim, uint32_t base,
+            uint32_t rows, uint32_t role, const void* pos_ptr);
+int op_kv_write(gh_backend* b, const gh_kv* kv, const gh_buf* k, const gh_buf* v,
+                uint64_t k_elem_off, uint64_t v_elem_off, uint32_t vectors, const void* pos_ptr);
+int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
+                 uint32_t q_heads, uint32_t base, uint32_t rows, uint32_t layer,
+                 const void* pos_ptr, uint32_t max_pos);
+int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, uint32_t embd,
+             const void* token_ptr);
+int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2);
+int op_step_advance(gh_backend* b, void* scalars, void* history);
+size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
+uint32_t attention_split_len(uint32_t max_len);
+}  // namespace gh
+
+#endif

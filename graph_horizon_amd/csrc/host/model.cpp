@@ -1,0 +1,383 @@
+// Graph driver: MistralGraph's op order recorded through the backend ops.
+//   decode  — forward::token (family/mistral/graph/forward.rs:68-83), block::record
+//             (block.rs:17-107), mlp::record (mlp.rs:12-61), tail::record (tail.rs:11-59);
+//   prefill — prefill::prefill / record_batch (graph/prefill/encode.rs:16-106) and
+//             prefill::layer::record (prefill/layer.rs:18-122).
+// The greedy loop replays one captured HIP graph per token: the token id and position live in
+// device memory, the step ends with an on-device argmax that becomes the next step's input.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <array>
+#include <cstring>
+#include <vector>
+
+#include "internal.h"
+
+using namespace gh;
+
+namespace {
+constexpr uint32_t kNoLayer = 0xFFFFFFFFu;
+
+struct Scratch {  // backend/buffers.rs:17-29, sized for `rows` token rows
+    gh_buf x, normed, q, k, v, attn, proj, gate, up, act, ffn_out;
+};
+}  // namespace
+
+struct gh_model {
+    gh_backend* b = nullptr;
+    gh_model_config cfg{};
+    std::vector<std::array<gh_buf, 9>> layers;
+    gh_buf token_embd{}, output_norm{}, output{};
+    Scratch dec{}, pre{};
+    gh_buf logits{};
+    gh_buf scalars{};  // u32[4]: position, token, argmax, spare
+    gh_buf history{};  // u32[kv_context]
+    gh_kv kv{};
+    std::vector<gh_buf> owned;
+    hipGraphExec_t step = nullptr;
+    hipGraph_t step_graph = nullptr;
+    uint64_t step_gen = 0;  // backend generation the step graph was captured against
+    uint32_t last_rows = 0;  // rows of the most recent pass (for read_x)
+    bool last_prefill = false;
+};
+
+namespace {
+
+int alloc(gh_model* m, uint64_t bytes, gh_buf* out) {
+    int rc = gh_alloc_buffer(m->b, std::max<uint64_t>(bytes, 256), out);
+    if (!rc) m->owned.push_back(*out);
+    return rc;
+}
+
+int alloc_scratch(gh_model* m, uint32_t rows, Scratch* s) {
+    const gh_model_config& c = m->cfg;
+    const uint64_t d = c.embedding_length, ffn = c.feed_forward_length;
+    const uint64_t qw = (uint64_t)c.head_count * c.key_length, kw = (uint64_t)c.kv_head_count * c.key_length;
+    const uint64_t vw = (uint64_t)c.kv_head_count * c.value_length, aw = (uint64_t)c.head_count * c.value_length;
+    int rc = alloc(m, rows * d * 4, &s->x);
+    if (!rc) rc = alloc(m, rows * d * 2, &s->normed);
+    if (!rc) rc = alloc(m, rows * qw * 2, &s->q);
+    if (!rc) rc = alloc(m, rows * kw * 2, &s->k);
+    if (!rc) rc = alloc(m, rows * vw * 2, &s->v);
+    if (!rc) rc = alloc(m, rows * aw * 2, &s->attn);
+    if (!rc) rc = alloc(m, rows * d * 2, &s->proj);
+    if (!rc) rc = alloc(m, rows * ffn * 2, &s->gate);
+    if (!rc) rc = alloc(m, rows * ffn * 2, &s->up);
+    if (!rc) rc = alloc(m, rows * ffn * 2, &s->act);
+    if (!rc) rc = alloc(m, rows * d * 2, &s->ffn_out);
+    return rc;
+}
+
+// One transformer layer over `rows` packed rows at absolute positions base + r
+// (+ *pos_ptr when the position lives on the device).
+int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t base,
+          uint32_t rows, const void* pos_ptr) {
+    gh_backend* b = m->b;
+    const gh_model_config& c = m->cfg;
+    const auto& w = m->layers[li];
+    const uint32_t d = c.embedding_length, ffn = c.feed_forward_length;
+    const uint32_t qw = c.head_count * c.key_length, kw = c.kv_head_count * c.key_length;
+    const uint32_t vw = c.kv_head_count * c.value_length, aw = c.head_count * c.value_length;
+    int rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_ATTN_NORM], d, c.rms_epsilon, rows);
+    gh_no_barrier(b);
+    if (!rc) rc = gh_matmul_batched(b, enc, &s.q, &s.normed, &w[GH_T_ATTN_Q], d, qw, rows);
+    gh_no_barrier(b);
+    if (!rc) rc = gh_matmul_batched(b, enc, &s.k, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);
+    if (!rc) rc = gh_matmul_batched(b, enc, &s.v, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
+    // rope_yarn (block.rs:147-166) / rope_yarn_batched (prefill/layer.rs:79-89)
+    if (!rc) rc = op_rope(b, &s.q, c.head_count, c.key_length, base, rows, GH_ROPE_QUERY, pos_ptr);
+    if (!rc) rc = op_rope(b, &s.k, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, pos_ptr);
+    // kv_cache::append_batch (kv_cache/mod.rs:133-177): payload offsets of (layer, base)
+    const uint64_t per_pos_k = (uint64_t)c.kv_head_count * c.key_length;
+    const uint64_t per_pos_v = (uint64_t)c.kv_head_count * c.value_length;
+    const uint64_t koff = ((uint64_t)li * m->kv.context + base) * per_pos_k;
+    const uint64_t voff = ((uint64_t)li * m->kv.context + base) * per_pos_v;
+    if (!rc) rc = op_kv_write(b, &m->kv, &s.k, &s.v, koff, voff, rows * c.kv_head_count, pos_ptr);
+    const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base + rows - 1;
+    if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, rows, li, pos_ptr, max_pos);
+    if (!rc) rc = gh_matmul_batched(b, enc, &s.proj, &s.attn, &w[GH_T_ATTN_OUTPUT], aw, d, rows);
+    if (!rc) rc = gh_residual_add(b, enc, &s.x, &s.proj, d * rows);
+    // mlp::record
+    if (!rc) rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_FFN_NORM], d, c.rms_epsilon, rows);
+    gh_no_barrier(b);
+    if (!rc) rc = gh_matmul_batched(b, enc, &s.gate, &s.normed, &w[GH_T_FFN_GATE], d, ffn, rows);
+    if (!rc) rc = gh_matmul_batched(b, enc, &s.up, &s.normed, &w[GH_T_FFN_UP], d, ffn, rows);
+    if (!rc) rc = gh_silu_mul(b, enc, &s.act, &s.gate, &s.up, ffn * rows);
+    if (!rc) rc = gh_matmul_batched(b, enc, &s.ffn_out, &s.act, &w[GH_T_FFN_DOWN], ffn, d, rows);
+    if (!rc) rc = gh_residual_add(b, enc, &s.x, &s.ffn_out, d * rows);
+    (void)vw;
+    return rc;
+}
+
+// tail::record_buffers (tail.rs:22-59): output_norm then FP32 logits (dedicated or tied).
+int tail(gh_model* m, gh_encoder* enc, const gh_buf* xrow, const gh_buf* normed_row) {
+    const gh_model_config& c = m->cfg;
+    int rc = gh_rmsnorm_x(m->b, enc, normed_row, xrow, &m->output_norm, c.embedding_length, c.rms_epsilon, 1);
+    const gh_buf* out = m->output.addr ? &m->output : &m->token_embd;
+    if (!rc) rc = gh_logits(m->b, enc, &m->logits, normed_row, out, c.embedding_length, c.vocab_size);
+    return rc;
+}
+
+bool weights_ready(const gh_model* m) {
+    if (!m->token_embd.addr || !m->output_norm.addr) return false;
+    for (const auto& l : m->layers)
+        for (const gh_buf& w : l)
+            if (!w.addr) return false;
+    return true;
+}
+
+// Record one decode step reading token and position from m->scalars (graph-capturable).
+int record_step(gh_model* m, gh_encoder* enc) {
+    const gh_model_config& c = m->cfg;
+    const void* pos_ptr = (const void*)m->scalars.addr;
+    const void* tok_ptr = (const void*)(m->scalars.addr + 4);
+    int rc = op_embed(m->b, &m->dec.x, &m->token_embd, 0, c.embedding_length, tok_ptr);
+    for (uint32_t li = 0; li < c.block_count && !rc; ++li) rc = layer(m, enc, m->dec, li, 0, 1, pos_ptr);
+    if (!rc) rc = tail(m, enc, &m->dec.x, &m->dec.normed);
+    if (!rc) rc = op_argmax(m->b, &m->logits, c.vocab_size, (void*)(m->scalars.addr + 8), nullptr);
+    if (!rc) rc = op_step_advance(m->b, (void*)m->scalars.addr, (void*)m->history.addr);
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gh_model_create(gh_backend* b, const gh_model_config* cfg, gh_model** out) {
+    if (!b || !cfg || !out) return GH_E_INVALID;
+    *out = nullptr;
+    const gh_model_config& c = *cfg;
+    if (c.block_count == 0 || c.embedding_length % 256 || c.feed_forward_length % 256 ||
+        c.head_count == 0 || c.kv_head_count == 0 || c.head_count % c.kv_head_count ||
+        c.key_length != 128 || c.value_length != 128 || c.vocab_size == 0 || c.kv_context == 0 ||
+        c.prefill_rows == 0 || (c.head_count * c.value_length) % 256 || !yarn_valid(&c.yarn) ||
+        c.yarn.rope_dim > c.key_length)
+        return fail(b, GH_E_INVALID, "model: unsupported shape");
+    auto* m = new gh_model();
+    m->b = b;
+    m->cfg = c;
+    m->layers.assign(c.block_count, std::array<gh_buf, 9>{});
+    m->kv.scheme = GH_KV_F16;
+    m->kv.block_count = c.block_count;
+    m->kv.context = c.kv_context;
+    m->kv.kv_heads = c.kv_head_count;
+    m->kv.head_dim = c.key_length;
+    m->kv.value_dim = c.value_length;
+    // kv_cache::alloc_shape (kv_cache/mod.rs:70-114); layout::buffer_bytes (f16)
+    const uint64_t kv_bytes = (uint64_t)c.block_count * c.kv_context * c.kv_head_count * c.key_length * 2;
+    int rc = alloc(m, kv_bytes, &m->kv.k);
+    if (!rc) rc = alloc(m, kv_bytes, &m->kv.v);
+    if (!rc) rc = alloc_scratch(m, 1, &m->dec);
+    if (!rc) rc = alloc_scratch(m, c.prefill_rows, &m->pre);
+    if (!rc) rc = alloc(m, (uint64_t)c.vocab_size * 4, &m->logits);
+    if (!rc) rc = alloc(m, 16, &m->scalars);
+    if (!rc) rc = alloc(m, (uint64_t)c.kv_context * 4, &m->history);
+    if (!rc) rc = ensure_rope(b, &c.yarn, c.kv_context);
+    // partials for a decode step and for one prefill chunk
+    const uint32_t dsl = attention_split_len(c.kv_context);
+    const uint32_t dsplits = (c.kv_context + dsl - 1) / dsl;
+    if (!rc) rc = ensure_workspace(b, attention_workspace(1, c.head_count, dsplits));
+    if (rc) {
+        gh_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return GH_OK;
+}
+
+void gh_model_destroy(gh_model* m) {
+    if (!m) return;
+    if (m->step) (void)hipGraphExecDestroy(m->step);
+    if (m->step_graph) (void)hipGraphDestroy(m->step_graph);
+    for (gh_buf& buf : m->owned) gh_free_buffer(m->b, &buf);
+    for (auto& l : m->layers)
+        for (gh_buf& w : l)
+            if (w.addr) gh_free_buffer(m->b, &w);
+    for (gh_buf* w : {&m->token_embd, &m->output_norm, &m->output})
+        if (w->addr) gh_free_buffer(m->b, w);
+    delete m;
+}
+
+int gh_model_load_tensor(gh_model* m, uint32_t layer_index, uint32_t tensor, uint32_t format,
+                         const void* bytes, uint64_t len) {
+    if (!m) return GH_E_INVALID;
+    const gh_model_config& c = m->cfg;
+    uint32_t in = 0, out = 0;
+    gh_buf* slot = nullptr;
+    const bool norm = tensor == GH_T_ATTN_NORM || tensor == GH_T_FFN_NORM || tensor == GH_T_OUTPUT_NORM;
+    if (layer_index == kNoLayer) {
+        switch (tensor) {
+            case GH_T_TOKEN_EMBD: in = c.embedding_length; out = c.vocab_size; slot = &m->token_embd; break;
+            case GH_T_OUTPUT_NORM: in = c.embedding_length; out = 1; slot = &m->output_norm; break;
+            case GH_T_OUTPUT: in = c.embedding_length; out = c.vocab_size; slot = &m->output; break;
+            default: return fail(m->b, GH_E_INVALID, "model: unknown global tensor");
+        }
+    } else {
+        if (layer_index >= c.block_count || tensor > GH_T_FFN_DOWN) return fail(m->b, GH_E_INVALID, "model: unknown layer tensor");
+        const uint32_t d = c.embedding_length;
+        switch (tensor) {
+            case GH_T_ATTN_NORM: case GH_T_FFN_NORM: in = d; out = 1; break;
+            case GH_T_ATTN_Q: in = d; out = c.head_count * c.key_length; break;
+            case GH_T_ATTN_K: in = d; out = c.kv_head_count * c.key_length; break;
+            case GH_T_ATTN_V: in = d; out = c.kv_head_count * c.value_length; break;
+            case GH_T_ATTN_OUTPUT: in = c.head_count * c.value_length; out = d; break;
+            case GH_T_FFN_GATE: case GH_T_FFN_UP: in = d; out = c.feed_forward_length; break;
+            case GH_T_FFN_DOWN: in = c.feed_forward_length; out = d; break;
+        }
+        slot = &m->layers[layer_index][tensor];
+    }
+    if (norm != (format == GH_FMT_F32 || format == GH_FMT_F16))
+        return fail(m->b, GH_E_UNSUPPORTED, "model: norms are F32/F16, matrices Q4_K/Q6_K");
+    if (slot->addr) gh_free_buffer(m->b, slot);
+    if (m->step) {
+        (void)hipGraphExecDestroy(m->step);
+        (void)hipGraphDestroy(m->step_graph);
+        m->step = nullptr;
+        m->step_graph = nullptr;
+    }
+    return gh_load_weight(m->b, format, bytes, len, in, out, slot);
+}
+
+int gh_model_token(gh_model* m, uint32_t token, uint32_t pos) {
+    if (!m) return GH_E_INVALID;
+    const gh_model_config& c = m->cfg;
+    if (!weights_ready(m)) return fail(m->b, GH_E_STATE, "model: weights not loaded");
+    if (pos >= c.context_length || pos >= m->kv.context) return fail(m->b, GH_E_RANGE, "model: position beyond context");
+    if (token >= c.vocab_size) return fail(m->b, GH_E_RANGE, "model: token beyond vocabulary");
+    gh_encoder* enc = nullptr;
+    int rc = gh_begin(m->b, &enc);
+    if (rc) return rc;
+    rc = gh_embed(m->b, enc, &m->dec.x, &m->token_embd, token, c.embedding_length);
+    for (uint32_t li = 0; li < c.block_count && !rc; ++li) rc = layer(m, enc, m->dec, li, pos, 1, nullptr);
+    if (!rc) rc = tail(m, enc, &m->dec.x, &m->dec.normed);
+    int rs = gh_submit(m->b, enc);
+    m->last_rows = 1;
+    m->last_prefill = false;
+    return rc ? rc : rs;
+}
+
+int gh_model_prefill(gh_model* m, const uint32_t* tokens, uint32_t n, uint32_t base) {
+    if (!m || !tokens) return GH_E_INVALID;
+    const gh_model_config& c = m->cfg;
+    if (n == 0) return fail(m->b, GH_E_INVALID, "model: empty prompt");
+    if (!weights_ready(m)) return fail(m->b, GH_E_STATE, "model: weights not loaded");
+    if ((uint64_t)base + n > m->kv.context || (uint64_t)base + n > c.context_length)
+        return fail(m->b, GH_E_RANGE, "model: prompt beyond context");
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] >= c.vocab_size) return fail(m->b, GH_E_RANGE, "model: token beyond vocabulary");
+    const uint32_t cap = c.prefill_rows;
+    const uint64_t d = c.embedding_length;
+    for (uint32_t off = 0; off < n; off += cap) {
+        const uint32_t rows = std::min(cap, n - off);
+        gh_encoder* enc = nullptr;
+        int rc = gh_begin(m->b, &enc);
+        if (rc) return rc;
+        for (uint32_t r = 0; r < rows && !rc; ++r) {
+            gh_buf xr;
+            rc = gh_view(m->b, &m->pre.x, r * d * 4, d * 4, &xr);
+            if (!rc) rc = gh_embed(m->b, enc, &xr, &m->token_embd, tokens[off + r], c.embedding_length);
+        }
+        for (uint32_t li = 0; li < c.block_count && !rc; ++li)
+            rc = layer(m, enc, m->pre, li, base + off, rows, nullptr);
+        if (!rc && off + rows == n) {  // the tail belongs to the last chunk's last row
+            gh_buf xr, nr;
+            rc = gh_view(m->b, &m->pre.x, (rows - 1) * d * 4, d * 4, &xr);
+            if (!rc) rc = gh_view(m->b, &m->pre.normed, (rows - 1) * d * 2, d * 2, &nr);
+            if (!rc) rc = tail(m, enc, &xr, &nr);
+        }
+        int rs = gh_submit(m->b, enc);
+        if (rc || rs) return rc ? rc : rs;
+        m->last_rows = rows;
+        m->last_prefill = true;
+    }
+    return GH_OK;
+}
+
+int gh_model_read_logits(gh_model* m, float* dst) {
+    if (!m || !dst) return GH_E_INVALID;
+    return gh_read_logits(m->b, &m->logits, m->cfg.vocab_size, dst);
+}
+
+int gh_model_read_argmax(gh_model* m, uint32_t* out) {
+    if (!m || !out) return GH_E_INVALID;
+    return gh_read_argmax(m->b, &m->logits, m->cfg.vocab_size, out);
+}
+
+int gh_model_decode_greedy(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps,
+                           uint32_t* tokens_out) {
+    if (!m || (steps && !tokens_out)) return GH_E_INVALID;
+    const gh_model_config& c = m->cfg;
+    if (!weights_ready(m)) return fail(m->b, GH_E_STATE, "model: weights not loaded");
+    if (token >= c.vocab_size) return fail(m->b, GH_E_RANGE, "model: token beyond vocabulary");
+    if ((uint64_t)pos + steps > m->kv.context || (uint64_t)pos + steps > c.context_length)
+        return fail(m->b, GH_E_RANGE, "model: decode beyond context");
+    if (steps == 0) return GH_OK;
+    gh_backend* b = m->b;
+    int rc = GH_OK;
+    if (m->step && m->step_gen != b->gen) {  // workspace or rope table moved: capture again
+        (void)hipGraphExecDestroy(m->step);
+        (void)hipGraphDestroy(m->step_graph);
+        m->step = nullptr;
+        m->step_graph = nullptr;
+    }
+    if (!m->step) {
+        gh_encoder* enc = nullptr;
+        rc = gh_begin(b, &enc);
+        if (rc) return rc;
+        rc = hip_check(b, hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        if (!rc) {
+            b->capturing = true;
+            int rec = record_step(m, enc);
+            b->capturing = false;
+            hipGraph_t g = nullptr;
+            int end = hip_check(b, hipStreamEndCapture(b->stream, &g), "hipStreamEndCapture");
+            rc = rec ? rec : end;
+            if (!rc) rc = hip_check(b, hipGraphInstantiate(&m->step, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+            if (rc && g) (void)hipGraphDestroy(g);
+            else m->step_graph = g;
+            m->step_gen = b->gen;
+        }
+        b->enc_open = false;
+        if (rc) return rc;
+    }
+    const uint32_t init[4] = {pos, token, 0, 0};
+    rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
+    for (uint32_t i = 0; i < steps && !rc; ++i)
+        rc = hip_check(b, hipGraphLaunch(m->step, b->stream), "hipGraphLaunch");
+    if (!rc) rc = gh_download(b, &m->history, (uint64_t)pos * 4, tokens_out, (uint64_t)steps * 4);
+    m->last_rows = 1;
+    m->last_prefill = false;
+    return rc;
+}
+
+int gh_model_kv(gh_model* m, gh_kv* out) {
+    if (!m || !out) return GH_E_INVALID;
+    *out = m->kv;
+    return GH_OK;
+}
+
+int gh_model_read_x(gh_model* m, float* dst) {
+    if (!m || !dst) return GH_E_INVALID;
+    const uint64_t d = m->cfg.embedding_length;
+    const gh_buf& x = m->last_prefill ? m->pre.x : m->dec.x;
+    const uint64_t off = m->last_prefill ? (uint64_t)(m->last_rows - 1) * d * 4 : 0;
+    return gh_download(m->b, &x, off, dst, d * 4);
+}
+
+int gh_model_weight(gh_model* m, uint32_t layer_index, uint32_t tensor, gh_buf* out) {
+    if (!m || !out) return GH_E_INVALID;
+    const gh_buf* w = nullptr;
+    if (layer_index == kNoLayer) {
+        if (tensor == GH_T_TOKEN_EMBD) w = &m->token_embd;
+        else if (tensor == GH_T_OUTPUT_NORM) w = &m->output_norm;
+        else if (tensor == GH_T_OUTPUT) w = &m->output;
+    } else if (layer_index < m->cfg.block_count && tensor <= GH_T_FFN_DOWN) {
+        w = &m->layers[layer_index][tensor];
+    }
+    if (!w || !w->addr) return fail(m->b, GH_E_INVALID, "model: no such tensor loaded");
+    *out = *w;
+    return GH_OK;
+}
+
+}  // extern "C"

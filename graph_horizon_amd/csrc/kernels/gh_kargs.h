@@ -1,0 +1,143 @@
+// Kernel argument blocks shared by the host library (g++) and the gfx950 kernels (hipcc).
+// Every kernel takes exactly one of these structs by value; the host packs the same struct
+// and hands hipModuleLaunchKernel a pointer to it. Plain C layout: u64 device addresses,
+// u32 sizes, f32 scalars, so both compilers agree on offsets.
+#ifndef GH_KARGS_H
+#define GH_KARGS_H
+#include <stdint.h>
+
+// Device layout of a Q4_K weight [rows][nb = cols/256 blocks] (lossless 16-byte permutation of
+// the GGUF bytes, same 144 B per block):
+//   QS plane at 0          : chunk (row, h, u) at row*128*nb + h*64*nb + 16*u, where unit
+//                            u = 4*b + g and the chunk holds qs bytes [32g+16h, 32g+16h+16) of
+//                            block b (g in 0..3 is the 32-byte qs group, h in 0..1 its half).
+//   HDR plane at rows*128*nb: 16 bytes per (row, b) = d, dmin, scales[12] of block b verbatim.
+// Device layout of a Q6_K weight [rows][nb] (same 210 B per block):
+//   QL/QH plane at 0       : chunk (row, p, u) at row*192*nb + p*64*nb + 16*u, u = 4*b + 2*s + h,
+//                            p = 0: ql[64s + 16h, +16), p = 1: ql[64s + 32 + 16h, +16),
+//                            p = 2: qh[32s + 16h, +16)  (s = 128-value segment, h = half).
+//   SC plane at rows*192*nb: 16 bytes per (row, b) = the int8 scales[16] verbatim.
+//   D plane at rows*208*nb : 2 bytes per (row, b) = d (f16).
+#define GH_Q4K_QS_BYTES 128u
+#define GH_Q6K_QLH_BYTES 192u
+
+struct GhRepackArgs {
+    uint64_t src;   // GGUF block bytes
+    uint64_t dst;   // device layout
+    uint32_t rows;
+    uint32_t nb;    // blocks per row
+};
+
+struct GhDequantArgs {
+    uint64_t w;     // device layout base
+    uint64_t out;   // f32 [rows][nb*256]
+    uint64_t row_ptr;  // optional u32* on the device: first row (embedding token id); 0 = use row0
+    uint32_t wrows; // total rows of the matrix (plane offsets)
+    uint32_t nb;
+    uint32_t row0;
+    uint32_t rows;
+};
+
+struct GhGemvArgs {
+    uint64_t w;       // device layout base
+    uint64_t x;       // f16 activations, token-major [n][in_dim]
+    uint64_t y;       // output, token-major [n][out_dim]: f16 or f32
+    uint32_t in_dim;
+    uint32_t out_dim;
+    uint32_t n;       // tokens (1 = decode GEMV)
+    uint32_t out_f32; // 1: FP32 output (logits), 0: FP16 output (matmul)
+};
+
+struct GhRmsnormArgs {
+    uint64_t out;   // f16 [rows][dim]
+    uint64_t x;     // f32 [rows][dim]
+    uint64_t w;     // f16 [dim]
+    uint32_t dim;
+    uint32_t rows;
+    float eps;
+    uint32_t pad;
+};
+
+// RoPE over `rows` packed rows of `heads` heads; row r sits at absolute position base + r (or
+// base + *pos_ptr when pos_ptr != 0). table: float2 (cos, sin) [positions][pairs];
+// post: f32 [positions] query post-scale (role 0) — 1.0 for keys.
+struct GhRopeArgs {
+    uint64_t x;       // f16 [rows][heads][head_dim], rotated in place
+    uint64_t table;
+    uint64_t post;    // 0 for keys
+    uint64_t pos_ptr; // optional u32* position on the device
+    uint32_t heads;
+    uint32_t head_dim;
+    uint32_t pairs;   // rope_dim / 2
+    uint32_t base;
+    uint32_t rows;
+    uint32_t pad;
+};
+
+struct GhEltArgs {
+    uint64_t out;
+    uint64_t a;
+    uint64_t b;
+    uint32_t n;
+    uint32_t pad;
+};
+
+// KV append of `vectors_k` K values (and V) at element offsets (off + pos*stride) when pos_ptr.
+struct GhKvWriteArgs {
+    uint64_t kc;
+    uint64_t vc;
+    uint64_t k;
+    uint64_t v;
+    uint64_t pos_ptr;    // optional u32* position; element offset = base + (*pos_ptr)*stride
+    uint64_t k_off;      // element offsets into the caches
+    uint64_t v_off;
+    uint32_t k_count;    // elements to copy
+    uint32_t v_count;
+    uint32_t k_stride;   // elements per position (pos_ptr mode)
+    uint32_t v_stride;
+};
+
+// Split-K flash decode: grid (kv_heads, splits, rows). Row r attends positions 0..pos_r where
+// pos_r = base + r (or *pos_ptr). Partials: m, l [rows][q_heads][splits],
+// acc [rows][q_heads][splits][value_dim].
+struct GhAttnArgs {
+    uint64_t q;        // f16 [rows][q_heads][key_dim]
+    uint64_t kc;       // f16 cache base [layer][context][kv_heads][key_dim]
+    uint64_t vc;
+    uint64_t out;      // f16 [rows][q_heads][value_dim]
+    uint64_t part_m;   // f32 workspace
+    uint64_t part_l;
+    uint64_t part_acc;
+    uint64_t pos_ptr;  // optional u32* position
+    uint32_t key_dim;
+    uint32_t value_dim;
+    uint32_t kv_heads;
+    uint32_t q_heads;
+    uint32_t layer;
+    uint32_t context;
+    uint32_t base;
+    uint32_t rows;
+    uint32_t splits;
+    uint32_t split_len; // positions per split
+    float scale;
+    uint32_t pad;
+};
+
+struct GhArgmaxArgs {
+    uint64_t logits;   // f32 [n]
+    uint64_t part_v;   // f32 [blocks]
+    uint64_t part_i;   // u32 [blocks]
+    uint64_t out;      // u32 result
+    uint64_t out2;     // optional second u32 destination (next token id for graph replay)
+    uint32_t n;
+    uint32_t blocks;
+};
+
+// End of a replayed greedy decode step: scalars u32[0] = position, [1] = token id,
+// [2] = argmax of this step. history[pos] = argmax; token = argmax; pos += 1.
+struct GhStepArgs {
+    uint64_t scalars;
+    uint64_t history;
+};
+
+#endif

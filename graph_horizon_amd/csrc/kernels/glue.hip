@@ -1,0 +1,146 @@
+// Decode/prefill glue: RMSNorm, YaRN RoPE, SiLU·up, residual add, KV append, argmax.
+#include "gh_common.h"
+
+// rmsnorm_x (backend/cpu/kernels/elementwise/normalization.rs:12-40): one workgroup per row,
+// Σx² reduced in FP32, inverse = 1/sqrt(Σx²/dim + eps), out = f16((x*inverse)*w).
+GH_KERNEL __launch_bounds__(256) void gh_rmsnorm_x(GhRmsnormArgs a) {
+#pragma clang fp contract(off)
+    const uint32_t row = blockIdx.x;
+    if (row >= a.rows) return;
+    const float* x = (const float*)a.x + (size_t)row * a.dim;
+    const uint16_t* w = (const uint16_t*)a.w;
+    uint16_t* out = (uint16_t*)a.out + (size_t)row * a.dim;
+    __shared__ float partial[4];
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < a.dim; i += blockDim.x) s += x[i] * x[i];
+    s = gh_wave_sum(s);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float sum = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inverse = 1.0f / __builtin_sqrtf(sum / (float)a.dim + a.eps);
+    for (uint32_t i = threadIdx.x; i < a.dim; i += blockDim.x)
+        out[i] = gh_f2h(x[i] * inverse * gh_h2f(w[i]));
+}
+
+// rope_yarn (cpu/kernels/elementwise/rope.rs:14-39): adjacent pairs rotated by the per
+// (position, pair) YaRN (cos, sin) table, then the role's post-scale; FP16 in place.
+// One thread per (row, head, pair).
+GH_KERNEL __launch_bounds__(256) void gh_rope(GhRopeArgs a) {
+#pragma clang fp contract(off)
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)a.rows * a.heads * a.pairs;
+    if (t >= total) return;
+    const uint32_t pair = (uint32_t)(t % a.pairs);
+    const size_t rh = t / a.pairs;
+    const uint32_t head = (uint32_t)(rh % a.heads);
+    const uint32_t row = (uint32_t)(rh / a.heads);
+    const uint32_t pos = (a.pos_ptr ? *(const uint32_t*)a.pos_ptr : 0u) + a.base + row;
+    const float2 cs = ((const float2*)a.table)[(size_t)pos * a.pairs + pair];
+    const float scale = a.post ? ((const float*)a.post)[pos] : 1.0f;
+    uint32_t* p = (uint32_t*)((uint16_t*)a.x + ((size_t)row * a.heads + head) * a.head_dim + 2 * pair);
+    const uint32_t v = *p;
+    const float x0 = gh_h2f(v & 0xFFFFu), x1 = gh_h2f(v >> 16);
+    const float y0 = (x0 * cs.x - x1 * cs.y) * scale;
+    const float y1 = (x0 * cs.y + x1 * cs.x) * scale;
+    *p = (uint32_t)gh_f2h(y0) | ((uint32_t)gh_f2h(y1) << 16);
+}
+
+// silu_mul (cpu/kernels/elementwise/activation.rs:16-29): out = f16(f16(g/(1+exp(-g))) * u).
+GH_KERNEL __launch_bounds__(256) void gh_silu_mul(GhEltArgs a) {
+#pragma clang fp contract(off)
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    const float g = gh_h2f(((const uint16_t*)a.a)[i]);
+    const float u = gh_h2f(((const uint16_t*)a.b)[i]);
+    const float silu = g / (1.0f + expf(-g));
+    const float rounded = gh_h2f(gh_f2h(silu));
+    ((uint16_t*)a.out)[i] = gh_f2h(rounded * u);
+}
+
+// residual_add (cpu/kernels/elementwise/residual.rs:12-22): x(f32) += f16 y.
+GH_KERNEL __launch_bounds__(256) void gh_residual_add(GhEltArgs a) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    float* x = (float*)a.out;
+    x[i] = x[i] + gh_h2f(((const uint16_t*)a.b)[i]);
+}
+
+// kv_write f16 (cpu/kernels/attention/write.rs:50-63): raw FP16 copy of K and V into the
+// caches at element offsets; with pos_ptr the offsets advance by stride * (*pos_ptr).
+GH_KERNEL __launch_bounds__(256) void gh_kv_write(GhKvWriteArgs a) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t pos = a.pos_ptr ? *(const uint32_t*)a.pos_ptr : 0u;
+    if (i < a.k_count)
+        ((uint16_t*)a.kc)[a.k_off + pos * a.k_stride + i] = ((const uint16_t*)a.k)[i];
+    if (i < a.v_count)
+        ((uint16_t*)a.vc)[a.v_off + pos * a.v_stride + i] = ((const uint16_t*)a.v)[i];
+}
+
+// argmax_f32 (backend/cpu/readback.rs:45-55): first index of the maximum, NaN never wins;
+// if no logit exceeds -inf the answer is 0. Stage 1: one (value, index) per workgroup.
+__device__ __forceinline__ void argmax_merge(float& v, uint32_t& i, float ov, uint32_t oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+__device__ __forceinline__ void argmax_block(float& v, uint32_t& i) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const uint32_t oi = __shfl_xor(i, off, 64);
+        argmax_merge(v, i, ov, oi);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = v;
+        si[threadIdx.x >> 6] = i;
+    }
+    __syncthreads();
+    v = sv[0];
+    i = si[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) argmax_merge(v, i, sv[w], si[w]);
+}
+
+GH_KERNEL __launch_bounds__(256) void gh_argmax_partial(GhArgmaxArgs a) {
+    const float* l = (const float*)a.logits;
+    float v = -__builtin_inff();
+    uint32_t idx = 0xFFFFFFFFu;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < a.n; j += stride) {
+        const float x = l[j];
+        if (x > v) {  // strict: the first (lowest) index of this thread's subset wins
+            v = x;
+            idx = j;
+        }
+    }
+    argmax_block(v, idx);
+    if (threadIdx.x == 0) {
+        ((float*)a.part_v)[blockIdx.x] = v;
+        ((uint32_t*)a.part_i)[blockIdx.x] = idx;
+    }
+}
+
+GH_KERNEL __launch_bounds__(256) void gh_argmax_final(GhArgmaxArgs a) {
+    float v = -__builtin_inff();
+    uint32_t idx = 0xFFFFFFFFu;
+    for (uint32_t j = threadIdx.x; j < a.blocks; j += blockDim.x)
+        argmax_merge(v, idx, ((const float*)a.part_v)[j], ((const uint32_t*)a.part_i)[j]);
+    argmax_block(v, idx);
+    if (threadIdx.x == 0) {
+        const uint32_t r = (idx == 0xFFFFFFFFu) ? 0u : idx;
+        *(uint32_t*)a.out = r;
+        if (a.out2) *(uint32_t*)a.out2 = r;
+    }
+}
+
+GH_KERNEL void gh_step_advance(GhStepArgs a) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    uint32_t* s = (uint32_t*)a.scalars;
+    const uint32_t pos = s[0], r = s[2];
+    ((uint32_t*)a.history)[pos] = r;
+    s[1] = r;
+    s[0] = pos + 1;
+}

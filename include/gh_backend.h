@@ -1,0 +1,261 @@
+/*
+ * gh_backend.h — C ABI of the MI355X (gfx950) numeric backend for graph_horizon_engine.
+ *
+ * This is the drop-in boundary: every entry point below replaces one method of the engine's
+ * `trait Backend` (crates/graph_horizon_engine/src/backend/contract.rs:20-319, cited per
+ * function as contract.rs:LINE), in the same argument order, so a Rust `backend/hip/` crate
+ * is a set of thin `extern "C"` delegators. Plain pointers and integers only.
+ *
+ * Conventions
+ *   - Status: 0 = GH_OK, negative = a bounded GH_E_* code. No exception crosses the ABI.
+ *   - Ops the trait declares infallible (matmul, logits, rmsnorm_x, silu_mul, residual_add,
+ *     attention_*) still return a status; an error is also latched in the encoder and
+ *     reported again by gh_submit, as the Vulkan backend reports at submit_wait.
+ *   - One backend = one HIP device + one HIP stream. The caller serializes calls
+ *     (generation is serialized in the engine, runtime/homogeneous.rs:18-124).
+ *   - Dimensions are u32, byte offsets u64 (contract.rs:29-56).
+ *   - FP16 activations, FP32 residual and logits, FP16 KV cache (the f16 scheme).
+ *   - Weight format travels with the buffer (cpu/buffer.rs:48-53): ggml type ids
+ *     F32 = 0, F16 = 1, Q4_K = 12, Q6_K = 14 (gguf/tensor_index.rs:36-54).
+ */
+#ifndef GH_BACKEND_H
+#define GH_BACKEND_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum gh_status {
+    GH_OK = 0,
+    GH_E_INVALID = -1,     /* bad argument, size or shape */
+    GH_E_NO_DEVICE = -2,   /* no HIP device, or the device is not gfx950 */
+    GH_E_HIP = -3,         /* a HIP runtime call failed */
+    GH_E_OOM = -4,         /* device allocation failed */
+    GH_E_RANGE = -5,       /* position/offset beyond a buffer or the context */
+    GH_E_MODULE = -6,      /* the gfx950 code object could not be loaded */
+    GH_E_STATE = -7,       /* call out of order (no encoder, double begin, ...) */
+    GH_E_UNSUPPORTED = -8  /* format/scheme outside the admitted Q4_K_M profile */
+};
+
+enum gh_format { GH_FMT_F32 = 0, GH_FMT_F16 = 1, GH_FMT_Q4_K = 12, GH_FMT_Q6_K = 14 };
+
+enum gh_buf_kind {
+    GH_BUF_ALLOC = 1,  /* owns a device allocation; free with gh_free_buffer */
+    GH_BUF_VIEW = 2,   /* aliases a parent window; never freed (contract.rs:32-48) */
+    GH_BUF_WEIGHT = 3  /* owns a quantized weight in the device layout; free with gh_free_buffer */
+};
+
+/* A buffer handle, passed by value like the trait's `Buffer`. `addr` is the device address of
+ * byte 0 of the window. For GH_BUF_WEIGHT, rows = out_dim and cols = in_dim of the matrix. */
+typedef struct gh_buf {
+    uint64_t addr;
+    uint64_t bytes;
+    uint32_t format;
+    uint32_t kind;
+    uint32_t rows;
+    uint32_t cols;
+} gh_buf;
+
+typedef struct gh_config {
+    int32_t device;               /* HIP device ordinal */
+    const char* code_object_path; /* NULL: gh_kernels_gfx950.co next to the library */
+} gh_config;
+
+/* Ministral YaRN parameters (backend/rope.rs:11-21). */
+typedef struct gh_yarn {
+    uint32_t rope_dim;
+    uint32_t original_context;
+    float freq_base;
+    float factor;
+    float beta_fast;
+    float beta_slow;
+    float log_multiplier;
+    float q_temperature_scale;
+} gh_yarn;
+
+enum gh_rope_role { GH_ROPE_QUERY = 0, GH_ROPE_KEY = 1 }; /* backend/rope.rs:23-27 */
+enum gh_kv_scheme { GH_KV_F16 = 0, GH_KV_INT8 = 1 };      /* kv_cache/scheme.rs */
+
+/* Request KV handle (kv_cache/mod.rs:29-38). Caches are [layer][context][kv_heads][dim]. */
+typedef struct gh_kv {
+    gh_buf k;
+    gh_buf v;
+    uint32_t scheme;
+    uint32_t block_count;
+    uint32_t context;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t value_dim;
+} gh_kv;
+
+typedef struct gh_backend gh_backend;
+typedef struct gh_encoder gh_encoder;
+
+/* ---- lifecycle: backend/selection.rs:40-81 (load) — device init, gfx950 check,
+ *      hipModuleLoad of the kernels' code object ---- */
+int gh_create(const gh_config* cfg, gh_backend** out);
+void gh_destroy(gh_backend* b);
+/* Short description of the most recent error on this backend (static storage, never NULL). */
+const char* gh_last_error(const gh_backend* b);
+
+/* ---- buffers ---- */
+/* alloc_buffer, contract.rs:29 */
+int gh_alloc_buffer(gh_backend* b, uint64_t bytes, gh_buf* out);
+/* free_buffer, contract.rs:30 (views are rejected with GH_E_INVALID, contract.rs:38-40) */
+int gh_free_buffer(gh_backend* b, gh_buf* buf);
+/* view, contract.rs:48: alias of [offset, offset+len) of `buf`, no allocation, no copy */
+int gh_view(gh_backend* b, const gh_buf* buf, uint64_t offset_bytes, uint64_t len_bytes,
+            gh_buf* out);
+/* min_buffer_offset_alignment, contract.rs:56 */
+uint64_t gh_min_buffer_offset_alignment(const gh_backend* b);
+/* host<->device copies (the CPU backend's buffer read/write; vulkan/mem/buffers.rs staging);
+ * synchronous with respect to the backend stream */
+int gh_upload(gh_backend* b, const gh_buf* dst, uint64_t offset, const void* src, uint64_t len);
+int gh_download(gh_backend* b, const gh_buf* src, uint64_t offset, void* dst, uint64_t len);
+/* Weight load (cpu/weights.rs:37-174, vulkan/mem/weights.rs): GGUF block bytes of an
+ * [out_dim][in_dim] matrix. Q4_K/Q6_K are validated as whole blocks (cpu/dequant.rs:35-41) and
+ * repacked losslessly into the device layout; F32 is narrowed RNE to F16 (cpu/weights.rs:155),
+ * F16 is copied. in_dim must be a multiple of 256 for quantized formats. */
+int gh_load_weight(gh_backend* b, uint32_t format, const void* bytes, uint64_t len,
+                   uint32_t in_dim, uint32_t out_dim, gh_buf* out);
+/* Decode rows [row0, row0+rows) of a quantized weight to FP32 [rows][in_dim] on the device
+ * (dequant_row, cpu/dequant.rs:47-67); the bit-exact reference for the dequant parity check. */
+int gh_dequant_rows(gh_backend* b, gh_encoder* enc, const gh_buf* out_f32, const gh_buf* w,
+                    uint32_t row0, uint32_t rows);
+
+/* ---- encoder: begin, contract.rs:78; submit, contract.rs:79 (synchronous);
+ *      no_barrier, contract.rs:87 (a scheduling hint; never changes the math) ---- */
+int gh_begin(gh_backend* b, gh_encoder** enc);
+int gh_submit(gh_backend* b, gh_encoder* enc);
+void gh_no_barrier(gh_backend* b);
+
+/* ---- numeric ops ---- */
+/* kv_write, contract.rs:64-75 (f16 scheme: raw copy of `vectors` K and V vectors to the
+ * payload byte offsets computed by kv_cache/layout.rs) */
+int gh_kv_write(gh_backend* b, gh_encoder* enc, const gh_kv* kv, const gh_buf* k,
+                const gh_buf* v, uint64_t k_payload_offset, uint64_t v_payload_offset,
+                uint64_t k_meta_offset, uint64_t v_meta_offset, uint32_t vectors);
+/* embed, contract.rs:91-98: dequantize row `token` of token_embd into FP32 x */
+int gh_embed(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* token_embd,
+             uint32_t token, uint32_t embd);
+/* matmul, contract.rs:101-109: out FP16[out_dim] = W · a (a FP16[in_dim]) */
+int gh_matmul(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* a,
+              const gh_buf* w, uint32_t in_dim, uint32_t out_dim);
+/* matmul_batched, contract.rs:119-145: a FP16[n][in_dim] -> out FP16[n][out_dim] */
+int gh_matmul_batched(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* a,
+                      const gh_buf* w, uint32_t in_dim, uint32_t out_dim, uint32_t n);
+/* logits, contract.rs:148-156: out FP32[out_dim] = W · x */
+int gh_logits(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* x,
+              const gh_buf* w, uint32_t in_dim, uint32_t out_dim);
+/* rmsnorm_x, contract.rs:159-168: FP32 x rows -> FP16 out, FP16 weight */
+int gh_rmsnorm_x(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* x,
+                 const gh_buf* w, uint32_t dim, float eps, uint32_t rows);
+/* rope_yarn, contract.rs:172-181: in place on FP16 x[heads][head_dim] at position pos */
+int gh_rope_yarn(gh_backend* b, gh_encoder* enc, const gh_buf* x, uint32_t heads,
+                 uint32_t head_dim, uint32_t pos, const gh_yarn* yarn, uint32_t role);
+/* rope_yarn_batched, contract.rs:187-246: rows packed Q then K rows at base..base+rows */
+int gh_rope_yarn_batched(gh_backend* b, gh_encoder* enc, const gh_buf* q, const gh_buf* k,
+                         uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t base,
+                         uint32_t rows, const gh_yarn* yarn);
+/* silu_mul, contract.rs:252-259: out = f16(f16(silu(gate)) * up) */
+int gh_silu_mul(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* gate,
+                const gh_buf* up, uint32_t n);
+/* residual_add, contract.rs:261: FP32 x[i] += FP16 y[i] */
+int gh_residual_add(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* y,
+                    uint32_t n);
+/* attention_decode, contract.rs:267-276 */
+int gh_attention_decode(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* q,
+                        const gh_kv* kv, uint32_t q_heads, uint32_t pos, uint32_t layer);
+/* attention_prefill, contract.rs:288-298 */
+int gh_attention_prefill(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* q,
+                         const gh_kv* kv, uint32_t q_heads, uint32_t base, uint32_t n,
+                         uint32_t layer);
+
+/* ---- read-back, contract.rs:300-318 (synchronous) ---- */
+int gh_read_logits(gh_backend* b, const gh_buf* logits, uint64_t vocab, float* dst);
+/* lowest index wins on equal logits (strict `>`) */
+int gh_read_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, uint32_t* out);
+/* min(k, vocab) pairs ordered by (logit desc by IEEE total order, index asc) */
+int gh_read_topk(gh_backend* b, const gh_buf* logits, uint64_t vocab, uint64_t k,
+                 uint32_t* idx, float* val, uint64_t* count);
+
+/* ---- measurement helpers (no counterpart in the reference: the engine measures through
+ *      its public event stream, harness/throughput.rs:64-147). HIP events recorded on the
+ *      backend's stream, so they bracket exactly the kernels this backend launches. ---- */
+int gh_timer_start(gh_backend* b);
+/* milliseconds since gh_timer_start, after synchronizing the stream */
+int gh_timer_stop(gh_backend* b, float* ms);
+int gh_synchronize(gh_backend* b);
+
+/* =====================================================================================
+ * Graph driver: a C++ restatement of the caller side of the boundary — MistralGraph's pinned
+ * op order for one token (family/mistral/graph/forward.rs:68-83, block.rs:17-107,
+ * mlp.rs:12-61, tail.rs:22-59) and for batched prefill (graph/prefill/encode.rs:16-106,
+ * prefill/layer.rs:18-122) — recorded through the ops above. It owns the engine-side
+ * `Buffers{weights, scratch, logits}` (backend/buffers.rs:17-60) and one request KV.
+ * ===================================================================================== */
+typedef struct gh_model_config {
+    uint32_t block_count;
+    uint32_t context_length;
+    uint32_t embedding_length;
+    uint32_t feed_forward_length;
+    uint32_t head_count;
+    uint32_t kv_head_count;
+    uint32_t key_length;
+    uint32_t value_length;
+    uint32_t vocab_size;
+    float rms_epsilon;
+    gh_yarn yarn;
+    uint32_t kv_context;   /* request KV capacity in tokens (kv_cache::alloc_shape) */
+    uint32_t prefill_rows; /* prefill chunk row capacity (graph/prefill/mod.rs:20-22) */
+} gh_model_config;
+
+/* Tensor ids for gh_model_load_tensor. Per-layer ids follow backend/source.rs's canonical
+ * order; global ids use layer = UINT32_MAX. */
+enum gh_tensor_id {
+    GH_T_ATTN_NORM = 0,
+    GH_T_ATTN_Q = 1,
+    GH_T_ATTN_K = 2,
+    GH_T_ATTN_V = 3,
+    GH_T_ATTN_OUTPUT = 4,
+    GH_T_FFN_NORM = 5,
+    GH_T_FFN_GATE = 6,
+    GH_T_FFN_UP = 7,
+    GH_T_FFN_DOWN = 8,
+    GH_T_TOKEN_EMBD = 16,
+    GH_T_OUTPUT_NORM = 17,
+    GH_T_OUTPUT = 18
+};
+
+typedef struct gh_model gh_model;
+int gh_model_create(gh_backend* b, const gh_model_config* cfg, gh_model** out);
+void gh_model_destroy(gh_model* m);
+/* GGUF bytes of one tensor (F32 norms are narrowed to F16 at load, cpu/weights.rs:151-174) */
+int gh_model_load_tensor(gh_model* m, uint32_t layer, uint32_t tensor, uint32_t format,
+                         const void* bytes, uint64_t len);
+/* forward::token: embed, block_count blocks, tail; FP32 logits left on the device */
+int gh_model_token(gh_model* m, uint32_t token, uint32_t pos);
+/* prefill::prefill: tokens[0..n) at positions base.., chunked by prefill_rows */
+int gh_model_prefill(gh_model* m, const uint32_t* tokens, uint32_t n, uint32_t base);
+int gh_model_read_logits(gh_model* m, float* dst);
+int gh_model_read_argmax(gh_model* m, uint32_t* out);
+/* Greedy decode loop (generation/mod.rs:107-139 with sampling's greedy argmax): starting
+ * from `token` at `pos`, runs `steps` decode steps; step i feeds the argmax of step i-1.
+ * The whole step (embed .. logits .. argmax) is one replayed HIP graph with the token id and
+ * position resident on the device; tokens_out[i] receives the argmax of step i. */
+int gh_model_decode_greedy(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps,
+                           uint32_t* tokens_out);
+/* KV cache handle of the model's request (for parity checks of the cache contents) */
+int gh_model_kv(gh_model* m, gh_kv* out);
+/* the FP32 residual x of the last token processed (embedding_length floats) */
+int gh_model_read_x(gh_model* m, float* dst);
+/* the device handle of one loaded tensor (layer = UINT32_MAX for global tensors), e.g. to
+ * time a single projection on the model's own resident weights */
+int gh_model_weight(gh_model* m, uint32_t layer, uint32_t tensor, gh_buf* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

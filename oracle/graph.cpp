@@ -1,0 +1,150 @@
+// gh_oracle graph restatement (test infrastructure): the pinned Ministral op order and FP16
+// rounding boundaries of family/mistral/graph/{forward,block,mlp,tail}.rs and
+// graph/prefill/{encode,layer}.rs, executed over host buffers with the oracle's ops.
+#include <cstring>
+#include <vector>
+
+#include "gh_oracle.h"
+#include "internal.h"
+
+using namespace gho;
+
+struct gho_model {
+    gho_model_cfg cfg;
+    gho_tensor token_embd, output_norm, output;
+    std::vector<gho_tensor> layers;
+    uint32_t kv_context;
+    std::vector<uint16_t> kc, vc;  // [layer][kv_context][kv_heads][head_dim]
+    std::vector<float> logits;
+    std::vector<float> last_x;
+};
+
+namespace {
+const uint16_t* f16p(const gho_tensor& t) { return (const uint16_t*)t.bytes; }
+
+// kv_cache::append_batch (kv_cache/mod.rs:133-177) + kv_write_f16 (attention/write.rs:50-63).
+void kv_append(gho_model* m, size_t layer, size_t pos, const uint16_t* k, const uint16_t* v,
+               size_t rows) {
+    const auto& c = m->cfg;
+    size_t elems = rows * c.kv_head_count * c.key_length;
+    size_t off = gho_kv_payload_offset(layer, pos, c.kv_head_count, c.key_length, m->kv_context) / 2;
+    std::memcpy(m->kc.data() + off, k, elems * 2);
+    size_t voff =
+        gho_kv_payload_offset(layer, pos, c.kv_head_count, c.value_length, m->kv_context) / 2;
+    std::memcpy(m->vc.data() + voff, v, rows * c.kv_head_count * c.value_length * 2);
+}
+
+// One layer for `rows` packed tokens at absolute positions base.. (prefill/layer.rs:18-122);
+// rows == 1 is block::record (block.rs:17-107) with matmul_batched(n=1) == matmul.
+void layer_rows(gho_model* m, size_t li, size_t base, size_t rows, std::vector<float>& x) {
+    const auto& c = m->cfg;
+    const gho_tensor* t = &m->layers[li * GHO_LAYER_TENSORS];
+    size_t d = c.embedding_length, ffn = c.feed_forward_length;
+    size_t qw = c.head_count * c.key_length, kw = c.kv_head_count * c.key_length;
+    size_t vw = c.kv_head_count * c.value_length, aw = c.head_count * c.value_length;
+    std::vector<uint16_t> normed(rows * d), q(rows * qw), k(rows * kw), v(rows * vw);
+    std::vector<uint16_t> attn(rows * aw), proj(rows * d);
+    gho_rmsnorm_x(normed.data(), x.data(), f16p(t[GHO_ATTN_NORM]), d, c.rms_epsilon, rows);
+    gho_matmul_batched(t[GHO_ATTN_Q].format, q.data(), normed.data(), t[GHO_ATTN_Q].bytes, d, qw, rows);
+    gho_matmul_batched(t[GHO_ATTN_K].format, k.data(), normed.data(), t[GHO_ATTN_K].bytes, d, kw, rows);
+    gho_matmul_batched(t[GHO_ATTN_V].format, v.data(), normed.data(), t[GHO_ATTN_V].bytes, d, vw, rows);
+    // rope_yarn_batched default (contract.rs:187-246): per row, Q then K at base + row.
+    for (size_t r = 0; r < rows; ++r) {
+        gho_rope_yarn(q.data() + r * qw, c.head_count, c.key_length, base + r, &c.yarn, 0);
+        gho_rope_yarn(k.data() + r * kw, c.kv_head_count, c.key_length, base + r, &c.yarn, 1);
+    }
+    kv_append(m, li, base, k.data(), v.data(), rows);
+    if (rows == 1)
+        gho_attention_decode(attn.data(), q.data(), m->kc.data(), m->vc.data(), c.key_length,
+                             c.value_length, c.kv_head_count, c.head_count, base, li, m->kv_context);
+    else
+        gho_attention_prefill(attn.data(), q.data(), m->kc.data(), m->vc.data(), c.key_length,
+                              c.value_length, c.kv_head_count, c.head_count, base, rows, li,
+                              m->kv_context);
+    gho_matmul_batched(t[GHO_ATTN_OUTPUT].format, proj.data(), attn.data(),
+                       t[GHO_ATTN_OUTPUT].bytes, aw, d, rows);
+    gho_residual_add(x.data(), proj.data(), d * rows);
+    // mlp::record (mlp.rs:12-61)
+    std::vector<uint16_t> gate(rows * ffn), up(rows * ffn), act(rows * ffn), ffn_out(rows * d);
+    gho_rmsnorm_x(normed.data(), x.data(), f16p(t[GHO_FFN_NORM]), d, c.rms_epsilon, rows);
+    gho_matmul_batched(t[GHO_FFN_GATE].format, gate.data(), normed.data(), t[GHO_FFN_GATE].bytes, d, ffn, rows);
+    gho_matmul_batched(t[GHO_FFN_UP].format, up.data(), normed.data(), t[GHO_FFN_UP].bytes, d, ffn, rows);
+    gho_silu_mul(act.data(), gate.data(), up.data(), ffn * rows);
+    gho_matmul_batched(t[GHO_FFN_DOWN].format, ffn_out.data(), act.data(), t[GHO_FFN_DOWN].bytes, ffn, d, rows);
+    gho_residual_add(x.data(), ffn_out.data(), d * rows);
+}
+
+// tail::record_buffers (tail.rs:22-59): output_norm then FP32 logits (dedicated or tied).
+void tail(gho_model* m, const float* xrow) {
+    const auto& c = m->cfg;
+    size_t d = c.embedding_length;
+    std::vector<uint16_t> normed(d);
+    gho_rmsnorm_x(normed.data(), xrow, f16p(m->output_norm), d, c.rms_epsilon, 1);
+    const gho_tensor& out = m->output.bytes ? m->output : m->token_embd;
+    gho_logits(out.format, m->logits.data(), normed.data(), out.bytes, d, c.vocab_size);
+}
+}  // namespace
+
+extern "C" {
+gho_model* gho_model_create(const gho_model_cfg* cfg, const gho_tensor* token_embd,
+                            const gho_tensor* output_norm, const gho_tensor* output,
+                            const gho_tensor* layers, uint32_t kv_context) {
+    auto* m = new gho_model();
+    m->cfg = *cfg;
+    m->token_embd = *token_embd;
+    m->output_norm = *output_norm;
+    m->output = output ? *output : gho_tensor{nullptr, 0};
+    m->layers.assign(layers, layers + (size_t)cfg->block_count * GHO_LAYER_TENSORS);
+    m->kv_context = kv_context;
+    size_t kv = (size_t)cfg->block_count * kv_context * cfg->kv_head_count;
+    m->kc.assign(kv * cfg->key_length, 0);
+    m->vc.assign(kv * cfg->value_length, 0);
+    m->logits.assign(cfg->vocab_size, 0.0f);
+    return m;
+}
+
+void gho_model_destroy(gho_model* m) { delete m; }
+
+// forward::token (forward.rs:68-83).
+int gho_model_token(gho_model* m, uint32_t token, uint32_t pos) {
+    const auto& c = m->cfg;
+    if (pos >= c.context_length || pos >= m->kv_context) return -1;
+    if (token >= c.vocab_size) return -1;
+    std::vector<float> x(c.embedding_length);
+    gho_embed(x.data(), m->token_embd.format, m->token_embd.bytes, token, c.embedding_length);
+    for (size_t li = 0; li < c.block_count; ++li) layer_rows(m, li, pos, 1, x);
+    tail(m, x.data());
+    m->last_x = x;
+    return 0;
+}
+
+// prefill::prefill + record_batch (prefill/encode.rs:16-106): chunks of row_capacity rows;
+// the tail runs only on the last chunk's last row.
+int gho_model_prefill(gho_model* m, const uint32_t* tokens, uint32_t n, uint32_t base,
+                      uint32_t row_capacity) {
+    const auto& c = m->cfg;
+    if (n == 0 || row_capacity == 0) return -1;
+    if ((size_t)base + n > m->kv_context) return -1;
+    size_t d = c.embedding_length;
+    for (uint32_t off = 0; off < n; off += row_capacity) {
+        uint32_t rows = std::min(row_capacity, n - off);
+        std::vector<float> x(rows * d);
+        for (uint32_t r = 0; r < rows; ++r) {
+            if (tokens[off + r] >= c.vocab_size) return -1;
+            gho_embed(x.data() + r * d, m->token_embd.format, m->token_embd.bytes, tokens[off + r], d);
+        }
+        for (size_t li = 0; li < c.block_count; ++li) layer_rows(m, li, base + off, rows, x);
+        if (off + rows == n) {
+            tail(m, x.data() + (rows - 1) * d);
+            m->last_x.assign(x.begin() + (rows - 1) * d, x.begin() + rows * d);
+        }
+    }
+    return 0;
+}
+
+const float* gho_model_logits(const gho_model* m) { return m->logits.data(); }
+const uint16_t* gho_model_kv(const gho_model* m, int role) {
+    return role == 0 ? m->kc.data() : m->vc.data();
+}
+const float* gho_model_x(const gho_model* m) { return m->last_x.data(); }
+}

@@ -1,0 +1,497 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker of the HIP backend.
+
+Each check is chosen so a plausible restatement mistake (wrong byte index, dropped term, swapped
+operand, wrong rounding) fails: the reference's own known-answer vectors, exhaustive sweeps,
+closed forms evaluated independently in numpy, and fp64 brute force.
+"""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from graph_horizon_amd import synth
+
+
+# ---------------------------------------------------------------- f16 (backend/f16.rs)
+def test_f16_known_answers(ora, goldens):
+    g = goldens["f16"]
+    lib = ora.lib()
+    for v in g["round_trip_exact"]:
+        h = lib.gho_f32_to_f16(v)
+        back = lib.gho_f16_to_f32(h)
+        assert np.float32(back).view(np.uint32) == np.float32(v).view(np.uint32)
+    for v, want in g["narrow"]:
+        v = float(v) if not isinstance(v, str) else float(v.replace("inf", "inf"))
+        assert lib.gho_f32_to_f16(v) == want
+    for h, want in g["widen"]:
+        got = lib.gho_f16_to_f32(h)
+        assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32)
+    bl = g["bytes_le"]
+    assert list(ora.f16(bl["values"]).view(np.uint8)) == bl["bytes"]
+    assert math.isnan(lib.gho_f16_to_f32(lib.gho_f32_to_f16(float("nan"))))
+
+
+def test_f16_widening_exhaustive_matches_numpy():
+    """All 65536 patterns: restated widening == numpy's independent binary16 conversion."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32).view(np.uint32)
+    # the scalar widening read through dequant_row(F16) (cpu/dequant.rs:55-60), which stores
+    # f32 bits to memory (a ctypes float return would quiet signaling NaNs in transit)
+    scalar = O.dequant(O.FMT_F16, h.view(np.uint8), 1, 65536)[0]
+    assert np.array_equal(scalar.view(np.uint32), want)  # backend/f16.rs:11-37, all patterns
+    # F16C slice widening (backend/cpu/f16.rs:131-168) quiets signaling NaNs (vcvtph2ps);
+    # every other pattern is bit-identical to the scalar.
+    snan = ((h & 0x7C00) == 0x7C00) & ((h & 0x03FF) != 0) & ((h & 0x0200) == 0)
+    got = O.f32(h).view(np.uint32)
+    assert np.array_equal(got[~snan], want[~snan])
+    assert np.all(np.isnan(O.f32(h[snan])))
+
+
+def test_f16_narrowing_rne_sweep():
+    """Scalar restated narrowing == numpy RNE over normals, subnormals and halfway cases."""
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2**32, 400_000, dtype=np.uint64).astype(np.uint32)
+    vals = bits.view(np.float32)
+    vals = vals[np.isfinite(vals)]
+    halfway = (np.arange(0, 65536, 7, dtype=np.uint32).astype(np.uint16).view(np.float16)
+               .astype(np.float32))
+    halfway = halfway[np.isfinite(halfway)]
+    mids = (halfway.view(np.uint32) + np.uint32(0x1000)).view(np.float32)
+    vals = np.concatenate([vals, mids[np.isfinite(mids)], np.float32([1e-8, -1e-8, 65519.99, 65520.0])])
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    got = np.array([O.lib().gho_f32_to_f16(float(v)) for v in vals[:20000]], dtype=np.uint16)
+    assert np.array_equal(got, want[:20000])
+    assert np.array_equal(O.f16(vals), want)  # F16C slice path (backend/cpu/f16.rs:176-218)
+
+
+# ---------------------------------------------------------------- dequant (cpu/dequant.rs)
+def _q4k_block(d, dmin, scales, qs):
+    b = bytearray(np.float16(d).tobytes() + np.float16(dmin).tobytes())
+    b += bytes(scales)
+    b += bytes(qs)
+    assert len(b) == 144
+    return np.frombuffer(bytes(b), dtype=np.uint8)
+
+
+def test_q4k_golden_vector(ora, goldens):
+    g = goldens["q4_k_golden_vector"]
+    blk = _q4k_block(g["d"], g["dmin"], g["scales"], [g["qs_byte"]] * 128)
+    out = ora.dequant(O.FMT_Q4_K, blk, 1, 256)[0]
+    for sb, want in enumerate(g["per_sub_block"]):
+        assert np.all(out[sb * 32:(sb + 1) * 32] == np.float32(want)), sb
+    for i, want in g["anchors"]:
+        assert out[i] == want
+    sc = np.frombuffer(bytes(g["scales"]), dtype=np.uint8)
+    for j, (s, m) in enumerate(g["sc_mn"]):
+        a, b_ = C.c_uint32(), C.c_uint32()
+        ora.lib().gho_scale_min(sc.ctypes.data, j, C.byref(a), C.byref(b_))
+        assert (a.value, b_.value) == (s, m)
+
+
+def test_q6k_golden_vector(ora, goldens):
+    g = goldens["q6_k_golden_vector"]
+    raw = bytes([g["ql_byte"]] * 128 + [g["qh_byte"]] * 64) + bytes(np.int8(g["scales"]).tobytes())
+    raw += np.float16(g["d"]).tobytes()
+    out = ora.dequant(O.FMT_Q6_K, np.frombuffer(raw, dtype=np.uint8), 1, 256)[0]
+    for seg in range(2):
+        for quarter, q in enumerate(g["q_for_quarter"]):
+            for l in range(32):
+                scale = seg * 8 + l // 16 + quarter * 2 + 1
+                assert out[seg * 128 + quarter * 32 + l] == np.float32(scale * q)
+    for i, want in g["anchors"]:
+        assert out[i] == want
+
+
+def test_validate_rejects_partial_blocks(ora, goldens):
+    for fmt, n, ok in goldens["validate"]["cases"]:
+        assert (ora.lib().gho_validate(fmt, n) == 0) == ok
+
+
+def _scale_min_spec(s):
+    """get_scale_min_k4 written from the ggml bit layout, vectorized over [n, 12] bytes."""
+    s = s.astype(np.uint32)
+    sc = np.zeros((s.shape[0], 8), np.uint32)
+    mn = np.zeros((s.shape[0], 8), np.uint32)
+    for j in range(4):
+        sc[:, j] = s[:, j] & 63
+        mn[:, j] = s[:, j + 4] & 63
+    for j in range(4, 8):
+        sc[:, j] = (s[:, j + 4] & 0xF) | ((s[:, j - 4] >> 6) << 4)
+        mn[:, j] = (s[:, j + 4] >> 4) | ((s[:, j] >> 6) << 4)
+    return sc, mn
+
+
+def test_scale_min_exhaustive_over_relevant_bits(ora):
+    """Every (sc, mn) of every sub-block depends on at most: byte j and j+4 (j<4), or the
+    whole byte j+4 plus the top two bits of bytes j-4 and j (j>=4). Sweep all of them."""
+    rng = np.random.default_rng(3)
+    cases = []
+    a = np.arange(65536)
+    lo = np.zeros((65536, 12), np.uint8)
+    lo[:, 0:4] = (a & 0xFF)[:, None]
+    lo[:, 4:8] = (a >> 8)[:, None]
+    lo[:, 8:12] = rng.integers(0, 256, (65536, 4))
+    cases.append(lo)
+    b = np.arange(4096)
+    hi = rng.integers(0, 256, (4096, 12)).astype(np.uint8)
+    hi[:, 8:12] = (b & 0xFF)[:, None]
+    hi[:, 0:4] = (hi[:, 0:4] & 0x3F) | (((b >> 8) & 3) << 6)[:, None].astype(np.uint8)
+    hi[:, 4:8] = (hi[:, 4:8] & 0x3F) | (((b >> 10) & 3) << 6)[:, None].astype(np.uint8)
+    cases.append(hi)
+    scales = np.concatenate(cases)
+    n = scales.shape[0]
+    # Read every (sc, mn) back through dequant_row: d=1,dmin=0,q=1 -> sc; d=0,dmin=1 -> -mn.
+    for d, dmin, which in ((1.0, 0.0, "sc"), (0.0, 1.0, "mn")):
+        blk = np.zeros((n, 144), np.uint8)
+        blk[:, 0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+        blk[:, 2:4] = np.frombuffer(np.float16(dmin).tobytes(), np.uint8)
+        blk[:, 4:16] = scales
+        blk[:, 16:] = 0x11
+        out = ora.dequant(O.FMT_Q4_K, blk.reshape(-1), 1, n * 256)[0].reshape(n, 8, 32)
+        sc, mn = _scale_min_spec(scales)
+        want = sc if which == "sc" else mn
+        got = out[:, :, 0] if which == "sc" else -out[:, :, 0]
+        assert np.array_equal(got.astype(np.uint32), want)
+
+
+def _q4k_closed_form(w, rows, in_dim):
+    nb = in_dim // 256
+    blk = w.reshape(rows * nb, 144)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = blk[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    sc, mn = _scale_min_spec(blk[:, 4:16])
+    qs = blk[:, 16:].astype(np.uint32)
+    q = np.zeros((rows * nb, 256), np.float32)
+    for g in range(4):
+        q[:, 64 * g:64 * g + 32] = qs[:, 32 * g:32 * g + 32] & 0xF
+        q[:, 64 * g + 32:64 * g + 64] = qs[:, 32 * g:32 * g + 32] >> 4
+    dl = (d[:, None] * sc.astype(np.float32)).repeat(32, axis=1)
+    ml = (dmin[:, None] * mn.astype(np.float32)).repeat(32, axis=1)
+    return (dl * q - ml).reshape(rows, in_dim)  # float32 mul, mul, sub: two roundings
+
+
+def _q6k_closed_form(w, rows, in_dim):
+    nb = in_dim // 256
+    blk = w.reshape(rows * nb, 210)
+    ql, qh = blk[:, :128].astype(np.int32), blk[:, 128:192].astype(np.int32)
+    sc = blk[:, 192:208].view(np.int8).astype(np.float32)
+    d = blk[:, 208:210].copy().view(np.float16).astype(np.float32)[:, 0]
+    out = np.zeros((rows * nb, 256), np.float32)
+    for seg in range(2):
+        for quarter in range(4):
+            src = ql[:, seg * 64 + (quarter & 1) * 32: seg * 64 + (quarter & 1) * 32 + 32]
+            nib = (src >> 4) if quarter >= 2 else (src & 0xF)
+            hi = (qh[:, seg * 32: seg * 32 + 32] >> (2 * quarter)) & 3
+            q = (nib | (hi << 4)) - 32
+            for half in range(2):
+                s = sc[:, seg * 8 + half + 2 * quarter]
+                sl = slice(seg * 128 + quarter * 32 + half * 16, seg * 128 + quarter * 32 + half * 16 + 16)
+                out[:, sl] = (d * s)[:, None] * q[:, half * 16:half * 16 + 16].astype(np.float32)
+    return out.reshape(rows, in_dim)
+
+
+@pytest.mark.parametrize("in_dim", [256, 1024])
+def test_dequant_closed_form_bit_exact(ora, in_dim):
+    rng = np.random.default_rng(11)
+    rows = 37
+    w4 = synth.q4k_blocks(rng, rows, in_dim)
+    assert np.array_equal(ora.dequant(O.FMT_Q4_K, w4, rows, in_dim).view(np.uint32),
+                          _q4k_closed_form(w4, rows, in_dim).view(np.uint32))
+    w6 = synth.q6k_blocks(rng, rows, in_dim)
+    assert np.array_equal(ora.dequant(O.FMT_Q6_K, w6, rows, in_dim).view(np.uint32),
+                          _q6k_closed_form(w6, rows, in_dim).view(np.uint32))
+
+
+# ---------------------------------------------------------------- GEMV (cpu/kernels/matmul)
+def _gemv_case(fmt, rows, in_dim, seed):
+    rng = np.random.default_rng(seed)
+    w = synth.quant_blocks(rng, fmt, rows, in_dim, 0.02)
+    x16 = O.f16(rng.standard_normal(in_dim).astype(np.float32))
+    return w, x16
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_Q4_K, O.FMT_Q6_K])
+@pytest.mark.parametrize("in_dim,rows", [(256, 9), (4096, 33)])
+def test_gemv_fp64_brute_force(ora, fmt, in_dim, rows):
+    w, x16 = _gemv_case(fmt, rows, in_dim, 5)
+    x = O.f32(x16).astype(np.float64)
+    deq = ora.dequant(fmt, w, rows, in_dim).astype(np.float64)
+    terms = deq * x[None, :]
+    want = terms.sum(axis=1)
+    scale = np.abs(terms).sum(axis=1)
+    got = ora.logits(fmt, x16, w, in_dim, rows).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2e-6 * scale + 1e-30)
+    # matmul is the same row dot narrowed RNE to FP16 (matmul/mod.rs:186-212)
+    assert np.array_equal(ora.matmul(fmt, x16, w, in_dim, rows), ora.f16(got.astype(np.float32)))
+    # scalar kernel (q4k.rs:58-96 / q6k.rs:31-64) agrees within FP32 rounding of the sum
+    xa = O.f32(x16)
+    fn = ora.lib().gho_row_dot_q4k_scalar if fmt == O.FMT_Q4_K else ora.lib().gho_row_dot_q6k_scalar
+    sc = np.array([fn(xa.ctypes.data, w.ctypes.data, r, in_dim) for r in range(rows)])
+    assert np.all(np.abs(sc - want) <= 2e-6 * scale + 1e-30)
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_Q4_K, O.FMT_Q6_K])
+def test_gemv_reference_pattern_within_reference_tolerance(ora, goldens, fmt):
+    """The reference's synthetic weights and activations (q4k.rs:373-424, q6k.rs:266-307)."""
+    g = goldens["synthetic_weight_pattern"]
+    in_dim, out_dim = 512, 17
+    nb = in_dim // 256
+    if fmt == O.FMT_Q4_K:
+        mul, add, mod = g["q4k_byte"]
+        w = ((np.arange(out_dim * nb * 144) * mul + add) % mod).astype(np.uint8)
+        for blk in range(out_dim * nb):
+            w[blk * 144:blk * 144 + 2] = np.frombuffer(np.float16(g["q4k_d"]).tobytes(), np.uint8)
+            w[blk * 144 + 2:blk * 144 + 4] = np.frombuffer(np.float16(g["q4k_dmin"]).tobytes(), np.uint8)
+    else:
+        mul, add, mod = g["q6k_byte"]
+        w = ((np.arange(out_dim * nb * 210) * mul + add) % mod).astype(np.uint8)
+        for blk in range(out_dim * nb):
+            w[blk * 210 + 208:blk * 210 + 210] = np.frombuffer(np.float16(g["q6k_d"]).tobytes(), np.uint8)
+    a16 = O.f16(np.sin(np.arange(in_dim, dtype=np.float32) * np.float32(0.013)))
+    a = O.f32(a16)
+    got = O.f32(ora.matmul(fmt, a16, w, in_dim, out_dim))
+    deq = ora.dequant(fmt, w, out_dim, in_dim)
+    want = np.array([np.float32(sum(np.float32(a[i]) * deq[o, i] for i in range(0, in_dim, 64)))
+                     for o in range(out_dim)])  # coarse sanity only
+    ref = (deq.astype(np.float64) * a.astype(np.float64)).sum(axis=1)
+    tol = g["rel_tol"] * np.maximum(np.abs(ref), 1e-3)
+    assert np.all(np.abs(got - ref) <= tol)
+    assert want.shape == got.shape
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_Q4_K, O.FMT_Q6_K])
+def test_matmul_batched_invariants(ora, fmt):
+    """Batched == per-row batched kernel exactly (q4k.rs:492-538, q6k.rs:339-384), and ==
+    single-token matmul within FP32 reassociation (q4k.rs:434-460)."""
+    rng = np.random.default_rng(9)
+    in_dim, out_dim, n = 512, 13, 5
+    w = synth.quant_blocks(rng, fmt, out_dim, in_dim, 0.02)
+    a16 = O.f16(rng.standard_normal(n * in_dim).astype(np.float32))
+    got = ora.matmul_batched(fmt, a16, w, in_dim, out_dim, n).reshape(n, out_dim)
+    a = O.f32(a16)
+    fn = (ora.lib().gho_row_dot_q4k_avx2_batched if fmt == O.FMT_Q4_K
+          else ora.lib().gho_row_dot_q6k_avx2_batched)
+    exp = np.zeros(n, np.float32)
+    for r in range(out_dim):
+        fn(a.ctypes.data, w.ctypes.data, r, in_dim, exp.ctypes.data, n)
+        assert np.array_equal(got[:, r], ora.f16(exp))
+    deq = ora.dequant(fmt, w, out_dim, in_dim).astype(np.float64)
+    for i in range(n):
+        single = O.f32(ora.matmul(fmt, a16[i * in_dim:(i + 1) * in_dim], w, in_dim, out_dim))
+        terms = deq * a[i * in_dim:(i + 1) * in_dim].astype(np.float64)[None]
+        tol = 2e-6 * np.abs(terms).sum(axis=1) + 1e-3 * np.abs(single) + 1e-30
+        assert np.all(np.abs(O.f32(got[i]) - single) <= tol)
+    # n == 1 takes the single-token kernel (q4k.rs:229-232)
+    assert np.array_equal(ora.matmul_batched(fmt, a16[:in_dim], w, in_dim, out_dim, 1),
+                          ora.matmul(fmt, a16[:in_dim], w, in_dim, out_dim))
+
+
+# ---------------------------------------------------------------- attention
+def _pattern(expr, n):
+    i = np.arange(n)
+    return eval(expr, {"i": i}).astype(np.float32)
+
+
+def test_attention_hand_computed_softmax(ora, goldens):
+    g = goldens["attention_hand_computed"]
+    q, k, v = O.f16(g["q"]), O.f16(g["k"]), O.f16(g["v"])
+    out = O.f32(ora.attention_decode(q, k, v, 2, 1, 1, g["pos"], 0, 2))
+    scale = np.float32(1.0) / np.sqrt(np.float32(2.0))
+    e1 = np.exp(-scale)
+    w0, w1 = 1.0 / (1.0 + e1), e1 / (1.0 + e1)
+    assert abs(out[0] - w0 * 2.0) < g["abs_tol"] and abs(out[1] - w1 * 4.0) < g["abs_tol"]
+
+
+def test_attention_decode_matches_serial_reference_bitwise(ora, goldens):
+    """attention/mod.rs:852-914: head_dim 4 (scalar tails), GQA group 4, bit-identical."""
+    p = goldens["attention_patterns"]
+    hd, kvh, qh, pos, layer, ctx = 4, 3, 12, 5, 0, 6
+    q = O.f16(_pattern(p["q"], qh * hd))
+    kc = O.f16(_pattern(p["k"], ctx * kvh * hd))
+    vc = O.f16(_pattern(p["v"], ctx * kvh * hd))
+    got = ora.attention_decode(q, kc, vc, hd, kvh, qh, pos, layer, ctx)
+    ser = np.empty(qh * hd, np.uint16)
+    ora.lib().gho_attention_decode_serial(ser.ctypes.data, q.ctypes.data, kc.ctypes.data,
+                                          vc.ctypes.data, hd, kvh, qh, pos, layer, ctx)
+    assert np.array_equal(got, ser)
+
+
+def test_prefill_n1_equals_decode_and_prefill_equals_rows(ora, goldens):
+    p = goldens["attention_patterns"]
+    hd, kvh, qh, layer, ctx = 128, 2, 8, 1, 40
+    rng = np.random.default_rng(2)
+    n, base = 6, 17
+    q = O.f16(rng.standard_normal(n * qh * hd).astype(np.float32))
+    kc = O.f16(rng.standard_normal((layer + 1) * ctx * kvh * hd).astype(np.float32))
+    vc = O.f16(rng.standard_normal((layer + 1) * ctx * kvh * hd).astype(np.float32))
+    pre = ora.attention_prefill(q, kc, vc, hd, kvh, qh, base, n, layer, ctx).reshape(n, -1)
+    for r in range(n):
+        dec = ora.attention_decode(q[r * qh * hd:(r + 1) * qh * hd], kc, vc, hd, kvh, qh, base + r,
+                                   layer, ctx)
+        assert np.array_equal(pre[r], dec)
+    assert p
+
+
+def test_attention_fp64_brute_force(ora):
+    rng = np.random.default_rng(4)
+    hd, kvh, qh, layer, ctx, pos = 128, 8, 32, 1, 300, 257
+    q = O.f16(rng.standard_normal(qh * hd).astype(np.float32))
+    kc = O.f16(rng.standard_normal(2 * ctx * kvh * hd).astype(np.float32))
+    vc = O.f16(rng.standard_normal(2 * ctx * kvh * hd).astype(np.float32))
+    got = O.f32(ora.attention_decode(q, kc, vc, hd, kvh, qh, pos, layer, ctx)).reshape(qh, hd)
+    K = O.f32(kc).reshape(2, ctx, kvh, hd)[layer, :pos + 1].astype(np.float64)
+    V = O.f32(vc).reshape(2, ctx, kvh, hd)[layer, :pos + 1].astype(np.float64)
+    Q = O.f32(q).reshape(qh, hd).astype(np.float64)
+    for h in range(qh):
+        s = K[:, h // 4] @ Q[h] / math.sqrt(hd)
+        w = np.exp(s - s.max())
+        want = (w / w.sum()) @ V[:, h // 4]
+        assert np.allclose(got[h], want, rtol=2e-3, atol=2e-3)
+
+
+# ---------------------------------------------------------------- glue
+def _yarn(d):
+    return O.Yarn(**d)
+
+
+def test_yarn_unit_tests(ora, goldens):
+    g = goldens["yarn_unit_tests"]
+    y = _yarn(g["yarn"])
+    lib = ora.lib()
+    for role, pos, want in g["post_scale"]:
+        assert abs(lib.gho_yarn_post_scale(C.byref(y), role, pos) - want) <= g["tol"]
+    c, s = C.c_float(), C.c_float()
+    for pos in g["unit_magnitude_key_pair1_positions"]:
+        assert lib.gho_yarn_pair(C.byref(y), 1, 1, pos, C.byref(c), C.byref(s)) == 0
+        assert abs(math.hypot(c.value, s.value) - 1.0) <= g["tol"]
+    pair, pos = g["unit_magnitude_query"]
+    assert lib.gho_yarn_pair(C.byref(y), 0, pair, pos, C.byref(c), C.byref(s)) == 0
+    assert abs(math.hypot(c.value, s.value) - 1.0) <= g["tol"]
+    bad = _yarn(dict(g["yarn"], factor=0.0))
+    assert lib.gho_yarn_pair(C.byref(bad), 0, 0, 0, C.byref(c), C.byref(s)) != 0
+    assert lib.gho_yarn_pair(C.byref(y), 1, 4, 0, C.byref(c), C.byref(s)) != 0
+
+
+def test_yarn_ramp_reduces_to_textbook_rope(ora):
+    """Pairs below the correction window extrapolate (plain RoPE angle pos·base^(-2i/d));
+    pairs above it interpolate (angle / factor); factor 1 is plain RoPE everywhere."""
+    lib = ora.lib()
+    c, s = C.c_float(), C.c_float()
+    y = O.Yarn(128, 16384, 1e6, 16.0, 32.0, 1.0, 1.0, 0.1)
+    lo, hi = C.c_float(), C.c_float()
+    lib.gho_yarn_correction_dims(C.byref(y), C.byref(lo), C.byref(hi))
+    assert 0 <= lo.value < hi.value <= 127
+    for pair in (0, int(lo.value) - 1, int(hi.value) + 1, 63):
+        if pair < 0 or pair > 63 or (lo.value <= pair <= hi.value):
+            continue
+        for pos in (1, 7, 300):
+            theta = pos * 1e6 ** (-2.0 * pair / 128)
+            if pair > hi.value:
+                theta /= 16.0
+            lib.gho_yarn_pair(C.byref(y), 1, pair, pos, C.byref(c), C.byref(s))
+            assert abs(c.value - math.cos(theta)) < 2e-5 and abs(s.value - math.sin(theta)) < 2e-5
+    plain = O.Yarn(128, 16384, 1e4, 1.0, 32.0, 1.0, 1.0, 0.1)
+    for pair in (0, 5, 40, 63):
+        theta = 3 * 1e4 ** (-2.0 * pair / 128)
+        lib.gho_yarn_pair(C.byref(plain), 0, pair, 3, C.byref(c), C.byref(s))
+        assert abs(c.value - math.cos(theta)) < 2e-6 and abs(s.value - math.sin(theta)) < 2e-6
+
+
+def test_rope_adjacent_pairs(ora, goldens):
+    g = goldens["rope_adjacent_pairs"]
+    y = _yarn(g["yarn"])
+    x = O.f16(g["input"])
+    out = O.f32(ora.rope_yarn(x, 1, 4, g["pos"], y, 1))
+    c, s = C.c_float(), C.c_float()
+    for pair in range(2):
+        ora.lib().gho_yarn_pair(C.byref(y), 1, pair, g["pos"], C.byref(c), C.byref(s))
+        a, b = g["input"][2 * pair], g["input"][2 * pair + 1]
+        assert abs(out[2 * pair] - (a * c.value - b * s.value)) <= g["tol"]
+        assert abs(out[2 * pair + 1] - (a * s.value + b * c.value)) <= g["tol"]
+    # query rows carry the post-scale bucket: position past original_context scales the pair
+    yq = _yarn(dict(g["yarn"], q_temperature_scale=2.0))
+    xs = O.f32(ora.rope_yarn(x, 1, 4, 130, yq, 0))
+    xk = O.f32(ora.rope_yarn(x, 1, 4, 130, yq, 1))
+    assert np.allclose(xs, xk * (math.log(2.0) * 2.0 + 1.0), rtol=2e-3)
+
+
+def test_silu_mul_sequential_fp16_rounding(ora, goldens):
+    g = goldens["silu_lcg"]
+
+    def lcg(n, seed):
+        st, out = seed, []
+        for _ in range(n):
+            st = (st * g["mul"] + g["add"]) & 0xFFFFFFFF
+            out.append((st >> 8) / float(1 << 24) * 4.0 - 2.0)
+        return np.float32(out)
+
+    gate, up = O.f16(lcg(g["n"], g["seeds"][0])), O.f16(lcg(g["n"], g["seeds"][1]))
+    got = ora.silu_mul(gate, up)
+    gf, uf = O.f32(gate).astype(np.float64), O.f32(up).astype(np.float64)
+    silu = (gf / (1.0 + np.exp(-gf))).astype(np.float32).astype(np.float16).astype(np.float64)
+    want = (silu * uf).astype(np.float32).astype(np.float16).view(np.uint16)
+    diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() >= 0.95
+
+
+def test_rmsnorm_formula(ora):
+    rng = np.random.default_rng(8)
+    dim, rows, eps = 4096, 3, 1e-5
+    x = rng.standard_normal(rows * dim).astype(np.float32) * 3
+    w = O.f16(1.0 + 0.05 * rng.standard_normal(dim))
+    got = O.f32(ora.rmsnorm_x(x, w, dim, eps, rows)).reshape(rows, dim)
+    xd = x.reshape(rows, dim).astype(np.float64)
+    want = xd / np.sqrt((xd ** 2).mean(axis=1, keepdims=True) + eps) * O.f32(w)[None]
+    assert np.allclose(got, want, rtol=1e-3, atol=1e-4)
+
+
+def test_argmax_topk_tiebreak(ora, goldens):
+    for vals, want in goldens["argmax"]["cases"]:
+        assert ora.argmax(vals) == want
+    g = goldens["topk"]
+    f32 = lambda pairs: [(int(i), float(np.float32(v))) for i, v in pairs]  # noqa: E731
+    assert ora.topk(g["logits"], 3) == f32(g["k3"])
+    allk = ora.topk(g["logits"], 99)
+    assert len(allk) == g["k99_len"] and allk[0] == f32([g["k99_first"]])[0]
+    assert allk[-1] == f32([g["k99_last"]])[0]
+    assert ora.argmax([float("nan"), 1.0, float("nan")]) == 1
+    assert ora.argmax([float("-inf")] * 4) == 0
+
+
+def test_kv_layout(ora, goldens):
+    g = goldens["kv_layout_f16"]
+    lib = ora.lib()
+    assert lib.gho_kv_buffer_bytes(g["block_count"], g["context"], g["kv_heads"], g["head_dim"]) == g["buffer_bytes"]
+    for layer, pos, want in g["payload_offsets"]:
+        assert lib.gho_kv_payload_offset(layer, pos, g["kv_heads"], g["head_dim"], g["context"]) == want
+
+
+# ---------------------------------------------------------------- graph
+def oracle_model(shape, seed, kv_context):
+    tensors = {}
+    for layer, tid, fmt, data in synth.model_tensors(shape, seed):
+        tensors[("g", tid) if layer == 0xFFFFFFFF else (layer, tid)] = (fmt, data)
+    y = synth.yarn_params(shape)
+    cfg = O.ModelCfg(shape.block_count, max(kv_context, 32768), shape.embedding_length,
+                     shape.feed_forward_length, shape.head_count, shape.kv_head_count,
+                     shape.head_dim, shape.head_dim, shape.vocab_size, 1e-5, O.Yarn(**y))
+    return O.Model(cfg, tensors, kv_context), tensors
+
+
+def test_graph_batched_prefill_matches_sequential_decode(ora, goldens):
+    """generation/tests.rs:716-773: batched prefill logits == sequential decode within abs 0.05."""
+    shape = synth.SHAPES["tiny"]
+    tokens = [5, 77, 1023, 4, 2000, 9]
+    seq, _ = oracle_model(shape, 21, 64)
+    for p, t in enumerate(tokens):
+        seq.token(t, p)
+    bat, _ = oracle_model(shape, 21, 64)
+    bat.prefill(tokens, 0, 4)  # two chunks: 4 + 2 rows
+    a, b = seq.logits(), bat.logits()
+    assert np.all(np.isfinite(a)) and np.abs(a).max() > 0.1
+    assert np.max(np.abs(a - b)) <= goldens["graph_batched_vs_sequential"]["abs_tol"]
+    seq.close()
+    bat.close()
