@@ -101,6 +101,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--shape", default="8b")
+    ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
+                    help="decode steps as one replayed HIP graph (default) or as direct "
+                         "stream launches of the same kernels (for kernel tracers)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -114,7 +117,8 @@ def main():
     per_block, per_token = weight_bytes(shape)
     kv_context = args.prompt + args.warmup + args.steps + 8
     hip = HipBackend(0)
-    model = HipModel(hip, synth.model_config(shape, kv_context, prefill_rows=512))
+    flags = F.MODEL_NO_GRAPH if args.launch == "stream" else 0
+    model = HipModel(hip, synth.model_config(shape, kv_context, prefill_rows=512, flags=flags))
     t0 = time.perf_counter()
     for layer, tid, fmt, data in synth.model_tensors(shape, seed=2024):
         model.load_tensor(layer, tid, fmt, data)
@@ -182,7 +186,8 @@ def main():
             "workload": f"{shape.name}-shaped Q4_K_M decoder, greedy decode bs=1 "
                         f"({shape.block_count} blocks of BASELINE configs[1]: d {d}, FFN {ffn}, "
                         f"32/8 heads x 128, Q/K/O/gate/up Q4_K, V/down Q6_K; Q6_K output "
-                        f"{shape.vocab_size}x{d}); context {args.prompt}..{pos + args.steps}",
+                        f"{shape.vocab_size}x{d}); context {args.prompt}..{pos + args.steps}; "
+                        f"{args.launch} launch",
             "weight_bytes_per_token": per_token,
             "decode_weight_roofline_frac": round(per_token * tok_s / (HBM_PEAK_GBPS * 1e9), 4),
             "q4k_gemv_c1_shape": None,

@@ -61,7 +61,11 @@ class GhModelConfig(C.Structure):
                 ("head_count", C.c_uint32), ("kv_head_count", C.c_uint32),
                 ("key_length", C.c_uint32), ("value_length", C.c_uint32),
                 ("vocab_size", C.c_uint32), ("rms_epsilon", C.c_float), ("yarn", GhYarn),
-                ("kv_context", C.c_uint32), ("prefill_rows", C.c_uint32)]
+                ("kv_context", C.c_uint32), ("prefill_rows", C.c_uint32),
+                ("flags", C.c_uint32)]
+
+
+MODEL_NO_GRAPH = 1
 
 
 P = C.c_void_p

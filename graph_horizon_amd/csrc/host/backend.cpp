@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -25,6 +26,8 @@ const KernelName kKernels[] = {
     {K_GEMV_Q4K_R1, "gh_gemv_q4k_r1"},     {K_GEMV_Q4K_R2, "gh_gemv_q4k_r2"},
     {K_GEMV_Q4K_R4, "gh_gemv_q4k_r4"},     {K_GEMV_Q6K_R1, "gh_gemv_q6k_r1"},
     {K_GEMV_Q6K_R2, "gh_gemv_q6k_r2"},     {K_GEMV_Q6K_R4, "gh_gemv_q6k_r4"},
+    {K_GEMV_MIXED_R2, "gh_gemv_mixed_r2"}, {K_GEMV_SWIGLU_R1, "gh_gemv_swiglu_r1"},
+    {K_GEMV_SWIGLU_R2, "gh_gemv_swiglu_r2"},
     {K_RMSNORM, "gh_rmsnorm_x"},           {K_ROPE, "gh_rope"},
     {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
     {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
@@ -333,6 +336,80 @@ int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, vo
     return rc;
 }
 
+// Rows per wavefront task: enough tasks to fill the machine (>= ~2 per SIMD) with as many
+// rows per task as that allows; GH_GEMV_ROWS (1, 2, 4) overrides for tuning sweeps.
+static uint32_t gemv_rows(uint64_t total_rows) {
+    static const int forced = [] {
+        const char* e = std::getenv("GH_GEMV_ROWS");
+        return e ? std::atoi(e) : 0;
+    }();
+    if (forced == 1 || forced == 2 || forced == 4) return (uint32_t)forced;
+    if (total_rows >= 16384) return 4;
+    if (total_rows >= 4096) return 2;
+    return 1;
+}
+
+int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
+            uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up) {
+    if (nseg == 0 || nseg > 3) return fail(b, GH_E_INVALID, "gemv: 1..3 segments");
+    GhGemvArgs a{};
+    const uint32_t in_dim = segs[0].w->cols;
+    bool mixed = false, rope = false, swiglu = false;
+    uint64_t total_rows = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        const gh_buf* w = segs[i].w;
+        if (!is_weight(w) || w->cols != in_dim) return fail(b, GH_E_INVALID, "gemv: segment shape");
+        mixed |= w->format != segs[0].w->format;
+        rope |= segs[i].epi == GH_EPI_ROPE || segs[i].epi == GH_EPI_ROPE_CACHE;
+        swiglu |= segs[i].epi == GH_EPI_SWIGLU;
+        total_rows += w->rows;
+    }
+    if (n > 1)
+        for (uint32_t i = 0; i < nseg; ++i)
+            if (segs[i].epi != GH_EPI_F16 && segs[i].epi != GH_EPI_F32)
+                return fail(b, GH_E_INVALID, "gemv: fused epilogues are single-token");
+    uint32_t r = gemv_rows(total_rows);
+    if (rope || mixed) r = 2;  // RoPE needs row pairs; the mixed kernel is compiled for R = 2
+    GhKernel k;
+    if (swiglu) {
+        if (nseg != 1 || !up || up->format != GH_FMT_Q4_K || segs[0].w->format != GH_FMT_Q4_K ||
+            up->rows != segs[0].w->rows || up->cols != in_dim)
+            return fail(b, GH_E_INVALID, "gemv: SwiGLU needs Q4_K gate/up of one shape");
+        r = std::min<uint32_t>(r, 2);
+        k = r == 2 ? K_GEMV_SWIGLU_R2 : K_GEMV_SWIGLU_R1;
+        a.aux = up->addr;
+    } else if (mixed) {
+        k = K_GEMV_MIXED_R2;
+    } else if (segs[0].w->format == GH_FMT_Q4_K) {
+        k = r == 4 ? K_GEMV_Q4K_R4 : r == 2 ? K_GEMV_Q4K_R2 : K_GEMV_Q4K_R1;
+    } else {
+        k = r == 4 ? K_GEMV_Q6K_R4 : r == 2 ? K_GEMV_Q6K_R2 : K_GEMV_Q6K_R1;
+    }
+    uint32_t task = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        a.seg[i].w = segs[i].w->addr;
+        a.seg[i].out = segs[i].out;
+        a.seg[i].rows = segs[i].w->rows;
+        a.seg[i].fmt = segs[i].w->format;
+        a.seg[i].epi = segs[i].epi;
+        a.seg[i].task0 = task;
+        task += ceil_div(segs[i].w->rows, r);
+    }
+    a.x = x->addr;
+    a.table = (uint64_t)b->rope.table;
+    a.post = (uint64_t)b->rope.post;
+    a.pos_ptr = (uint64_t)pos_ptr;
+    a.in_dim = in_dim;
+    a.nseg = nseg;
+    a.n = n;
+    a.base = base;
+    a.pairs = b->rope.yarn.rope_dim / 2;
+    a.head_dim = head_dim;
+    a.tasks = task;
+    if (rope && !b->rope.table) return fail(b, GH_E_STATE, "gemv: RoPE table not built");
+    return launch(b, k, ceil_div(task, 4), 1, 1, 256, &a);
+}
+
 int op_step_advance(gh_backend* b, void* scalars, void* history) {
     GhStepArgs a{(uint64_t)scalars, (uint64_t)history};
     return launch(b, K_STEP_ADVANCE, 1, 1, 1, 64, &a);
@@ -574,20 +651,8 @@ static int gemv_launch(gh_backend* b, const gh_buf* out, const gh_buf* a, const 
     if (w->cols != in_dim || w->rows != out_dim) return fail(b, GH_E_INVALID, "matmul: weight shape mismatch");
     if (!fits(a, (uint64_t)n * in_dim * 2) || !fits(out, (uint64_t)n * out_dim * (f32 ? 4 : 2)))
         return fail(b, GH_E_RANGE, "matmul: buffer too small");
-    GhGemvArgs g{};
-    g.w = w->addr;
-    g.x = a->addr;
-    g.y = out->addr;
-    g.in_dim = in_dim;
-    g.out_dim = out_dim;
-    g.n = n;
-    g.out_f32 = f32 ? 1 : 0;
-    // rows per wavefront: keep >= 2048 wavefronts in flight where the matrix allows it
-    const bool q4 = w->format == GH_FMT_Q4_K;
-    uint32_t r = out_dim >= 16384 ? 4 : (out_dim >= 8192 ? 2 : 1);
-    GhKernel k = q4 ? (r == 4 ? K_GEMV_Q4K_R4 : r == 2 ? K_GEMV_Q4K_R2 : K_GEMV_Q4K_R1)
-                    : (r == 4 ? K_GEMV_Q6K_R4 : r == 2 ? K_GEMV_Q6K_R2 : K_GEMV_Q6K_R1);
-    return launch(b, k, ceil_div(out_dim, 4 * r), 1, 1, 256, &g);
+    GemvSeg seg{w, out->addr, f32 ? (uint32_t)GH_EPI_F32 : (uint32_t)GH_EPI_F16};
+    return op_gemv(b, &seg, 1, a, n, 0, nullptr, 0, nullptr);
 }
 
 int gh_matmul(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* a,
@@ -618,8 +683,9 @@ int gh_rmsnorm_x(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf
     if (rc) return rc;
     if (dim == 0 || !fits(x, (uint64_t)rows * dim * 4) || !fits(out, (uint64_t)rows * dim * 2) || !fits(w, (uint64_t)dim * 2))
         return latch(enc, fail(b, GH_E_RANGE, "rmsnorm_x: buffer too small"));
+    if (dim % 4) return latch(enc, fail(b, GH_E_INVALID, "rmsnorm_x: dim must be a multiple of 4"));
     GhRmsnormArgs a{out->addr, x->addr, w->addr, dim, rows, eps, 0};
-    return latch(enc, launch(b, K_RMSNORM, rows, 1, 1, 256, &a));
+    return latch(enc, launch(b, K_RMSNORM, rows, 1, 1, 1024, &a));
 }
 
 int gh_rope_yarn(gh_backend* b, gh_encoder* enc, const gh_buf* x, uint32_t heads,

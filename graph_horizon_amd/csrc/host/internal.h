@@ -21,6 +21,9 @@ enum GhKernel : int {
     K_GEMV_Q6K_R1,
     K_GEMV_Q6K_R2,
     K_GEMV_Q6K_R4,
+    K_GEMV_MIXED_R2,
+    K_GEMV_SWIGLU_R1,
+    K_GEMV_SWIGLU_R2,
     K_RMSNORM,
     K_ROPE,
     K_SILU_MUL,
@@ -88,6 +91,14 @@ int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, ui
              const void* token_ptr);
 int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2);
 int op_step_advance(gh_backend* b, void* scalars, void* history);
+// Decode GEMVs with fused epilogues (n = 1). Segments are launched as one grid.
+struct GemvSeg {
+    const gh_buf* w;
+    uint64_t out;
+    uint32_t epi;
+};
+int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
+            uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up);
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
 uint32_t attention_split_len(uint32_t max_len);
 }  // namespace gh

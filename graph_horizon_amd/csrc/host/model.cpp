@@ -50,6 +50,11 @@ int alloc(gh_model* m, uint64_t bytes, gh_buf* out) {
     return rc;
 }
 
+int latch_rc(gh_encoder* enc, int rc) {
+    if (rc != GH_OK && enc && enc->latched == GH_OK) enc->latched = rc;
+    return rc;
+}
+
 int alloc_scratch(gh_model* m, uint32_t rows, Scratch* s) {
     const gh_model_config& c = m->cfg;
     const uint64_t d = c.embedding_length, ffn = c.feed_forward_length;
@@ -69,10 +74,49 @@ int alloc_scratch(gh_model* m, uint32_t rows, Scratch* s) {
     return rc;
 }
 
+// One decode layer (rows == 1) with the glue fused into the GEMV epilogues:
+//   rmsnorm → [Q, K, V GEMVs + RoPE(Q) + RoPE(K)→K cache + V→V cache] → attention →
+//   [O GEMV + residual] → rmsnorm → [gate/up GEMVs + SwiGLU] → [down GEMV + residual].
+// Same values as the op-by-op recording below: each epilogue applies the reference op to
+// the FP16-rounded projection (block.rs:17-107, mlp.rs:12-61).
+int layer_decode_fused(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li,
+                       uint32_t base, const void* pos_ptr) {
+    gh_backend* b = m->b;
+    const gh_model_config& c = m->cfg;
+    const auto& w = m->layers[li];
+    const uint32_t d = c.embedding_length;
+    const uint64_t kv_row_k = (uint64_t)c.kv_head_count * c.key_length;
+    const uint64_t kv_row_v = (uint64_t)c.kv_head_count * c.value_length;
+    const uint64_t kbase = m->kv.k.addr + (uint64_t)li * m->kv.context * kv_row_k * 2;
+    const uint64_t vbase = m->kv.v.addr + (uint64_t)li * m->kv.context * kv_row_v * 2;
+    int rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_ATTN_NORM], d, c.rms_epsilon, 1);
+    const GemvSeg qkv[3] = {{&w[GH_T_ATTN_Q], s.q.addr, GH_EPI_ROPE},
+                            {&w[GH_T_ATTN_K], kbase, GH_EPI_ROPE_CACHE},
+                            {&w[GH_T_ATTN_V], vbase, GH_EPI_CACHE}};
+    if (!rc) rc = op_gemv(b, qkv, 3, &s.normed, 1, base, pos_ptr, c.key_length, nullptr);
+    const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base;
+    if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, 1, li, pos_ptr, max_pos);
+    const GemvSeg o{&w[GH_T_ATTN_OUTPUT], s.x.addr, GH_EPI_RESID};
+    if (!rc) rc = op_gemv(b, &o, 1, &s.attn, 1, 0, nullptr, 0, nullptr);
+    if (!rc) rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_FFN_NORM], d, c.rms_epsilon, 1);
+    const GemvSeg gu{&w[GH_T_FFN_GATE], s.act.addr, GH_EPI_SWIGLU};
+    if (!rc) rc = op_gemv(b, &gu, 1, &s.normed, 1, 0, nullptr, 0, &w[GH_T_FFN_UP]);
+    const GemvSeg dn{&w[GH_T_FFN_DOWN], s.x.addr, GH_EPI_RESID};
+    if (!rc) rc = op_gemv(b, &dn, 1, &s.act, 1, 0, nullptr, 0, nullptr);
+    return latch_rc(enc, rc);
+}
+
+bool fusable(const gh_model* m, uint32_t li) {
+    const auto& w = m->layers[li];
+    return w[GH_T_FFN_GATE].format == GH_FMT_Q4_K && w[GH_T_FFN_UP].format == GH_FMT_Q4_K &&
+           m->cfg.head_count * m->cfg.value_length == w[GH_T_ATTN_OUTPUT].cols;
+}
+
 // One transformer layer over `rows` packed rows at absolute positions base + r
 // (+ *pos_ptr when the position lives on the device).
 int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t base,
           uint32_t rows, const void* pos_ptr) {
+    if (rows == 1 && fusable(m, li)) return layer_decode_fused(m, enc, s, li, base, pos_ptr);
     gh_backend* b = m->b;
     const gh_model_config& c = m->cfg;
     const auto& w = m->layers[li];
@@ -106,8 +150,7 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
     if (!rc) rc = gh_silu_mul(b, enc, &s.act, &s.gate, &s.up, ffn * rows);
     if (!rc) rc = gh_matmul_batched(b, enc, &s.ffn_out, &s.act, &w[GH_T_FFN_DOWN], ffn, d, rows);
     if (!rc) rc = gh_residual_add(b, enc, &s.x, &s.ffn_out, d * rows);
-    (void)vw;
-    return rc;
+    return latch_rc(enc, rc);
 }
 
 // tail::record_buffers (tail.rs:22-59): output_norm then FP32 logits (dedicated or tied).
@@ -315,6 +358,21 @@ int gh_model_decode_greedy(gh_model* m, uint32_t token, uint32_t pos, uint32_t s
     if (steps == 0) return GH_OK;
     gh_backend* b = m->b;
     int rc = GH_OK;
+    const uint32_t init[4] = {pos, token, 0, 0};
+    if (c.flags & GH_MODEL_NO_GRAPH) {
+        rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
+        gh_encoder* enc = nullptr;
+        if (!rc) rc = gh_begin(b, &enc);
+        for (uint32_t i = 0; i < steps && !rc; ++i) rc = record_step(m, enc);
+        if (enc) {
+            int rs = gh_submit(b, enc);
+            rc = rc ? rc : rs;
+        }
+        if (!rc) rc = gh_download(b, &m->history, (uint64_t)pos * 4, tokens_out, (uint64_t)steps * 4);
+        m->last_rows = 1;
+        m->last_prefill = false;
+        return rc;
+    }
     if (m->step && m->step_gen != b->gen) {  // workspace or rope table moved: capture again
         (void)hipGraphExecDestroy(m->step);
         (void)hipGraphDestroy(m->step_graph);
@@ -341,7 +399,6 @@ int gh_model_decode_greedy(gh_model* m, uint32_t token, uint32_t pos, uint32_t s
         b->enc_open = false;
         if (rc) return rc;
     }
-    const uint32_t init[4] = {pos, token, 0, 0};
     rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
     for (uint32_t i = 0; i < steps && !rc; ++i)
         rc = hip_check(b, hipGraphLaunch(m->step, b->stream), "hipGraphLaunch");

@@ -39,6 +39,33 @@ __device__ __forceinline__ float gh_wave_max(float v) {
     return v;
 }
 
+#define GH_GLOBAL __attribute__((address_space(1)))
+
+// Global-address-space views of a device address (global_load/global_store, not flat).
+template <class T>
+__device__ __forceinline__ const GH_GLOBAL T* gh_gp(uint64_t a) {
+    return (const GH_GLOBAL T*)a;
+}
+template <class T>
+__device__ __forceinline__ GH_GLOBAL T* gh_gpw(uint64_t a) {
+    return (GH_GLOBAL T*)a;
+}
+
+#define GH_DPP(v, ctrl, rmask) \
+    __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, rmask, 0xF, false))
+
+// Sum across a wavefront with DPP (quad perms, half-row/row mirrors, row broadcasts); the
+// total lands in lanes 48..63 (read it from lane 63).
+__device__ __forceinline__ float gh_wave_sum63(float v) {
+    v += GH_DPP(v, 0xB1, 0xF);   // quad_perm [1,0,3,2]
+    v += GH_DPP(v, 0x4E, 0xF);   // quad_perm [2,3,0,1]
+    v += GH_DPP(v, 0x141, 0xF);  // row_half_mirror
+    v += GH_DPP(v, 0x140, 0xF);  // row_mirror
+    v += GH_DPP(v, 0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+    v += GH_DPP(v, 0x143, 0xC);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
 // Byte `i` (runtime, 0..15) of a 16-byte register block.
 __device__ __forceinline__ uint32_t gh_byte(const uint4& v, uint32_t i) {
     uint32_t w = (i < 4) ? v.x : (i < 8) ? v.y : (i < 12) ? v.z : v.w;

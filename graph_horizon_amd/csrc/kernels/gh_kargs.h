@@ -38,14 +38,41 @@ struct GhDequantArgs {
     uint32_t rows;
 };
 
+// Decode GEMV epilogues (what happens to an output row's FP32 dot product).
+#define GH_EPI_F16 0      // out[row] = f16(acc)                         (matmul)
+#define GH_EPI_F32 1      // out[row] = acc                              (logits)
+#define GH_EPI_RESID 2    // out[row] += f32(f16(acc)), out is the FP32 residual (matmul+residual_add)
+#define GH_EPI_ROPE 3     // query rows (2i, 2i+1): f16, rotated at pos, x post[pos], f16 at out[row]
+#define GH_EPI_CACHE 4    // f16(acc) at out[pos*rows + row] (the V cache row of this position)
+#define GH_EPI_SWIGLU 5   // out[row] = f16(f16(silu(f16(gate))) * f16(up)); up weights in `aux`
+#define GH_EPI_ROPE_CACHE 6  // key rows: as GH_EPI_ROPE without post-scale, at out[pos*rows+row]
+
+// One matrix of a (possibly fused) GEMV launch. Wavefront tasks [task0, next task0) of the
+// launch belong to it; each task covers R consecutive rows.
+struct GhGemvSeg {
+    uint64_t w;      // device layout base
+    uint64_t out;    // destination base (meaning set by epi)
+    uint32_t rows;   // out_dim
+    uint32_t fmt;    // 12 = Q4_K, 14 = Q6_K
+    uint32_t epi;    // GH_EPI_*
+    uint32_t task0;  // first task index
+};
+
 struct GhGemvArgs {
-    uint64_t w;       // device layout base
-    uint64_t x;       // f16 activations, token-major [n][in_dim]
-    uint64_t y;       // output, token-major [n][out_dim]: f16 or f32
+    GhGemvSeg seg[3];
+    uint64_t x;        // f16 activations, token-major [n][in_dim]
+    uint64_t table;    // GH_EPI_ROPE: float2 (cos, sin) [positions][pairs]
+    uint64_t post;     // GH_EPI_ROPE: f32 post-scale [positions] (0 = 1.0, keys)
+    uint64_t pos_ptr;  // optional u32* position on the device (added to base)
+    uint64_t aux;      // GH_EPI_SWIGLU: the up matrix (same shape/format as seg[0])
     uint32_t in_dim;
-    uint32_t out_dim;
-    uint32_t n;       // tokens (1 = decode GEMV)
-    uint32_t out_f32; // 1: FP32 output (logits), 0: FP16 output (matmul)
+    uint32_t nseg;
+    uint32_t n;        // tokens (> 1 only with GH_EPI_F16 / GH_EPI_F32)
+    uint32_t base;     // position (GH_EPI_ROPE / GH_EPI_CACHE)
+    uint32_t pairs;    // rope pairs per head (rope_dim / 2)
+    uint32_t head_dim;
+    uint32_t tasks;    // total tasks of the launch
+    uint32_t pad;
 };
 
 struct GhRmsnormArgs {

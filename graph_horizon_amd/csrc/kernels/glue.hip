@@ -1,25 +1,38 @@
 // Decode/prefill glue: RMSNorm, YaRN RoPE, SiLU·up, residual add, KV append, argmax.
 #include "gh_common.h"
 
-// rmsnorm_x (backend/cpu/kernels/elementwise/normalization.rs:12-40): one workgroup per row,
-// Σx² reduced in FP32, inverse = 1/sqrt(Σx²/dim + eps), out = f16((x*inverse)*w).
-GH_KERNEL __launch_bounds__(256) void gh_rmsnorm_x(GhRmsnormArgs a) {
+// rmsnorm_x (backend/cpu/kernels/elementwise/normalization.rs:12-40): one 1024-thread
+// workgroup per row, 4 consecutive FP32 values per thread per step, Σx² reduced with DPP and
+// LDS, inverse = 1/sqrt(Σx²/dim + eps), out = f16((x*inverse)*w). dim % 4 == 0.
+GH_KERNEL __launch_bounds__(1024) void gh_rmsnorm_x(GhRmsnormArgs a) {
 #pragma clang fp contract(off)
     const uint32_t row = blockIdx.x;
     if (row >= a.rows) return;
-    const float* x = (const float*)a.x + (size_t)row * a.dim;
-    const uint16_t* w = (const uint16_t*)a.w;
-    uint16_t* out = (uint16_t*)a.out + (size_t)row * a.dim;
-    __shared__ float partial[4];
+    const GH_GLOBAL float4* x = gh_gp<float4>(a.x + (uint64_t)row * a.dim * 4);
+    const GH_GLOBAL uint2* w = gh_gp<uint2>(a.w);
+    GH_GLOBAL uint2* out = gh_gpw<uint2>(a.out + (uint64_t)row * a.dim * 2);
+    __shared__ float partial[16];
+    const uint32_t n4 = a.dim >> 2;
     float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < a.dim; i += blockDim.x) s += x[i] * x[i];
-    s = gh_wave_sum(s);
-    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = s;
+    for (uint32_t i = threadIdx.x; i < n4; i += blockDim.x) {
+        const float4 v = x[i];
+        s += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+    s = gh_wave_sum63(s);
+    if ((threadIdx.x & 63) == 63) partial[threadIdx.x >> 6] = s;
     __syncthreads();
-    const float sum = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < (blockDim.x >> 6); ++i) sum += partial[i];
     const float inverse = 1.0f / __builtin_sqrtf(sum / (float)a.dim + a.eps);
-    for (uint32_t i = threadIdx.x; i < a.dim; i += blockDim.x)
-        out[i] = gh_f2h(x[i] * inverse * gh_h2f(w[i]));
+    for (uint32_t i = threadIdx.x; i < n4; i += blockDim.x) {
+        const float4 v = x[i];
+        const uint2 wv = w[i];
+        const uint32_t o0 = gh_f2h(v.x * inverse * gh_h2f(wv.x & 0xFFFFu));
+        const uint32_t o1 = gh_f2h(v.y * inverse * gh_h2f(wv.x >> 16));
+        const uint32_t o2 = gh_f2h(v.z * inverse * gh_h2f(wv.y & 0xFFFFu));
+        const uint32_t o3 = gh_f2h(v.w * inverse * gh_h2f(wv.y >> 16));
+        out[i] = make_uint2(o0 | (o1 << 16), o2 | (o3 << 16));
+    }
 }
 
 // rope_yarn (cpu/kernels/elementwise/rope.rs:14-39): adjacent pairs rotated by the per

@@ -102,14 +102,16 @@ def yarn_params(shape: Shape):
                 q_temperature_scale=0.1)
 
 
-def model_config(shape: Shape, kv_context: int, prefill_rows: int = 512) -> F.GhModelConfig:
+def model_config(shape: Shape, kv_context: int, prefill_rows: int = 512,
+                 flags: int = 0) -> F.GhModelConfig:
     y = yarn_params(shape)
     return F.GhModelConfig(
         block_count=shape.block_count, context_length=max(kv_context, 32768),
         embedding_length=shape.embedding_length, feed_forward_length=shape.feed_forward_length,
         head_count=shape.head_count, kv_head_count=shape.kv_head_count,
         key_length=shape.head_dim, value_length=shape.head_dim, vocab_size=shape.vocab_size,
-        rms_epsilon=1e-5, yarn=F.GhYarn(**y), kv_context=kv_context, prefill_rows=prefill_rows)
+        rms_epsilon=1e-5, yarn=F.GhYarn(**y), kv_context=kv_context, prefill_rows=prefill_rows,
+        flags=flags)
 
 
 def tensor_dims(shape: Shape, tensor: int):

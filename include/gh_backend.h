@@ -210,7 +210,13 @@ typedef struct gh_model_config {
     gh_yarn yarn;
     uint32_t kv_context;   /* request KV capacity in tokens (kv_cache::alloc_shape) */
     uint32_t prefill_rows; /* prefill chunk row capacity (graph/prefill/mod.rs:20-22) */
+    uint32_t flags;        /* GH_MODEL_* bits */
 } gh_model_config;
+
+/* gh_model_decode_greedy launches each step's kernels directly on the stream instead of
+ * replaying one captured HIP graph (same kernels, same device-resident token/position);
+ * for tools that cannot trace kernels inside graphs. */
+#define GH_MODEL_NO_GRAPH 1u
 
 /* Tensor ids for gh_model_load_tensor. Per-layer ids follow backend/source.rs's canonical
  * order; global ids use layer = UINT32_MAX. */

@@ -1,0 +1,72 @@
+"""forward::token restated in Python over the C ABI, op by op (test helper).
+
+This is the engine's own structure — the graph recorders generic over `Backend`
+(family/mistral/graph/forward.rs:68-83, block.rs:17-107, mlp.rs:12-61, tail.rs:22-59) —
+driving the gh_* entry points one trait method at a time. The fused driver (gh_model_*) must
+produce the same bits: its epilogues apply the same ops to the same FP16-rounded values.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from graph_horizon_amd import Yarn, synth
+from graph_horizon_amd import _ffi as F
+
+
+class AbiGraph:
+    def __init__(self, hip, shape, seed, kv_context):
+        self.hip, self.shape = hip, shape
+        self.w = {}
+        for layer, tid, fmt, data in synth.model_tensors(shape, seed):
+            if fmt == F.FMT_F32:
+                self.w[(layer, tid)] = hip.load_weight(F.FMT_F32, data, data.size, 1)
+            else:
+                ind, outd = ((shape.embedding_length, shape.vocab_size) if layer == F.NO_LAYER
+                             else synth.tensor_dims(shape, tid))
+                self.w[(layer, tid)] = hip.load_weight(fmt, data, ind, outd)
+        d, ffn = shape.embedding_length, shape.feed_forward_length
+        qw, kw = shape.head_count * shape.head_dim, shape.kv_head_count * shape.head_dim
+        a = hip.alloc_buffer
+        self.x, self.normed = a(d * 4), a(d * 2)
+        self.q, self.k, self.v, self.attn = a(qw * 2), a(kw * 2), a(kw * 2), a(qw * 2)
+        self.proj, self.gate, self.up, self.act = a(d * 2), a(ffn * 2), a(ffn * 2), a(ffn * 2)
+        self.ffn_out, self.logits = a(d * 2), a(shape.vocab_size * 4)
+        n = shape.block_count * kv_context * kw
+        self.kv = F.GhKv(a(n * 2), a(n * 2), F.KV_F16, shape.block_count, kv_context,
+                         shape.kv_head_count, shape.head_dim, shape.head_dim)
+        self.kv_context = kv_context
+        self.yarn = Yarn(**synth.yarn_params(shape))
+
+    def token(self, tok, pos):
+        h, s = self.hip, self.shape
+        d, ffn = s.embedding_length, s.feed_forward_length
+        qw, kw = s.head_count * s.head_dim, s.kv_head_count * s.head_dim
+        eps = 1e-5
+        h.begin()
+        h.embed(self.x, self.w[(F.NO_LAYER, F.T_TOKEN_EMBD)], tok, d)
+        for li in range(s.block_count):
+            w = lambda t: self.w[(li, t)]  # noqa: E731
+            h.rmsnorm_x(self.normed, self.x, w(F.T_ATTN_NORM), d, eps, 1)
+            h.matmul(self.q, self.normed, w(F.T_ATTN_Q), d, qw)
+            h.matmul(self.k, self.normed, w(F.T_ATTN_K), d, kw)
+            h.matmul(self.v, self.normed, w(F.T_ATTN_V), d, kw)
+            h.rope_yarn(self.q, s.head_count, s.head_dim, pos, self.yarn, F.ROPE_QUERY)
+            h.rope_yarn(self.k, s.kv_head_count, s.head_dim, pos, self.yarn, F.ROPE_KEY)
+            off = ((li * self.kv_context + pos) * kw) * 2
+            h.kv_write(self.kv, self.k, self.v, off, off, s.kv_head_count)
+            h.attention_decode(self.attn, self.q, self.kv, s.head_count, pos, li)
+            h.matmul(self.proj, self.attn, w(F.T_ATTN_OUTPUT), qw, d)
+            h.residual_add(self.x, self.proj, d)
+            h.rmsnorm_x(self.normed, self.x, w(F.T_FFN_NORM), d, eps, 1)
+            h.matmul(self.gate, self.normed, w(F.T_FFN_GATE), d, ffn)
+            h.matmul(self.up, self.normed, w(F.T_FFN_UP), d, ffn)
+            h.silu_mul(self.act, self.gate, self.up, ffn)
+            h.matmul(self.ffn_out, self.act, w(F.T_FFN_DOWN), ffn, d)
+            h.residual_add(self.x, self.ffn_out, d)
+        h.rmsnorm_x(self.normed, self.x, self.w[(F.NO_LAYER, F.T_OUTPUT_NORM)], d, eps, 1)
+        h.logits(self.logits, self.normed, self.w[(F.NO_LAYER, F.T_OUTPUT)], d, s.vocab_size)
+        h.submit()
+        return h.read_logits(self.logits, s.vocab_size)
+
+    def read_x(self):
+        return self.hip.download(self.x, np.float32, self.shape.embedding_length)

@@ -418,3 +418,46 @@ def test_model_rejects_bad_inputs(hip):
     with pytest.raises(GhError):
         gm.prefill([], 0)
     gm.close()
+
+
+def test_greedy_decode_stream_launch_equals_graph(hip):
+    """GH_MODEL_NO_GRAPH launches the same step kernels directly: identical tokens."""
+    from graph_horizon_amd import HipModel
+
+    shape = synth.SHAPES["tiny"]
+    outs = []
+    for flags in (0, F.MODEL_NO_GRAPH):
+        gm = HipModel(hip, synth.model_config(shape, 64, 16, flags=flags))
+        for layer, tid, fmt, data in synth.model_tensors(shape, 35):
+            gm.load_tensor(layer, tid, fmt, data)
+        gm.prefill([4, 5, 6], 0)
+        outs.append(gm.decode_greedy(9, 3, 20))
+        gm.close()
+    assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("shape_name", ["tiny", "small"])
+def test_fused_decode_is_bit_identical_to_op_by_op(hip, shape_name):
+    """The fused driver (RoPE + KV write in the QKV epilogue, residual in O/down, SwiGLU in
+    gate/up) leaves the same bits as recording every trait op separately."""
+    from graph_horizon_amd import HipModel
+    from graph_over_abi import AbiGraph
+
+    shape = synth.SHAPES[shape_name]
+    ref = AbiGraph(hip, shape, 41, 64)
+    gm = HipModel(hip, synth.model_config(shape, 64, 16))
+    for layer, tid, fmt, data in synth.model_tensors(shape, 41):
+        gm.load_tensor(layer, tid, fmt, data)
+    for pos, tok in enumerate([11, 700, 3, 1999, 56]):
+        want = ref.token(tok, pos)
+        gm.token(tok, pos)
+        got = gm.read_logits()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), pos
+        assert np.array_equal(gm.read_x().view(np.uint32), ref.read_x().view(np.uint32)), pos
+    kv = gm.kv()
+    n = shape.block_count * 64 * shape.kv_head_count * shape.head_dim
+    for role in ("k", "v"):  # positions 0..4 of every layer were written
+        a = hip.download(getattr(kv, role), np.uint16, n).reshape(shape.block_count, 64, -1)
+        b = hip.download(getattr(ref.kv, role), np.uint16, n).reshape(shape.block_count, 64, -1)
+        assert np.array_equal(a[:, :5], b[:, :5]), role
+    gm.close()
