@@ -31,9 +31,9 @@ const KernelName kKernels[] = {
     {K_RMSNORM, "gh_rmsnorm_x"},           {K_ROPE, "gh_rope"},
     {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
     {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
-    {K_ARGMAX_FINAL, "gh_argmax_final"},   {K_ATTN_SPLIT_G1, "gh_attn_split_g1"},
-    {K_ATTN_SPLIT_G2, "gh_attn_split_g2"}, {K_ATTN_SPLIT_G4, "gh_attn_split_g4"},
-    {K_ATTN_SPLIT_G8, "gh_attn_split_g8"}, {K_ATTN_MERGE, "gh_attn_merge"},
+    {K_ARGMAX_FINAL, "gh_argmax_final"},   {K_ATTN_G1, "gh_attn_g1"},
+    {K_ATTN_G2, "gh_attn_g2"},             {K_ATTN_G4, "gh_attn_g4"},
+    {K_ATTN_G8, "gh_attn_g8"},
     {K_STEP_ADVANCE, "gh_step_advance"},
 };
 
@@ -144,11 +144,11 @@ int hip_check(gh_backend* b, hipError_t e, const char* what) {
 }
 
 int launch(gh_backend* b, GhKernel k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
-           const void* args) {
+           const void* args, uint32_t shmem) {
     if (gx == 0 || gy == 0 || gz == 0) return GH_OK;
     void* params[] = {const_cast<void*>(args)};
-    return hip_check(b, hipModuleLaunchKernel(b->fn[k], gx, gy, gz, bx, 1, 1, 0, b->stream, params,
-                                              nullptr),
+    return hip_check(b, hipModuleLaunchKernel(b->fn[k], gx, gy, gz, bx, 1, 1, shmem, b->stream,
+                                              params, nullptr),
                      "hipModuleLaunchKernel");
 }
 
@@ -242,15 +242,31 @@ int op_kv_write(gh_backend* b, const gh_kv* kv, const gh_buf* k, const gh_buf* v
     return launch(b, K_KV_WRITE, ceil_div(std::max(a.k_count, a.v_count), 256), 1, 1, 256, &a);
 }
 
-uint32_t attention_split_len(uint32_t max_len) {
-    uint32_t sl = ceil_div(max_len, 512);
-    sl = ((sl + 63) / 64) * 64;
-    return std::min<uint32_t>(std::max<uint32_t>(sl, 64), 256);
+// Workgroups per (row, kv head): one per 64-position chunk up to 32; longer contexts loop.
+uint32_t attention_splits(uint32_t max_len) {
+    return std::min<uint32_t>(ceil_div(max_len, 64), 32);
 }
 
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits) {
     size_t n = (size_t)rows * q_heads * splits;
     return n * 4 * 2 + n * 128 * 4 + 1024;
+}
+
+int ensure_counters(gh_backend* b, size_t slots) {
+    if (b->counter_slots >= slots) return GH_OK;
+    if (b->capturing) return fail(b, GH_E_STATE, "counter growth during graph capture");
+    slots = std::max<size_t>(slots, 4096);
+    int rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    if (b->counters) (void)hipFree(b->counters);
+    b->counters = nullptr;
+    b->counter_slots = 0;
+    rc = hip_check(b, hipMalloc(&b->counters, slots * 4), "hipMalloc(counters)");
+    if (!rc) rc = hip_check(b, hipMemset(b->counters, 0, slots * 4), "hipMemset(counters)");
+    if (rc) return rc;
+    b->counter_slots = slots;
+    ++b->gen;
+    return GH_OK;
 }
 
 // Causal GQA attention for `rows` query rows at positions base + r (+ *pos_ptr);
@@ -261,19 +277,19 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
     const uint32_t group = q_heads / kv->kv_heads;
     GhKernel k;
     switch (group) {
-        case 1: k = K_ATTN_SPLIT_G1; break;
-        case 2: k = K_ATTN_SPLIT_G2; break;
-        case 4: k = K_ATTN_SPLIT_G4; break;
-        case 8: k = K_ATTN_SPLIT_G8; break;
+        case 1: k = K_ATTN_G1; break;
+        case 2: k = K_ATTN_G2; break;
+        case 4: k = K_ATTN_G4; break;
+        case 8: k = K_ATTN_G8; break;
         default: return fail(b, GH_E_UNSUPPORTED, "attention: GQA group must be 1, 2, 4 or 8");
     }
-    const uint32_t split_len = attention_split_len(max_pos + 1);
-    const uint32_t splits = ceil_div((uint64_t)max_pos + 1, split_len);
-    // bound the partials: process rows in groups that fit a 256 MiB workspace
+    const uint32_t splits = attention_splits(max_pos + 1);
+    // bound the partials: rows in groups that fit a 256 MiB workspace
     const size_t per_row = attention_workspace(1, q_heads, splits);
     uint32_t group_rows = (uint32_t)std::max<size_t>(1, ((size_t)256 << 20) / per_row);
     group_rows = std::min(group_rows, rows);
     int rc = ensure_workspace(b, attention_workspace(group_rows, q_heads, splits));
+    if (!rc) rc = ensure_counters(b, (size_t)group_rows * kv->kv_heads);
     if (rc) return rc;
     char* ws = (char*)b->ws + kArgmaxBytes;
     for (uint32_t r0 = 0; r0 < rows; r0 += group_rows) {
@@ -288,6 +304,7 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.part_l = (uint64_t)(ws + n * 4);
         a.part_acc = (uint64_t)(ws + n * 8);
         a.pos_ptr = (uint64_t)pos_ptr;
+        a.counters = (uint64_t)b->counters;
         a.key_dim = kv->head_dim;
         a.value_dim = kv->value_dim;
         a.kv_heads = kv->kv_heads;
@@ -297,10 +314,8 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.base = base + r0;
         a.rows = nr;
         a.splits = splits;
-        a.split_len = split_len;
         a.scale = 1.0f / std::sqrt((float)kv->head_dim);
-        rc = launch(b, k, kv->kv_heads, splits, nr, 256, &a);
-        if (!rc) rc = launch(b, K_ATTN_MERGE, q_heads, nr, 1, 128, &a);
+        rc = launch(b, k, splits, kv->kv_heads, nr, 256, &a);
         if (rc) return rc;
     }
     return GH_OK;
@@ -407,7 +422,15 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     a.head_dim = head_dim;
     a.tasks = task;
     if (rope && !b->rope.table) return fail(b, GH_E_STATE, "gemv: RoPE table not built");
-    return launch(b, k, ceil_div(task, 4), 1, 1, 256, &a);
+    if (in_dim / 64 > 256) return fail(b, GH_E_UNSUPPORTED, "gemv: in_dim above 16384");
+    // x staged once per workgroup in LDS (144 B per 64-weight unit; both layouts if mixed);
+    // the persistent grid loops its waves over the tasks.
+    const uint32_t shmem = (in_dim / 64) * 144 * (mixed ? 2 : 1);
+    static const uint32_t max_wg = [] {
+        const char* e = std::getenv("GH_GEMV_MAX_WG");
+        return e ? (uint32_t)std::atoi(e) : 1024u;
+    }();
+    return launch(b, k, std::min<uint32_t>(ceil_div(task, 4), max_wg), 1, 1, 256, &a, shmem);
 }
 
 int op_step_advance(gh_backend* b, void* scalars, void* history) {
@@ -469,6 +492,7 @@ void gh_destroy(gh_backend* b) {
     if (!b) return;
     if (b->stream) (void)hipStreamSynchronize(b->stream);
     if (b->ws) (void)hipFree(b->ws);
+    if (b->counters) (void)hipFree(b->counters);
     if (b->rope.table) (void)hipFree(b->rope.table);
     if (b->rope.post) (void)hipFree(b->rope.post);
     for (hipModule_t m : b->modules) (void)hipModuleUnload(m);

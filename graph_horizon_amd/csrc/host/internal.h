@@ -31,11 +31,10 @@ enum GhKernel : int {
     K_KV_WRITE,
     K_ARGMAX_PARTIAL,
     K_ARGMAX_FINAL,
-    K_ATTN_SPLIT_G1,
-    K_ATTN_SPLIT_G2,
-    K_ATTN_SPLIT_G4,
-    K_ATTN_SPLIT_G8,
-    K_ATTN_MERGE,
+    K_ATTN_G1,
+    K_ATTN_G2,
+    K_ATTN_G4,
+    K_ATTN_G8,
     K_STEP_ADVANCE,
     K_COUNT
 };
@@ -67,6 +66,8 @@ struct gh_backend {
     // growable device workspace (attention partials, argmax partials)
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    void* counters = nullptr;  // attention merge counters, zero between launches
+    size_t counter_slots = 0;
     GhRopeTable rope;
     uint64_t gen = 0;  // bumped whenever the workspace or rope table moves (captured graphs hold them)
 };
@@ -75,7 +76,7 @@ namespace gh {
 int fail(gh_backend* b, int code, const std::string& msg);
 int hip_check(gh_backend* b, hipError_t e, const char* what);
 int launch(gh_backend* b, GhKernel k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
-           const void* args);
+           const void* args, uint32_t shmem = 0);
 int ensure_workspace(gh_backend* b, size_t bytes);
 int ensure_rope(gh_backend* b, const gh_yarn* y, uint32_t positions);
 bool yarn_valid(const gh_yarn* y);
@@ -100,7 +101,8 @@ struct GemvSeg {
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
             uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up);
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
-uint32_t attention_split_len(uint32_t max_len);
+uint32_t attention_splits(uint32_t max_len);
+int ensure_counters(gh_backend* b, size_t slots);
 }  // namespace gh
 
 #endif

@@ -16,45 +16,78 @@
 // FP32 accumulation; the result differs from the reference's AVX2 loop only by the rounding of
 // a re-associated FP32 sum (checked to 1e-3 relative by the parity tests). The wave reduction
 // is a DPP tree (gh_wave_sum63); row results land in lane 63, which runs the epilogue.
+#include <type_traits>
+
 #include "gh_common.h"
 
 namespace {
 
 constexpr uint32_t kQ4K = 12, kQ6K = 14;
 
-// Activations of one Q4_K unit: x[0..63] (sub-block 2g then 2g+1) as FP16 pairs matching the
-// quant dwords: for quant dword k (weights 4k..4k+3 of a 32-weight sub-block)
-// p02[k] = (x[4k], x[4k+2]), p13[k] = (x[4k+1], x[4k+3]).
-struct XQ4 {
-    uint32_t lo02[8], lo13[8], hi02[8], hi13[8];
-    float bias_lo, bias_hi, sum_lo, sum_hi;
+// Bit-manipulation constants held in registers: gfx9 VOP3 cannot encode a literal, so with the
+// masks in VGPRs and the 1024.0 pair in an SGPR each FP16 pair is one v_and_or_b32.
+struct Masks {
+    uint32_t lo4, hi4, lo6, bias;
 };
 
-__device__ __forceinline__ void pairs32(const uint4 (&v)[4], uint32_t p02[8], uint32_t p13[8],
-                                        float& sum) {
+__device__ __forceinline__ Masks make_masks() {
+    Masks m{0x000F000Fu, 0x00F000F0u, 0x003F003Fu, 0x64006400u};
+    asm volatile("" : "+v"(m.lo4), "+v"(m.hi4), "+v"(m.lo6));
+    asm volatile("" : "+s"(m.bias));
+    return m;
+}
+
+// x staged in LDS once per workgroup, as FP16 pairs in the order the quant dwords produce them.
+// Unit u's 8 uint4 of pairs sit at xs[k * units + u] (k = 0..7: conflict-free b128 reads);
+// its activation sums at sums[u].
+//   Q4_K unit (x[256b + 64g .. +64)): k = 0,1: lo02, 2,3: lo13, 4,5: hi02, 6,7: hi13 where
+//     for quant dword j of a 32-weight sub-block, p02[j] = (x[4j], x[4j+2]),
+//     p13[j] = (x[4j+1], x[4j+3]); sums = (Σ lo half, Σ hi half).
+//   Q6_K unit (quarter q: x[256b + 128s + 32q + 16h .. +16)): k = q: p02 of quarter q,
+//     k = 4 + q: p13 of quarter q; sums = Σ of each quarter.
+__device__ __forceinline__ void pair16(const uint4& a, const uint4& b, uint4& p02, uint4& p13,
+                                       float& sum) {
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t e[4], o[4];
     float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint4& q = v[k >> 1];
-        const uint32_t a = (k & 1) ? q.z : q.x, b = (k & 1) ? q.w : q.y;
-        p02[k] = (a & 0xFFFFu) | (b << 16);
-        p13[k] = (a >> 16) | (b & 0xFFFF0000u);
-        s += (gh_h2f(a & 0xFFFFu) + gh_h2f(a >> 16)) + (gh_h2f(b & 0xFFFFu) + gh_h2f(b >> 16));
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = w[2 * j], hi = w[2 * j + 1];
+        e[j] = (lo & 0xFFFFu) | (hi << 16);
+        o[j] = (lo >> 16) | (hi & 0xFFFF0000u);
+        s += (gh_h2f(lo & 0xFFFFu) + gh_h2f(lo >> 16)) + (gh_h2f(hi & 0xFFFFu) + gh_h2f(hi >> 16));
     }
+    p02 = make_uint4(e[0], e[1], e[2], e[3]);
+    p13 = make_uint4(o[0], o[1], o[2], o[3]);
     sum = s;
 }
 
-__device__ __forceinline__ void load_x_q4(const uint16_t* x, uint32_t b, uint32_t g, XQ4& o) {
-    const GH_GLOBAL uint4* p = gh_gp<uint4>((uint64_t)(x + (size_t)b * 256 + g * 64));
-    uint4 lo[4], hi[4];
+template <uint32_t FMT>
+__device__ __forceinline__ void stage_x(const uint16_t* x, uint32_t units, uint4* xs, float4* sums) {
+    for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
+        const GH_GLOBAL uint4* p;
+        if constexpr (FMT == kQ4K) {
+            p = gh_gp<uint4>((uint64_t)(x + (size_t)(u >> 2) * 256 + (u & 3u) * 64));
+            uint4 v[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lo[i] = p[i];
+            for (int i = 0; i < 8; ++i) v[i] = p[i];
+            float s[4];
+            pair16(v[0], v[1], xs[0 * units + u], xs[2 * units + u], s[0]);
+            pair16(v[2], v[3], xs[1 * units + u], xs[3 * units + u], s[1]);
+            pair16(v[4], v[5], xs[4 * units + u], xs[6 * units + u], s[2]);
+            pair16(v[6], v[7], xs[5 * units + u], xs[7 * units + u], s[3]);
+            sums[u] = make_float4(s[0] + s[1], s[2] + s[3], 0.0f, 0.0f);
+        } else {
+            const uint32_t b = u >> 2, sg = (u >> 1) & 1u, h = u & 1u;
+            float s[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hi[i] = p[4 + i];
-    pairs32(lo, o.lo02, o.lo13, o.sum_lo);
-    pairs32(hi, o.hi02, o.hi13, o.sum_hi);
-    o.bias_lo = -1024.0f * o.sum_lo;
-    o.bias_hi = -1024.0f * o.sum_hi;
+            for (int q = 0; q < 4; ++q) {
+                p = gh_gp<uint4>((uint64_t)(x + (size_t)b * 256 + sg * 128 + q * 32 + h * 16));
+                pair16(p[0], p[1], xs[q * units + u], xs[(4 + q) * units + u], s[q]);
+            }
+            sums[u] = make_float4(s[0], s[1], s[2], s[3]);
+        }
+    }
 }
 
 struct WQ4 {
@@ -70,55 +103,30 @@ __device__ __forceinline__ void load_w_q4(const uint8_t* w, uint32_t rows, uint3
                                     ((size_t)row * nb + (u >> 2)) * 16));
 }
 
-__device__ __forceinline__ float dot_q4(const XQ4& x, const WQ4& w, uint32_t g) {
+// One Q4_K unit: the 32 qs bytes of group g (sub-blocks 2g, 2g+1) against staged x.
+__device__ __forceinline__ float dot_q4(const uint4 (&xv)[8], const float4& xsum, const WQ4& w,
+                                        uint32_t g, const Masks& m) {
     const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
-    float slo = x.bias_lo, shi = x.bias_hi;
+    const uint32_t lo02[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
+    const uint32_t lo13[8] = {xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
+    const uint32_t hi02[8] = {xv[4].x, xv[4].y, xv[4].z, xv[4].w, xv[5].x, xv[5].y, xv[5].z, xv[5].w};
+    const uint32_t hi13[8] = {xv[6].x, xv[6].y, xv[6].z, xv[6].w, xv[7].x, xv[7].y, xv[7].z, xv[7].w};
+    float slo = -1024.0f * xsum.x, shi = -1024.0f * xsum.y;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const uint32_t v = qw[k], v8 = v >> 8;
-        slo = gh_dot2(x.lo02[k], (v & 0x000F000Fu) | 0x64006400u, slo);
-        slo = gh_dot2(x.lo13[k], (v8 & 0x000F000Fu) | 0x64006400u, slo);
-        shi = gh_dot2(x.hi02[k], (v & 0x00F000F0u) | 0x64006400u, shi);
-        shi = gh_dot2(x.hi13[k], (v8 & 0x00F000F0u) | 0x64006400u, shi);
+        slo = gh_dot2(lo02[k], (v & m.lo4) | m.bias, slo);
+        slo = gh_dot2(lo13[k], (v8 & m.lo4) | m.bias, slo);
+        shi = gh_dot2(hi02[k], (v & m.hi4) | m.bias, shi);
+        shi = gh_dot2(hi13[k], (v8 & m.hi4) | m.bias, shi);
     }
     const float d = gh_h2f(w.hd.x & 0xFFFFu), dmin = gh_h2f(w.hd.x >> 16);
     uint32_t sc0, mn0, sc1, mn1;
     gh_q4k_scale_min(w.hd, 2 * g, sc0, mn0);
     gh_q4k_scale_min(w.hd, 2 * g + 1, sc1, mn1);
     // slo = Σx·q_lo, shi = 16·Σx·q_hi
-    return (d * (float)sc0) * slo - (dmin * (float)mn0) * x.sum_lo +
-           (d * (float)sc1 * 0.0625f) * shi - (dmin * (float)mn1) * x.sum_hi;
-}
-
-// Activations of one Q6_K unit: quarter k covers x[256b + 128s + 32k + 16h + 0..15].
-struct XQ6 {
-    uint32_t p02[4][4], p13[4][4];
-    float bias[4];
-};
-
-__device__ __forceinline__ void load_x_q6(const uint16_t* x, uint32_t b, uint32_t s, uint32_t h,
-                                          XQ6& o) {
-    uint4 v[4][2];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const GH_GLOBAL uint4* p =
-            gh_gp<uint4>((uint64_t)(x + (size_t)b * 256 + s * 128 + k * 32 + h * 16));
-        v[k][0] = p[0];
-        v[k][1] = p[1];
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        float sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint4& q = v[k][j >> 1];
-            const uint32_t a = (j & 1) ? q.z : q.x, c = (j & 1) ? q.w : q.y;
-            o.p02[k][j] = (a & 0xFFFFu) | (c << 16);
-            o.p13[k][j] = (a >> 16) | (c & 0xFFFF0000u);
-            sum += (gh_h2f(a & 0xFFFFu) + gh_h2f(a >> 16)) + (gh_h2f(c & 0xFFFFu) + gh_h2f(c >> 16));
-        }
-        o.bias[k] = -1056.0f * sum;  // pair value = 1024 + (q + 32)
-    }
+    return (d * (float)sc0) * slo - (dmin * (float)mn0) * xsum.x +
+           (d * (float)sc1 * 0.0625f) * shi - (dmin * (float)mn1) * xsum.y;
 }
 
 struct WQ6 {
@@ -138,11 +146,14 @@ __device__ __forceinline__ void load_w_q6(const uint8_t* w, uint32_t rows, uint3
     o.d = *gh_gp<uint16_t>((uint64_t)(w + (size_t)rows * 208 * nb + blk * 2));
 }
 
-__device__ __forceinline__ float dot_q6(const XQ6& x, const WQ6& w, uint32_t s, uint32_t h) {
+// One Q6_K unit (segment s, half h of block b): 16 weights of each quarter.
+__device__ __forceinline__ float dot_q6(const uint4 (&xv)[8], const float4& xsum, const WQ6& w,
+                                        uint32_t s, uint32_t h, const Masks& m) {
     const uint32_t A[4] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w};
     const uint32_t B[4] = {w.qb.x, w.qb.y, w.qb.z, w.qb.w};
     const uint32_t H[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
-    float sk[4] = {x.bias[0], x.bias[1], x.bias[2], x.bias[3]};
+    // pair value = 1024 + (q + 32): start each quarter at -1056·Σx
+    float sk[4] = {-1056.0f * xsum.x, -1056.0f * xsum.y, -1056.0f * xsum.z, -1056.0f * xsum.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         uint32_t v[4];
@@ -152,8 +163,10 @@ __device__ __forceinline__ float dot_q6(const XQ6& x, const WQ6& w, uint32_t s, 
         v[3] = ((B[j] >> 4) & 0x0F0F0F0Fu) | ((H[j] >> 2) & 0x30303030u);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            sk[k] = gh_dot2(x.p02[k][j], (v[k] & 0x003F003Fu) | 0x64006400u, sk[k]);
-            sk[k] = gh_dot2(x.p13[k][j], ((v[k] >> 8) & 0x003F003Fu) | 0x64006400u, sk[k]);
+            const uint32_t p02 = j == 0 ? xv[k].x : j == 1 ? xv[k].y : j == 2 ? xv[k].z : xv[k].w;
+            const uint32_t p13 = j == 0 ? xv[4 + k].x : j == 1 ? xv[4 + k].y : j == 2 ? xv[4 + k].z : xv[4 + k].w;
+            sk[k] = gh_dot2(p02, (v[k] & m.lo6) | m.bias, sk[k]);
+            sk[k] = gh_dot2(p13, ((v[k] >> 8) & m.lo6) | m.bias, sk[k]);
         }
     }
     // int8 scales sc[8s + h + 2k], k = 0..3
@@ -164,50 +177,42 @@ __device__ __forceinline__ float dot_q6(const XQ6& x, const WQ6& w, uint32_t s, 
     return gh_h2f(w.d) * (s0 * sk[0] + s1 * sk[1] + s2 * sk[2] + s3 * sk[3]);
 }
 
-// R rows (and, for SwiGLU, the same R rows of a second matrix) of one format over the whole
-// in-dimension; per-lane partial sums in acc[m][r].
+template <uint32_t FMT>
+using WRow = typename std::conditional<FMT == kQ4K, WQ4, WQ6>::type;
+
+// Weights of one pipeline step: chunk `u0` of rows row0..row0+R-1 of M matrices (lane's unit).
 template <uint32_t FMT, int R, int M>
-__device__ __forceinline__ void rows_dot(const uint8_t* const (&w)[M], uint32_t rows, uint32_t nb,
-                                         const uint16_t* x, uint32_t row0, float (&acc)[M][R]) {
-    const uint32_t lane = threadIdx.x & 63u, units = nb * 4;
+__device__ __forceinline__ void load_step(const uint8_t* const (&w)[M], uint32_t rows,
+                                          uint32_t nb, uint32_t row0, uint32_t u,
+                                          WRow<FMT> (&wr)[M][R]) {
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
-    for (uint32_t u0 = 0; u0 < units; u0 += 64) {
-        const uint32_t u = u0 + lane;
-        if (u >= units) continue;
-        const uint32_t b = u >> 2;
-        if constexpr (FMT == kQ4K) {
-            const uint32_t g = u & 3u;
-            WQ4 wr[M][R];
-#pragma unroll
-            for (int m = 0; m < M; ++m)
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    load_w_q4(w[m], rows, nb, min(row0 + r, rows - 1), u, wr[m][r]);
-            XQ4 xv;
-            load_x_q4(x, b, g, xv);
-#pragma unroll
-            for (int m = 0; m < M; ++m)
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[m][r] += dot_q4(xv, wr[m][r], g);
-        } else {
-            const uint32_t s = (u >> 1) & 1u, h = u & 1u;
-            WQ6 wr[M][R];
-#pragma unroll
-            for (int m = 0; m < M; ++m)
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    load_w_q6(w[m], rows, nb, min(row0 + r, rows - 1), u, wr[m][r]);
-            XQ6 xv;
-            load_x_q6(x, b, s, h, xv);
-#pragma unroll
-            for (int m = 0; m < M; ++m)
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[m][r] += dot_q6(xv, wr[m][r], s, h);
+        for (int r = 0; r < R; ++r) {
+            if constexpr (FMT == kQ4K)
+                load_w_q4(w[m], rows, nb, min(row0 + r, rows - 1), u, wr[m][r]);
+            else
+                load_w_q6(w[m], rows, nb, min(row0 + r, rows - 1), u, wr[m][r]);
         }
-    }
+}
+
+template <uint32_t FMT, int R, int M>
+__device__ __forceinline__ void compute_step(const uint4* xs, const float4* sums, uint32_t units,
+                                             uint32_t u, const Masks& mk,
+                                             const WRow<FMT> (&wr)[M][R], float (&acc)[M][R]) {
+    uint4 xv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xv[k] = xs[k * units + u];
+    const float4 xsum = sums[u];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if constexpr (FMT == kQ4K)
+                acc[m][r] += dot_q4(xv, xsum, wr[m][r], u & 3u, mk);
+            else
+                acc[m][r] += dot_q6(xv, xsum, wr[m][r], (u >> 1) & 1u, u & 1u, mk);
+        }
 }
 
 __device__ __forceinline__ uint32_t position(const GhGemvArgs& a) {
@@ -297,41 +302,114 @@ __device__ __forceinline__ void epilogue(const GhGemvArgs& a, const GhGemvSeg& s
 // MODE: which row kernels a launch may need (specialized to keep register use low).
 enum : int { kModeQ4 = 0, kModeQ6 = 1, kModeMixed = 2, kModeSwiglu = 3 };
 
+__device__ __forceinline__ uint32_t i_end(const GhGemvArgs& a, uint32_t si) {
+    return si + 1 < a.nseg ? a.seg[si + 1].task0 : a.tasks;
+}
+
+// A wave's work: tasks first, first + stride, ... < ntask of one segment; a task is nch chunks
+// of 64 units. The weights of a chunk (all R rows, both matrices for SwiGLU) are requested
+// together before any arithmetic; lanes past the last unit re-read the last unit (addresses
+// stay valid, loads stay unconditional so the wait counts stay exact) and add nothing.
+// `primed`: the caller already loaded the first chunk of the first task into wa.
+template <uint32_t FMT, int R, int M>
+__device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg& sg,
+                                            uint32_t first, uint32_t stride, uint32_t ntask,
+                                            uint32_t t, uint32_t nb, const uint4* xs,
+                                            const float4* sums, const Masks& mk, bool primed,
+                                            WRow<FMT> (&wa)[M][R]) {
+    const uint32_t lane = threadIdx.x & 63u, units = nb * 4;
+    const uint32_t nch = (units + 63) / 64;
+    const uint8_t* w[M];
+    w[0] = (const uint8_t*)sg.w;
+    if constexpr (M == 2) w[1] = (const uint8_t*)a.aux;
+    for (uint32_t k = first; k < ntask; k += stride) {
+        float acc[M][R];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+        for (uint32_t c = 0; c < nch; ++c) {
+            const uint32_t u = c * 64 + lane, uc = min(u, units - 1);
+            if (!primed) load_step<FMT, R, M>(w, sg.rows, nb, k * R, uc, wa);
+            primed = false;
+            if (u < units) compute_step<FMT, R, M>(xs, sums, units, u, mk, wa, acc);
+        }
+        float v[M][R];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) v[m][r] = gh_wave_sum63(acc[m][r]);
+        if (lane == 63u) epilogue<R>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr);
+    }
+}
+
+// Staged x lives in dynamic LDS: 144 B per 64-weight unit (twice for the mixed kernel).
+// Waves are split between the segments in proportion to their tasks (args: seg.task0 is the
+// first task index, the wave split is recomputed here), so a wave only ever runs one format.
 template <int R, int MODE>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
-    const uint32_t task = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (task >= a.tasks) return;
-    uint32_t si = 0;
-    if (a.nseg > 1 && task >= a.seg[1].task0) si = 1;
-    if (a.nseg > 2 && task >= a.seg[2].task0) si = 2;
+    extern __shared__ uint4 lds[];
+    constexpr int M = MODE == kModeSwiglu ? 2 : 1;
+    const uint32_t nb = a.in_dim >> 8, units = nb * 4;
+    uint4* xs4 = lds;
+    float4* xsum4 = (float4*)(lds + 8 * units);
+    uint4* xs6 = lds + 9 * units;
+    float4* xsum6 = (float4*)(lds + 17 * units);
+    const uint32_t waves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    // segment of this wave and its position among the segment's waves
+    uint32_t si = 0, w0 = 0, nw = waves;
+    if (a.nseg > 1) {
+        uint32_t acc_w = 0;
+        for (uint32_t i = 0; i < a.nseg; ++i) {
+            const uint32_t t_end = i + 1 < a.nseg ? a.seg[i + 1].task0 : a.tasks;
+            const uint32_t t_n = t_end - a.seg[i].task0;
+            uint32_t n_w = i + 1 < a.nseg ? (uint32_t)(((uint64_t)t_n * waves + a.tasks - 1) / a.tasks)
+                                          : waves - acc_w;
+            n_w = max(1u, min(n_w, waves - acc_w - (a.nseg - 1 - i)));
+            if (gw >= acc_w && gw < acc_w + n_w) {
+                si = i;
+                w0 = acc_w;
+                nw = n_w;
+            }
+            acc_w += n_w;
+        }
+    }
     const GhGemvSeg sg = a.seg[si];
-    const uint32_t row0 = (task - sg.task0) * R;
-    const uint32_t nb = a.in_dim >> 8;
-    const bool lane63 = (threadIdx.x & 63u) == 63u;
+    const uint32_t ntask = i_end(a, si) - sg.task0, first = gw - w0;
+    const Masks mk = make_masks();
+    // The first step's weights of the kernel's primary format are requested before x is
+    // staged, so their latency overlaps the staging.
+    constexpr uint32_t F0 = MODE == kModeQ6 ? kQ6K : kQ4K;
+    WRow<F0> w0r[M][R];
+    const bool primed = sg.fmt == F0 && first < ntask;
+    if (primed) {
+        const uint8_t* w[M];
+        w[0] = (const uint8_t*)sg.w;
+        if constexpr (M == 2) w[1] = (const uint8_t*)a.aux;
+        load_step<F0, R, M>(w, sg.rows, nb, first * R, min(threadIdx.x & 63u, units - 1), w0r);
+    }
     for (uint32_t t = 0; t < a.n; ++t) {
         const uint16_t* x = (const uint16_t*)a.x + (size_t)t * a.in_dim;
-        if constexpr (MODE == kModeSwiglu) {
-            const uint8_t* const w[2] = {(const uint8_t*)sg.w, (const uint8_t*)a.aux};
-            float acc[2][R];
-            rows_dot<kQ4K, R, 2>(w, sg.rows, nb, x, row0, acc);
-            float g[R], u[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                g[r] = gh_wave_sum63(acc[0][r]);
-                u[r] = gh_wave_sum63(acc[1][r]);
-            }
-            if (lane63) epilogue<R>(a, sg, t, row0, g, u);
+        if (t) __syncthreads();
+        if constexpr (MODE == kModeQ6) {
+            stage_x<kQ6K>(x, units, xs4, xsum4);
         } else {
-            const uint8_t* const w[1] = {(const uint8_t*)sg.w};
-            float acc[1][R];
-            if (MODE == kModeQ4 || (MODE == kModeMixed && sg.fmt == kQ4K))
-                rows_dot<kQ4K, R, 1>(w, sg.rows, nb, x, row0, acc);
-            else
-                rows_dot<kQ6K, R, 1>(w, sg.rows, nb, x, row0, acc);
-            float v[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) v[r] = gh_wave_sum63(acc[0][r]);
-            if (lane63) epilogue<R>(a, sg, t, row0, v, nullptr);
+            stage_x<kQ4K>(x, units, xs4, xsum4);
+            if constexpr (MODE == kModeMixed) stage_x<kQ6K>(x, units, xs6, xsum6);
+        }
+        __syncthreads();
+        if constexpr (MODE == kModeQ6) {
+            run_segment<kQ6K, R, M>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r);
+        } else if constexpr (MODE == kModeMixed) {
+            if (sg.fmt == kQ4K) {
+                run_segment<kQ4K, R, M>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r);
+            } else {
+                WRow<kQ6K> w6[M][R];
+                run_segment<kQ6K, R, M>(a, sg, first, nw, ntask, t, nb, xs6, xsum6, mk, false, w6);
+            }
+        } else {
+            run_segment<kQ4K, R, M>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r);
         }
     }
 }

@@ -124,9 +124,9 @@ struct GhKvWriteArgs {
     uint32_t v_stride;
 };
 
-// Split-K flash decode: grid (kv_heads, splits, rows). Row r attends positions 0..pos_r where
-// pos_r = base + r (or *pos_ptr). Partials: m, l [rows][q_heads][splits],
-// acc [rows][q_heads][splits][value_dim].
+// Split-K flash decode: grid (splits, kv_heads, rows). Row r attends positions 0..pos_r where
+// pos_r = base + r (+ *pos_ptr). Partials: m, l [rows][q_heads][splits],
+// acc [rows][q_heads][splits][value_dim]; counters u32 [rows][kv_heads], zero between launches.
 struct GhAttnArgs {
     uint64_t q;        // f16 [rows][q_heads][key_dim]
     uint64_t kc;       // f16 cache base [layer][context][kv_heads][key_dim]
@@ -136,6 +136,7 @@ struct GhAttnArgs {
     uint64_t part_l;
     uint64_t part_acc;
     uint64_t pos_ptr;  // optional u32* position
+    uint64_t counters; // u32 [rows][kv_heads]
     uint32_t key_dim;
     uint32_t value_dim;
     uint32_t kv_heads;
@@ -144,10 +145,8 @@ struct GhAttnArgs {
     uint32_t context;
     uint32_t base;
     uint32_t rows;
-    uint32_t splits;
-    uint32_t split_len; // positions per split
+    uint32_t splits;   // grid.x: workgroups per (row, kv head), <= 32
     float scale;
-    uint32_t pad;
 };
 
 struct GhArgmaxArgs {
