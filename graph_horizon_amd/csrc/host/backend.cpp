@@ -359,9 +359,14 @@ static uint32_t gemv_rows(uint64_t total_rows) {
         return e ? std::atoi(e) : 0;
     }();
     if (forced == 1 || forced == 2 || forced == 4) return (uint32_t)forced;
-    if (total_rows >= 16384) return 4;
-    if (total_rows >= 4096) return 2;
-    return 1;
+    return total_rows >= 4096 ? 2 : 1;
+}
+
+uint32_t resident_wgs(gh_backend* b, GhKernel k, uint32_t block, uint32_t shmem) {
+    int n = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, b->fn[k], (int)block, shmem) != hipSuccess || n < 1)
+        n = 1;
+    return (uint32_t)n * b->cus;
 }
 
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
@@ -424,13 +429,14 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     if (rope && !b->rope.table) return fail(b, GH_E_STATE, "gemv: RoPE table not built");
     if (in_dim / 64 > 256) return fail(b, GH_E_UNSUPPORTED, "gemv: in_dim above 16384");
     // x staged once per workgroup in LDS (144 B per 64-weight unit; both layouts if mixed);
-    // the persistent grid loops its waves over the tasks.
+    // the persistent grid (at most what is resident at once) loops its waves over the tasks.
     const uint32_t shmem = (in_dim / 64) * 144 * (mixed ? 2 : 1);
     static const uint32_t max_wg = [] {
         const char* e = std::getenv("GH_GEMV_MAX_WG");
-        return e ? (uint32_t)std::atoi(e) : 1024u;
+        return e ? (uint32_t)std::atoi(e) : 0u;
     }();
-    return launch(b, k, std::min<uint32_t>(ceil_div(task, 4), max_wg), 1, 1, 256, &a, shmem);
+    const uint32_t cap = max_wg ? max_wg : resident_wgs(b, k, 256, shmem);
+    return launch(b, k, std::max<uint32_t>(1, std::min<uint32_t>(ceil_div(task, 4), cap)), 1, 1, 256, &a, shmem);
 }
 
 int op_step_advance(gh_backend* b, void* scalars, void* history) {
@@ -456,6 +462,7 @@ int gh_create(const gh_config* cfg, gh_backend** out) {
     if (hipSetDevice(dev) != hipSuccess) return GH_E_NO_DEVICE;
     auto* b = new gh_backend();
     b->device = dev;
+    b->cus = (uint32_t)std::max(1, prop.multiProcessorCount);
     b->enc.b = b;
     int rc = hip_check(b, hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking), "hipStreamCreate");
     if (!rc) rc = hip_check(b, hipEventCreate(&b->ev_start), "hipEventCreate");

@@ -55,6 +55,7 @@ struct gh_encoder {
 
 struct gh_backend {
     int device = 0;
+    uint32_t cus = 0;  // compute units of the device
     hipStream_t stream = nullptr;
     std::vector<hipModule_t> modules;
     hipFunction_t fn[K_COUNT] = {};
@@ -78,6 +79,8 @@ int hip_check(gh_backend* b, hipError_t e, const char* what);
 int launch(gh_backend* b, GhKernel k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
            const void* args, uint32_t shmem = 0);
 int ensure_workspace(gh_backend* b, size_t bytes);
+// Workgroups of `block` threads and `shmem` bytes of LDS resident on the whole device at once.
+uint32_t resident_wgs(gh_backend* b, GhKernel k, uint32_t block, uint32_t shmem);
 int ensure_rope(gh_backend* b, const gh_yarn* y, uint32_t positions);
 bool yarn_valid(const gh_yarn* y);
 // Graph-capturable op variants used by the model driver: positions/tokens read from device.
