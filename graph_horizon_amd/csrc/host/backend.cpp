@@ -35,9 +35,11 @@ const KernelName kKernels[] = {
     {K_ATTN_G2, "gh_attn_g2"},             {K_ATTN_G4, "gh_attn_g4"},
     {K_ATTN_G8, "gh_attn_g8"},
     {K_STEP_ADVANCE, "gh_step_advance"},
+    {K_GEMM_Q4K, "gh_gemm_q4k"},           {K_GEMM_Q6K, "gh_gemm_q6k"},
+    {K_GEMM_REDUCE, "gh_gemm_reduce"},
 };
 
-const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention"};
+const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
 
 constexpr uint32_t kArgmaxBlocks = 256;
 // argmax scratch at the front of the workspace: f32[256] values, u32[256] indices, u32 result
@@ -676,12 +678,40 @@ int gh_embed(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* w, u
     return latch(enc, op_embed(b, x, w, token, embd, nullptr));
 }
 
+// Matrix-core GEMM for n >= kGemmMinTokens: 128 x 128 (tokens x rows) workgroup tiles; split-K
+// over the units when the tiles alone would leave resident workgroup slots idle.
+constexpr uint32_t kGemmMinTokens = 8;
+
+int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n) {
+    const uint32_t in_dim = w->cols, rows = w->rows, units = in_dim / 64;
+    const GhKernel k = w->format == GH_FMT_Q4_K ? K_GEMM_Q4K : K_GEMM_Q6K;
+    const uint32_t tr = ceil_div(rows, 128), tt = ceil_div(n, 128), tiles = tr * tt;
+    static const uint32_t forced = [] {
+        const char* e = std::getenv("GH_GEMM_SPLITS");
+        return e ? (uint32_t)std::atoi(e) : 0u;
+    }();
+    uint32_t splits = forced ? forced : std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles);
+    splits = std::max<uint32_t>(1, std::min<uint32_t>({splits, std::max<uint32_t>(1, units / 8), 16u}));
+    GhGemmArgs ga{a->addr, w->addr, out, 0, in_dim, rows, n, splits};
+    if (splits > 1) {
+        int rc = ensure_workspace(b, (size_t)splits * n * rows * 4);
+        if (rc) return rc;
+        ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
+    }
+    int rc = launch(b, k, tr, tt, splits, 256, &ga);
+    if (rc || splits == 1) return rc;
+    const uint64_t total = (uint64_t)n * rows;
+    return launch(b, K_GEMM_REDUCE, (uint32_t)std::min<uint64_t>(ceil_div(total, (uint64_t)256), 4096), 1, 1,
+                  256, &ga);
+}
+
 static int gemv_launch(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w,
                        uint32_t in_dim, uint32_t out_dim, uint32_t n, bool f32) {
     if (!is_weight(w)) return fail(b, GH_E_UNSUPPORTED, "matmul: weight must be Q4_K or Q6_K");
     if (w->cols != in_dim || w->rows != out_dim) return fail(b, GH_E_INVALID, "matmul: weight shape mismatch");
     if (!fits(a, (uint64_t)n * in_dim * 2) || !fits(out, (uint64_t)n * out_dim * (f32 ? 4 : 2)))
         return fail(b, GH_E_RANGE, "matmul: buffer too small");
+    if (!f32 && n >= kGemmMinTokens) return op_gemm(b, out->addr, a, w, n);
     GemvSeg seg{w, out->addr, f32 ? (uint32_t)GH_EPI_F32 : (uint32_t)GH_EPI_F16};
     return op_gemv(b, &seg, 1, a, n, 0, nullptr, 0, nullptr);
 }

@@ -36,6 +36,9 @@ enum GhKernel : int {
     K_ATTN_G4,
     K_ATTN_G8,
     K_STEP_ADVANCE,
+    K_GEMM_Q4K,
+    K_GEMM_Q6K,
+    K_GEMM_REDUCE,
     K_COUNT
 };
 

@@ -75,6 +75,18 @@ struct GhGemvArgs {
     uint32_t pad;
 };
 
+// Prefill GEMM (gemm.hip): out f16 [n][rows] (or FP32 split partials [splits][n][rows]).
+struct GhGemmArgs {
+    uint64_t x;     // f16 activations [n][in_dim]
+    uint64_t w;     // device layout weights [rows][in_dim]
+    uint64_t out;   // f16 [n][rows]
+    uint64_t part;  // FP32 partials when splits > 1
+    uint32_t in_dim;
+    uint32_t rows;
+    uint32_t n;
+    uint32_t splits;
+};
+
 struct GhRmsnormArgs {
     uint64_t out;   // f16 [rows][dim]
     uint64_t x;     // f32 [rows][dim]
