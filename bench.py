@@ -104,6 +104,9 @@ def main():
     ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
                     help="decode steps as one replayed HIP graph (default) or as direct "
                          "stream launches of the same kernels (for kernel tracers)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the roofline kernel (4 distinct weights) and a 256 MiB "
+                         "device copy of known size, for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -113,6 +116,9 @@ def main():
     from graph_horizon_amd import HipBackend, HipModel, synth
     from graph_horizon_amd import _ffi as F
 
+    if args.traffic_probe:
+        traffic_probe(synth.SHAPES[args.shape])
+        return
     shape = synth.SHAPES[args.shape]
     per_block, per_token = weight_bytes(shape)
     kv_context = args.prompt + args.warmup + args.steps + 8
@@ -198,19 +204,59 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": ROOFLINE_TRAFFIC_BYTES,
             "kernel": f"gh_gemv_q4k (Q4_K GEMV {ffn}x{d}, {gemv_bytes} B/launch)",
             "avg_us": round(gemv_ms * 1e3, 3),
         },
     }
     c1 = c1_gemv(hip, model, shape)
     result["config"]["q4k_gemv_c1_shape"] = c1
+    result["config"]["prefill_gemm_c3"] = prefill_gemm(hip, model, shape, 512)
     model.close()
     hip.close()
     if not args.no_cpu:
         log("bench: CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(shape, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+# HBM bytes per launch of the roofline kernel (gh_gemv_q4k_r2 at 12288x4096), from the two
+# rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --traffic-probe`, each scaled by
+# the same counter's reading for a 256 MiB device-to-device copy (FETCH_SIZE x 2.0, WRITE_SIZE
+# x 1.0): profiles/q4k_gemv_12288x4096.txt. Re-measure whenever the kernel changes.
+ROOFLINE_TRAFFIC_BYTES = 28534276
+
+
+def traffic_probe(shape):
+    """Roofline kernel launches plus a copy of known size, nothing else (for PMC passes)."""
+    import ctypes as C
+
+    from graph_horizon_amd import HipBackend, synth
+
+    hip = HipBackend(0)
+    d, ffn = shape.embedding_length, shape.feed_forward_length
+    rng = np.random.default_rng(5)
+    ws = [hip.load_weight(12, synth.quant_blocks(rng, 12, ffn, d, 0.02), d, ffn) for _ in range(4)]
+    xb = hip.from_host(synth.f16_bits(rng.standard_normal(d)))
+    yb = hip.alloc_buffer(ffn * 2)
+    enc = hip.begin()
+    for w in ws:
+        hip.lib.gh_matmul(hip.h, enc, C.byref(yb), C.byref(xb), C.byref(w), d, ffn)
+    hip.submit()
+    rt = C.CDLL("libamdhip64.so")
+    nbytes = 256 << 20
+    src, dst = C.c_void_p(), C.c_void_p()
+    assert rt.hipMalloc(C.byref(src), C.c_size_t(nbytes)) == 0
+    assert rt.hipMalloc(C.byref(dst), C.c_size_t(nbytes)) == 0
+    assert rt.hipMemset(src, 1, C.c_size_t(nbytes)) == 0
+    for _ in range(2):  # device-to-device: the runtime's blit copy kernel
+        assert rt.hipMemcpy(dst, src, C.c_size_t(nbytes), 3) == 0
+    assert rt.hipDeviceSynchronize() == 0
+    log(f"bench: traffic probe: 4 x gh_matmul {ffn}x{d} ({ffn * (d // 256) * 144} B of weights "
+        f"each), 2 x copy of {nbytes} B")
+    rt.hipFree(src)
+    rt.hipFree(dst)
+    hip.close()
 
 
 def model_weight(model, layer, tid):
@@ -223,6 +269,51 @@ def model_weight(model, layer, tid):
     rc = model.b.lib.gh_model_weight(model.h, layer, tid, C.byref(buf))
     assert rc == 0, rc
     return buf
+
+
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_gemm(hip, model, shape, n):
+    """the n-token prefill GEMMs (gate/up Q4_K d->FFN, down Q6_K FFN->d) on
+    the matrix cores, over 8 distinct layers' weights, timed with HIP events."""
+    import ctypes as C
+
+    from graph_horizon_amd import _ffi as F
+
+    d, ffn = shape.embedding_length, shape.feed_forward_length
+    rng = np.random.default_rng(11)
+    a_d = hip.from_host(synth_f16(rng, n * d))
+    a_f = hip.from_host(synth_f16(rng, n * ffn))
+    y = hip.alloc_buffer(n * max(d, ffn) * 2)
+    out = {}
+    for name, tid, ind, outd, a in (("gate_up_q4k", F.T_FFN_GATE, d, ffn, a_d),
+                                    ("down_q6k", F.T_FFN_DOWN, ffn, d, a_f)):
+        ws = [model_weight(model, li, tid) for li in range(min(8, shape.block_count))]
+        enc = hip.begin()
+        hip.lib.gh_matmul_batched(hip.h, enc, C.byref(y), C.byref(a), C.byref(ws[0]), ind, outd, n)
+        hip.submit()
+        reps = 4
+        enc = hip.begin()
+        hip.timer_start()
+        for _ in range(reps):
+            for w in ws:
+                hip.lib.gh_matmul_batched(hip.h, enc, C.byref(y), C.byref(a), C.byref(w), ind, outd, n)
+        ms = hip.timer_stop() / (reps * len(ws))
+        hip.submit()
+        tflops = 2.0 * n * ind * outd / (ms * 1e-3) / 1e12
+        out[name] = {"shape": f"{n}x{ind}->{outd}", "avg_us": round(ms * 1e3, 2),
+                     "tflops": round(tflops, 1), "frac_f16_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        log(f"bench: prefill GEMM {name} {n}x{ind}->{outd}: {ms * 1e3:.1f} us, {tflops:.0f} TFLOP/s")
+    for b in (a_d, a_f, y):
+        hip.free_buffer(b)
+    return out
+
+
+def synth_f16(rng, count):
+    from graph_horizon_amd import synth
+
+    return synth.f16_bits(rng.standard_normal(count))
 
 
 def c1_gemv(hip, model, shape):

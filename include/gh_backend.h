@@ -60,7 +60,8 @@ typedef struct gh_buf {
 
 typedef struct gh_config {
     int32_t device;               /* HIP device ordinal */
-    const char* code_object_path; /* NULL: gh_kernels_gfx950.co next to the library */
+    const char* code_object_path; /* directory of the gh_<module>_gfx950.co code objects;
+                                     NULL: the directory libgh_hip.so was loaded from */
 } gh_config;
 
 /* Ministral YaRN parameters (backend/rope.rs:11-21). */
