@@ -36,7 +36,7 @@ const KernelName kKernels[] = {
     {K_ATTN_G8, "gh_attn_g8"},
     {K_STEP_ADVANCE, "gh_step_advance"},
     {K_GEMM_Q4K, "gh_gemm_q4k"},           {K_GEMM_Q6K, "gh_gemm_q6k"},
-    {K_GEMM_REDUCE, "gh_gemm_reduce"},
+    {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -273,6 +273,8 @@ int ensure_counters(gh_backend* b, size_t slots) {
 
 // Causal GQA attention for `rows` query rows at positions base + r (+ *pos_ptr);
 // max_pos bounds the positions the launch can see (sizes the split grid).
+constexpr uint32_t kAttnPrefillMinRows = 32;
+
 int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
                  uint32_t q_heads, uint32_t base, uint32_t rows, uint32_t layer,
                  const void* pos_ptr, uint32_t max_pos) {
@@ -284,6 +286,26 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         case 4: k = K_ATTN_G4; break;
         case 8: k = K_ATTN_G8; break;
         default: return fail(b, GH_E_UNSUPPORTED, "attention: GQA group must be 1, 2, 4 or 8");
+    }
+    // Batched prefill on the matrix cores: 32-row query blocks x kv heads (G = 4, head 128).
+    static const bool no_mfma = std::getenv("GH_ATTN_PREFILL_SIMT") != nullptr;
+    if (!no_mfma && !pos_ptr && rows >= kAttnPrefillMinRows && group == 4 && kv->head_dim == 128 &&
+        kv->value_dim == 128) {
+        GhAttnArgs a{};
+        a.q = q->addr;
+        a.kc = kv->k.addr;
+        a.vc = kv->v.addr;
+        a.out = out->addr;
+        a.key_dim = kv->head_dim;
+        a.value_dim = kv->value_dim;
+        a.kv_heads = kv->kv_heads;
+        a.q_heads = q_heads;
+        a.layer = layer;
+        a.context = kv->context;
+        a.base = base;
+        a.rows = rows;
+        a.scale = 1.0f / std::sqrt((float)kv->head_dim);
+        return launch(b, K_ATTN_PREFILL_G4, ceil_div(rows, 32), kv->kv_heads, 1, 256, &a);
     }
     const uint32_t splits = attention_splits(max_pos + 1);
     // bound the partials: rows in groups that fit a 256 MiB workspace

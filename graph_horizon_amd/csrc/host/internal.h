@@ -39,6 +39,7 @@ enum GhKernel : int {
     K_GEMM_Q4K,
     K_GEMM_Q6K,
     K_GEMM_REDUCE,
+    K_ATTN_PREFILL_G4,
     K_COUNT
 };
 

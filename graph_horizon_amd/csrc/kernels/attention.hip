@@ -185,3 +185,218 @@ GH_KERNEL __launch_bounds__(256) void gh_attn_g1(GhAttnArgs a) { attn_body<1>(a)
 GH_KERNEL __launch_bounds__(256) void gh_attn_g2(GhAttnArgs a) { attn_body<2>(a); }
 GH_KERNEL __launch_bounds__(256) void gh_attn_g4(GhAttnArgs a) { attn_body<4>(a); }
 GH_KERNEL __launch_bounds__(256) void gh_attn_g8(GhAttnArgs a) { attn_body<8>(a); }
+
+// ---------------------------------------------------------------------------------------------
+// Causal GQA prefill attention on the matrix cores (flash attention, G = 4 query heads per kv
+// head, head_dim = value_dim = 128).
+//
+// Grid (query blocks of 32 rows, kv heads), 256 threads; wave w owns query head 4·kvh + w for
+// the block's 32 rows, so every K/V tile staged in LDS serves all four heads. Per tile of 64
+// key positions, with v_mfma_f32_16x16x32_f16 and FP32 accumulators:
+//   S^T = K · Q^T   A = K rows (LDS), B = the wave's FP16 query rows (registers); the output
+//                   layout gives each lane one query row (lane % 16) and four key positions
+//                   per 16 x 16 tile, so the row's running max/sum stay in that lane;
+//   O^T += V^T · P^T  P goes to the B operand straight from the S^T registers (a lane's key
+//                   positions name its k-slots; V^T is read from LDS in the same slot order,
+//                   which leaves the product unchanged). P is split into FP16 hi + lo parts
+//                   (two MFMAs), so P·V carries FP32-level accuracy.
+// Softmax in base 2: scores are scaled by scale·log2(e), p = 2^(s - m), rescale 2^(m_old - m).
+// Rows: query r at position base + r attends positions 0..base + r (the reference's prefill,
+// attention/mod.rs:582-725). Query blocks run heaviest (latest) first.
+namespace {
+typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
+typedef float af4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPQ = 32;          // query rows per workgroup
+constexpr int kPK = 64;          // key positions per tile
+constexpr int kKP = 128 + 8;     // K tile pitch (FP16): [64 keys][128 dims]
+constexpr int kVP = kPK + 8;     // V^T tile pitch (FP16): [128 dims][64 keys]
+
+struct KVStage {
+    uint4 k0, k1, k2, k3;  // K: chunk (key c/16, dims 8·(c%16)), c = tid + 256 i
+    uint4 v0, v1, v2, v3;  // V: keys 4·(lane%16) + i, dims 8·(lane/16 + 4·wave)
+};
+
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xFFFF0000u); }
+
+__device__ __forceinline__ void kv_load(const GhAttnArgs& a, const uint16_t* kc, const uint16_t* vc,
+                                        size_t kv_row, uint32_t t0, uint32_t kv_end, KVStage& s) {
+    const uint32_t tid = threadIdx.x;
+    auto kld = [&](uint32_t i) {
+        const uint32_t c = tid + 256u * i, p = min(t0 + (c >> 4), kv_end - 1);
+        return *gh_gp<uint4>((uint64_t)(kc + (size_t)p * kv_row + (c & 15u) * 8));
+    };
+    s.k0 = kld(0);
+    s.k1 = kld(1);
+    s.k2 = kld(2);
+    s.k3 = kld(3);
+    const uint32_t lane = tid & 63u, dg = (lane >> 4) + 4 * (tid >> 6), kg = lane & 15u;
+    auto vld = [&](uint32_t i) {
+        const uint32_t p = min(t0 + 4 * kg + i, kv_end - 1);
+        return *gh_gp<uint4>((uint64_t)(vc + (size_t)p * kv_row + dg * 8));
+    };
+    s.v0 = vld(0);
+    s.v1 = vld(1);
+    s.v2 = vld(2);
+    s.v3 = vld(3);
+}
+
+__device__ __forceinline__ void kv_store(const KVStage& s, _Float16* kt, _Float16* vt) {
+    const uint32_t tid = threadIdx.x;
+    _Float16* kd = kt + (tid >> 4) * kKP + (tid & 15u) * 8;  // + 16 keys per i
+    *(uint4*)(kd) = s.k0;
+    *(uint4*)(kd + 16 * kKP) = s.k1;
+    *(uint4*)(kd + 32 * kKP) = s.k2;
+    *(uint4*)(kd + 48 * kKP) = s.k3;
+    // V transposed: dims 8·dg + e get the four keys 4·kg .. 4·kg + 3 as one 8-byte run
+    const uint32_t lane = tid & 63u, dg = (lane >> 4) + 4 * (tid >> 6), kg = lane & 15u;
+    const uint32_t r0[4] = {s.v0.x, s.v0.y, s.v0.z, s.v0.w};
+    const uint32_t r1[4] = {s.v1.x, s.v1.y, s.v1.z, s.v1.w};
+    const uint32_t r2[4] = {s.v2.x, s.v2.y, s.v2.z, s.v2.w};
+    const uint32_t r3[4] = {s.v3.x, s.v3.y, s.v3.z, s.v3.w};
+    _Float16* vd = vt + (dg * 8) * kVP + kg * 4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        *(uint2*)(vd + (2 * c) * kVP) = make_uint2(lo_pair(r0[c], r1[c]), lo_pair(r2[c], r3[c]));
+        *(uint2*)(vd + (2 * c + 1) * kVP) = make_uint2(hi_pair(r0[c], r1[c]), hi_pair(r2[c], r3[c]));
+    }
+}
+
+__device__ __forceinline__ float xor_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float xor_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+__device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
+    __shared__ __attribute__((aligned(16))) _Float16 kt[2][kPK * kKP];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][128 * kVP];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t nqb = (a.rows + kPQ - 1) / kPQ;
+    const uint32_t qb = nqb - 1 - blockIdx.x, kvh = blockIdx.y, h = kvh * 4 + wave;
+    const uint32_t q0 = qb * kPQ;
+    const uint32_t kv_end = a.base + min(q0 + kPQ, a.rows);  // keys 0 .. kv_end-1 are visible
+    const uint32_t ntiles = (kv_end + kPK - 1) / kPK;
+    const size_t kv_row = (size_t)a.kv_heads * 128;
+    const size_t cache0 = (size_t)a.layer * a.context * kv_row + (size_t)kvh * 128;
+    const uint16_t* kc = (const uint16_t*)a.kc + cache0;
+    const uint16_t* vc = (const uint16_t*)a.vc + cache0;
+    const uint32_t fr = lane & 15u, fg = lane >> 4;  // fragment row / lane group
+    const float sl2 = a.scale * 1.4426950408889634f;  // scores in base-2 units
+
+    // this wave's query rows as B operands: [q tile t][k step ks] = dims 32 ks + 8 fg .. + 8
+    ah8 qf[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t r = min(q0 + 16 * t + fr, a.rows - 1);
+        const GH_GLOBAL uint4* qp = gh_gp<uint4>(a.q + (((uint64_t)r * a.q_heads + h) * 128 + 8 * fg) * 2);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qf[t][ks] = __builtin_bit_cast(ah8, qp[4 * ks]);
+    }
+    const uint32_t qpos[2] = {a.base + q0 + fr, a.base + q0 + 16 + fr};
+
+    af4 o[8][2];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j][0] = o[j][1] = af4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[2] = {-__builtin_inff(), -__builtin_inff()}, l[2] = {0.0f, 0.0f};
+
+    KVStage st;
+    kv_load(a, kc, vc, kv_row, 0, kv_end, st);
+    kv_store(st, kt[0], vt[0]);
+    __syncthreads();
+    for (uint32_t tile = 0; tile < ntiles; ++tile) {
+        const uint32_t cur = tile & 1u, t0 = tile * kPK;
+        const bool more = tile + 1 < ntiles;
+        if (more) kv_load(a, kc, vc, kv_row, t0 + kPK, kv_end, st);
+        const _Float16* kb = kt[cur];
+        const _Float16* vb = vt[cur];
+        // S^T tiles: [key tile kk][q tile t], lane holds keys 16 kk + 4 fg + e of query fr
+        af4 s[4][2];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            s[kk][0] = s[kk][1] = af4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const ah8 kf = *(const ah8*)(kb + (16 * kk + fr) * kKP + 32 * ks + 8 * fg);
+                s[kk][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][ks], s[kk][0], 0, 0, 0);
+                s[kk][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][ks], s[kk][1], 0, 0, 0);
+            }
+        }
+        // online softmax per query row (lane), P as FP16 hi/lo B operands in key-slot order
+        ah8 ph[2][2], pl[2][2];  // [k step (keys 32 ks2 ..)][q tile]
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float v[4][4];
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t p = t0 + 16 * kk + 4 * fg + e;
+                    v[kk][e] = p <= qpos[t] ? s[kk][t][e] * sl2 : -__builtin_inff();
+                    mx = fmaxf(mx, v[kk][e]);
+                }
+            const float m_new = fmaxf(m[t], xor_max(mx));  // finite: key 0 is in tile 0
+            const float f = exp2f(m[t] - m_new);
+            m[t] = m_new;
+            float sum = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[kk][e] = exp2f(v[kk][e] - m_new);
+                    sum += v[kk][e];
+                }
+            l[t] = l[t] * f + sum;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j][t] *= f;
+#pragma unroll
+            for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float pv = v[2 * ks2 + (e >> 2)][e & 3];
+                    const _Float16 hi = (_Float16)pv;
+                    ph[ks2][t][e] = hi;
+                    pl[ks2][t][e] = (_Float16)(pv - (float)hi);
+                }
+        }
+        // O^T += V^T P^T: A = V^T rows (dims 16 j + fr), k-slots = keys 32 ks2 + {4 fg .. +3,
+        // 16 + 4 fg .. +3}, the same keys the lane's P values belong to
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int ks2 = 0; ks2 < 2; ++ks2) {
+                const _Float16* vr = vb + (16 * j + fr) * kVP + 32 * ks2 + 4 * fg;
+                const uint2 va = *(const uint2*)vr, vb2 = *(const uint2*)(vr + 16);
+                const ah8 vf = __builtin_bit_cast(ah8, make_uint4(va.x, va.y, vb2.x, vb2.y));
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    o[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[ks2][t], o[j][t], 0, 0, 0);
+                    o[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[ks2][t], o[j][t], 0, 0, 0);
+                }
+            }
+        if (more) kv_store(st, kt[cur ^ 1u], vt[cur ^ 1u]);
+        __syncthreads();
+    }
+    // O^T tile (j, t): lane holds dims 16 j + 4 fg + e of query row q0 + 16 t + fr
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t r = q0 + 16 * t + fr;
+        const float inv = 1.0f / xor_sum(l[t]);
+        if (r >= a.rows) continue;
+        GH_GLOBAL uint16_t* op = gh_gpw<uint16_t>(a.out) + ((size_t)r * a.q_heads + h) * 128 + 4 * fg;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w0 = (uint32_t)gh_f2h(o[j][t][0] * inv) | ((uint32_t)gh_f2h(o[j][t][1] * inv) << 16);
+            const uint32_t w1 = (uint32_t)gh_f2h(o[j][t][2] * inv) | ((uint32_t)gh_f2h(o[j][t][3] * inv) << 16);
+            *(GH_GLOBAL uint2*)(op + 16 * j) = make_uint2(w0, w1);
+        }
+    }
+}
+}  // namespace
+
+GH_KERNEL __launch_bounds__(256) void gh_attn_prefill_g4(GhAttnArgs a) { attn_prefill_g4(a); }

@@ -1,0 +1,128 @@
+"""Prefill attention on the matrix cores (gh_attention_prefill with n >= 32 rows, G = 4)
+against the oracle, and against the reference's own prefill-attention test vectors.
+
+Bars:
+  * oracle (attention/mod.rs:582-725 restated): |got - want| <= 1e-3·|want| + 1e-5 — outputs
+    are convex combinations of V rows; P·V runs with FP16 hi + lo probabilities, so the only
+    FP16 rounding left is the output's (2^-11 relative);
+  * the reference's Vulkan prefill test (vulkan/mod.rs:935-1110): its q/k/v generators, shapes
+    (q_heads 4, kv_heads 1, head_dim 128; contexts 2048 / 8192 / 28000, n = 64 / 32 / 16 at the
+    end of the context) and its bar |got - want| <= 2e-2 + 2e-2·|want| (vulkan/mod.rs:1245-1258),
+    against both the per-row decode path and the CPU softmax.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from graph_horizon_amd import _ffi as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _kv(hip, layers, ctx, kvh, kc, vc):
+    return F.GhKv(hip.from_host(kc), hip.from_host(vc), F.KV_F16, layers, ctx, kvh, 128, 128)
+
+
+def _free(hip, *bufs):
+    for b in bufs:
+        hip.free_buffer(b)
+
+
+def _close(got, want, what, rel=1e-3, floor=1e-5):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    tol = rel * np.abs(want) + floor
+    bad = np.abs(got - want) > tol
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} outside, worst " \
+        f"{np.max(np.abs(got - want) / tol):.3f}x tol"
+
+
+@pytest.mark.parametrize("ctx,base,n,layer", [
+    (512, 0, 32, 0),      # one query block, first tile only
+    (512, 0, 100, 1),     # ragged rows
+    (1024, 300, 200, 1),  # base inside a key tile, query blocks straddling tiles
+    (2048, 0, 512, 0),    # the model's prefill chunk
+    (4096, 4000, 96, 1),  # late chunk of a long context
+])
+def test_prefill_attention_matches_oracle(hip, ctx, base, n, layer):
+    rng = np.random.default_rng(ctx + base + n)
+    layers, qh, kvh = 2, 32, 8
+    kc = O.f16(rng.standard_normal(layers * ctx * kvh * 128).astype(np.float32))
+    vc = O.f16(rng.standard_normal(layers * ctx * kvh * 128).astype(np.float32))
+    q = O.f16(rng.standard_normal(n * qh * 128).astype(np.float32))
+    kv = _kv(hip, layers, ctx, kvh, kc, vc)
+    qb, ob = hip.from_host(q), hip.alloc_buffer(n * qh * 128 * 2)
+    hip.attention_prefill(ob, qb, kv, qh, base, n, layer)
+    got = O.f32(hip.download(ob, np.uint16, n * qh * 128))
+    want = O.f32(O.attention_prefill(q, kc, vc, 128, kvh, qh, base, n, layer, ctx))
+    assert np.isfinite(got).all()
+    _close(got, want, f"ctx {ctx} base {base} n {n}")
+    _free(hip, qb, ob, kv.k, kv.v)
+
+
+def test_prefill_attention_c4_2048(hip):
+    """BASELINE config 4 prefill: 2048 causal rows, 32 q / 8 kv heads, head_dim 128; 48 rows
+    (first, last and spread) checked against the oracle's decode of that row (prefill row r ==
+    decode at base + r, attention/mod.rs:920-1024)."""
+    n, ctx, qh, kvh = 2048, 2048, 32, 8
+    rng = np.random.default_rng(2048)
+    kc = O.f16(rng.standard_normal(ctx * kvh * 128).astype(np.float32))
+    vc = O.f16(rng.standard_normal(ctx * kvh * 128).astype(np.float32))
+    q = O.f16(rng.standard_normal(n * qh * 128).astype(np.float32))
+    kv = _kv(hip, 1, ctx, kvh, kc, vc)
+    qb, ob = hip.from_host(q), hip.alloc_buffer(n * qh * 128 * 2)
+    hip.attention_prefill(ob, qb, kv, qh, 0, n, 0)
+    got = O.f32(hip.download(ob, np.uint16, n * qh * 128)).reshape(n, qh * 128)
+    assert np.isfinite(got).all()
+    rows = sorted(set([0, 1, 31, 32, 63, 64, 1023, 2046, 2047] + list(rng.integers(0, n, 39))))
+    for r in rows:
+        want = O.f32(O.attention_decode(q[r * qh * 128:(r + 1) * qh * 128], kc, vc, 128, kvh, qh,
+                                        r, 0, ctx))
+        _close(got[r], want, f"row {r}")
+    _free(hip, qb, ob, kv.k, kv.v)
+
+
+def _reference_case(ctx_total):
+    """attention_prefill_decode_for_scheme inputs (vulkan/mod.rs:955-1000), one layer."""
+    qh, hd = 4, 128
+    pos = np.arange(ctx_total)[:, None]
+    i = np.arange(hd)[None, :]
+    k = (((pos * 7 + i) % 13).astype(np.float32) * np.float32(0.025) - np.float32(0.12))
+    v = (((pos * 11 + i) % 19).astype(np.float32) * np.float32(0.02) - np.float32(0.15))
+    return qh, O.f16(k.reshape(-1)), O.f16(v.reshape(-1))
+
+
+@pytest.mark.parametrize("context", [2048, 8192, 28000])
+def test_reference_prefill_attention_vectors(hip, context):
+    qh, kc, vc = _reference_case(context)
+    kv = _kv(hip, 1, context, 1, kc, vc)
+    for n in (64, 32, 16):  # n = 16 runs the per-row split-K path
+        base = context - n
+        idx = np.arange(n * qh * 128)
+        q = O.f16(((idx % 17).astype(np.float32) * np.float32(0.03) - np.float32(0.22)))
+        qb, pb, db = hip.from_host(q), hip.alloc_buffer(q.nbytes), hip.alloc_buffer(q.nbytes)
+        hip.attention_prefill(pb, qb, kv, qh, base, n, 0)
+        for r in range(n):
+            qr = hip.view(qb, r * qh * 256, qh * 256)
+            dr = hip.view(db, r * qh * 256, qh * 256)
+            hip.attention_decode(dr, qr, kv, qh, base + r, 0)
+        got_p = O.f32(hip.download(pb, np.uint16, q.size)).astype(np.float64)
+        got_d = O.f32(hip.download(db, np.uint16, q.size)).astype(np.float64)
+        # CPU softmax in fp64 over the FP16 inputs (the reference test's own CPU oracle)
+        kf = O.f32(kc).astype(np.float64).reshape(context, 128)
+        vf = O.f32(vc).astype(np.float64).reshape(context, 128)
+        qf = O.f32(q).astype(np.float64).reshape(n, qh, 128)
+        cpu = np.empty((n, qh, 128))
+        for r in range(n):
+            s = qf[r] @ kf[:base + r + 1].T / np.sqrt(128.0)
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            cpu[r] = (p / p.sum(axis=1, keepdims=True)) @ vf[:base + r + 1]
+        cpu = cpu.reshape(-1)
+        for what, a, b in (("prefill vs decode", got_p, got_d), ("prefill vs cpu", got_p, cpu),
+                           ("decode vs cpu", got_d, cpu)):
+            err = np.abs(a - b)
+            ok = err <= 2e-2 + 2e-2 * np.abs(b)
+            assert ok.all(), f"ctx {context} n {n} {what}: {(~ok).sum()} outside"
+            # and the repository's own bar on the same data
+            _close(a, b, f"ctx {context} n {n} {what}", rel=1e-3, floor=1e-5)
+        _free(hip, qb, pb, db)
+    _free(hip, kv.k, kv.v)
