@@ -245,8 +245,16 @@ int op_kv_write(gh_backend* b, const gh_kv* kv, const gh_buf* k, const gh_buf* v
 }
 
 // Workgroups per (row, kv head): one per 64-position chunk up to 32; longer contexts loop.
-uint32_t attention_splits(uint32_t max_len) {
-    return std::min<uint32_t>(ceil_div(max_len, 64), 32);
+// Workgroups per (row, kv head): enough that rows x kv heads x splits covers about two
+// workgroups per CU, at most one per 64-position chunk and at most 32 (the merge's limit).
+uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows) {
+    static const uint32_t forced = [] {
+        const char* e = std::getenv("GH_ATTN_SPLITS");
+        return e ? (uint32_t)std::atoi(e) : 0u;
+    }();
+    const uint32_t chunks = ceil_div(max_len, 64);
+    const uint32_t want = forced ? forced : ceil_div(2 * std::max(b->cus, 1u), std::max(kv_heads * rows, 1u));
+    return std::max<uint32_t>(1, std::min<uint32_t>({want, chunks, 32u}));
 }
 
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits) {
@@ -307,7 +315,7 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.scale = 1.0f / std::sqrt((float)kv->head_dim);
         return launch(b, K_ATTN_PREFILL_G4, ceil_div(rows, 32), kv->kv_heads, 1, 256, &a);
     }
-    const uint32_t splits = attention_splits(max_pos + 1);
+    const uint32_t splits = attention_splits(b, max_pos + 1, kv->kv_heads, rows);
     // bound the partials: rows in groups that fit a 256 MiB workspace
     const size_t per_row = attention_workspace(1, q_heads, splits);
     uint32_t group_rows = (uint32_t)std::max<size_t>(1, ((size_t)256 << 20) / per_row);

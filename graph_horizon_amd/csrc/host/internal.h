@@ -108,7 +108,7 @@ struct GemvSeg {
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
             uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up);
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
-uint32_t attention_splits(uint32_t max_len);
+uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows);
 int ensure_counters(gh_backend* b, size_t slots);
 }  // namespace gh
 

@@ -218,7 +218,7 @@ int gh_model_create(gh_backend* b, const gh_model_config* cfg, gh_model** out) {
     if (!rc) rc = alloc(m, (uint64_t)c.kv_context * 4, &m->history);
     if (!rc) rc = ensure_rope(b, &c.yarn, c.kv_context);
     // partials for a decode step and for one prefill chunk
-    const uint32_t dsplits = attention_splits(c.kv_context);
+    const uint32_t dsplits = attention_splits(b, c.kv_context, c.kv_head_count, 1);
     if (!rc) rc = ensure_workspace(b, attention_workspace(1, c.head_count, dsplits));
     if (!rc) rc = ensure_counters(b, c.kv_head_count);
     if (rc) {

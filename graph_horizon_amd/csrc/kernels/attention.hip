@@ -2,16 +2,20 @@
 //
 // Grid (splits, kv_heads, rows); 256 threads. A workgroup takes one kv head, the G =
 // q_heads/kv_heads query heads sharing it (each K/V row is read once for all G), and every
-// nsplit-th chunk of 64 positions of one query row (pos_r = base + r, or *pos_ptr + base + r):
+// nsplit-th chunk of 64 positions of one query row (pos_r = base + r, or *pos_ptr + base + r).
+// Wave w owns positions 16 w .. 16 w + 15 of each chunk and keeps its own online-softmax
+// state, so chunks need no workgroup barrier:
 //   scores  4 lanes per position, 32 FP16 of the K row each, v_dot2_f32_f16 against the FP16
 //           query (products of FP16 values are exact in FP32), quad DPP sum, x 1/sqrt(128);
-//   online softmax per head across the workgroup's chunks: running max m, Σe l, Σe·V acc
-//           (each lane owns 2 value dims; waves split the positions of a chunk).
-// The workgroup's (m, l, acc) goes to the workspace; the last workgroup of a (row, kv head)
-// to finish (agent-scope atomic counter, which it resets for the next launch) merges them:
+//   softmax running max m, Σe l, Σe·V acc per head (each lane owns 2 value dims; the weights
+//           of the wave's 16 positions are broadcast with v_readlane).
+// The next chunk's K/V loads are issued before the current chunk is computed. At the end the
+// four waves merge in LDS; with one split the workgroup writes the output, otherwise it writes
+// (m, l, acc) to the workspace and the last workgroup of its (row, kv head) (agent-scope atomic
+// counter, reset by that workgroup for the next launch) merges the splits:
 //   out = Σ_s e^{m_s-M} acc_s / Σ_s e^{m_s-M} l_s,  M = max_s m_s
 // — the reference's three-pass softmax-weighted V sum (attention/mod.rs:220-258), re-associated.
-// head_dim = value_dim = 128; splits <= 32.
+// head_dim = value_dim = 128; splits <= kMaxSplits.
 #include "gh_common.h"
 
 namespace {
@@ -20,127 +24,158 @@ constexpr int kWaves = 4;
 constexpr uint32_t kMaxSplits = 32;
 
 template <int G>
+struct ChunkRegs {
+    uint4 k[4];       // K row of position 16·wave + lane/4, dims 32·(lane%4) .. +32
+    uint32_t v[16];   // V dims 2·lane, 2·lane+1 of positions 16·wave + i
+};
+
+template <int G>
+__device__ __forceinline__ void load_chunk(const uint16_t* kc, const uint16_t* vc, size_t kv_row,
+                                           uint32_t c, uint32_t len, ChunkRegs<G>& r) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t p0 = c * kChunk + wave * 16;
+    const uint32_t pk = min(p0 + (lane >> 2), len - 1);
+    const GH_GLOBAL uint4* src = gh_gp<uint4>((uint64_t)(kc + (size_t)pk * kv_row + (lane & 3u) * 32));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.k[i] = src[i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t pv = min(p0 + (uint32_t)i, len - 1);
+        r.v[i] = gh_gp<uint32_t>((uint64_t)(vc + (size_t)pv * kv_row))[lane];
+    }
+}
+
+template <int G>
+__device__ __forceinline__ void chunk_step(const ChunkRegs<G>& r, const uint4 (&qv)[G][4], float scale,
+                                           uint32_t c, uint32_t len, float (&m)[G], float (&l)[G],
+                                           float (&acc)[G][2]) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t pos = c * kChunk + wave * 16 + (lane >> 2);
+    const bool valid = pos < len;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s = gh_dot2(qv[h][i].x, r.k[i].x, s);
+            s = gh_dot2(qv[h][i].y, r.k[i].y, s);
+            s = gh_dot2(qv[h][i].z, r.k[i].z, s);
+            s = gh_dot2(qv[h][i].w, r.k[i].w, s);
+        }
+        s += GH_DPP(s, 0xB1, 0xF);  // quad_perm [1,0,3,2]
+        s += GH_DPP(s, 0x4E, 0xF);  // quad_perm [2,3,0,1]
+        s = valid ? s * scale : -__builtin_inff();
+        // max over the wave's 16 positions: rotate by 4 and 8 within each 16-lane row, then
+        // the four rows' maxima through SGPRs
+        float mx = fmaxf(s, GH_DPP(s, 0x124, 0xF));  // row_ror:4
+        mx = fmaxf(mx, GH_DPP(mx, 0x128, 0xF));      // row_ror:8
+        mx = fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0)),
+                         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16))),
+                   fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32)),
+                         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 48))));
+        const float m_new = fmaxf(m[h], mx);  // finite: the wave's first position is valid
+        const float f = m_new == -__builtin_inff() ? 1.0f : expf(m[h] - m_new);
+        const float p = valid ? expf(s - m_new) : 0.0f;
+        m[h] = m_new;
+        l[h] = l[h] * f + ((lane & 3u) == 0 ? p : 0.0f);  // per-lane partial of Σe
+        float a0 = acc[h][0] * f, a1 = acc[h][1] * f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float pi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 4 * i));
+            a0 += pi * gh_h2f(r.v[i] & 0xFFFFu);
+            a1 += pi * gh_h2f(r.v[i] >> 16);
+        }
+        acc[h][0] = a0;
+        acc[h][1] = a1;
+    }
+}
+
+template <int G>
 __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
-    __shared__ float sc[G][kChunk];
-    __shared__ float stat[G][2];  // per head: running max, rescale factor of this chunk
-    __shared__ float red[kWaves][G][128];
+    __shared__ float wm[kWaves][G], wl[kWaves][G];
+    __shared__ float wacc[kWaves][G][128];
     __shared__ float wsplit[G][kMaxSplits];
     __shared__ uint32_t last;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
+    const uint32_t h0 = kvh * G;
+    // FP16 query slices [32·qd, +32) of the G heads, as 16 pairs each (issued before the
+    // position is known)
+    uint4 qv[G][4];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const GH_GLOBAL uint4* qp =
+            gh_gp<uint4>(a.q + (((uint64_t)row * a.q_heads + h0 + h) * 128 + (lane & 3u) * 32) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[h][i] = qp[i];
+    }
     const uint32_t pos = (a.pos_ptr ? *gh_gp<uint32_t>(a.pos_ptr) : 0u) + a.base + row;
     const uint32_t len = pos + 1;
     const uint32_t nchunk = (len + kChunk - 1) / kChunk;
     const uint32_t nsplit = min(nchunk, a.splits);
     if (split >= nsplit) return;  // fixed grids (replayed graphs) may exceed the causal range
-    const uint32_t h0 = kvh * G;
     const size_t kv_row = (size_t)a.kv_heads * 128;
     const size_t cache0 = (size_t)a.layer * a.context * kv_row + (size_t)kvh * 128;
     const uint16_t* kc = (const uint16_t*)a.kc + cache0;
     const uint16_t* vc = (const uint16_t*)a.vc + cache0;
-    const uint32_t qd = lane & 3u;
-    const uint32_t pl = wave * 16 + (lane >> 2);  // this lane's position within a chunk (scores)
 
-    // FP16 query slices [32·qd, +32) of the G heads, as 16 pairs each
-    uint4 qv[G][4];
+    float m[G], l[G], acc[G][2];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const GH_GLOBAL uint4* qp =
-            gh_gp<uint4>(a.q + (((uint64_t)row * a.q_heads + h0 + h) * 128 + qd * 32) * 2);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qv[h][i] = qp[i];
-    }
-    float m_run[G], l_run[G], acc[G][2];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        m_run[h] = -__builtin_inff();
-        l_run[h] = 0.0f;
+        m[h] = -__builtin_inff();
+        l[h] = 0.0f;
         acc[h][0] = acc[h][1] = 0.0f;
     }
-
-    for (uint32_t c = split; c < nchunk; c += nsplit) {
-        const uint32_t t0 = c * kChunk;
-        const uint32_t n = min(len - t0, kChunk);
-        // issue this chunk's K (4 x 16 B per lane) and V (16 dwords per lane) loads together
-        uint4 kr[4];
-        {
-            const GH_GLOBAL uint4* src =
-                gh_gp<uint4>((uint64_t)(kc + (size_t)(t0 + min(pl, n - 1)) * kv_row + qd * 32));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) kr[i] = src[i];
-        }
-        uint32_t vv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t pp = min(wave + 4 * (uint32_t)i, n - 1);
-            vv[i] = gh_gp<uint32_t>((uint64_t)(vc + (size_t)(t0 + pp) * kv_row))[lane];
-        }
-        // scores
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                s = gh_dot2(qv[h][i].x, kr[i].x, s);
-                s = gh_dot2(qv[h][i].y, kr[i].y, s);
-                s = gh_dot2(qv[h][i].z, kr[i].z, s);
-                s = gh_dot2(qv[h][i].w, kr[i].w, s);
-            }
-            s += GH_DPP(s, 0xB1, 0xF);  // quad_perm [1,0,3,2]
-            s += GH_DPP(s, 0x4E, 0xF);  // quad_perm [2,3,0,1]
-            if (qd == 0 && pl < n) sc[h][pl] = s * a.scale;
-        }
-        __syncthreads();
-        // chunk max and exponentials, one wave per head
-        for (uint32_t h = wave; h < (uint32_t)G; h += kWaves) {
-            const float v = lane < n ? sc[h][lane] : -__builtin_inff();
-            const float m_new = fmaxf(m_run[h], gh_wave_max(v));
-            if (lane < n) sc[h][lane] = expf(v - m_new);
-            if (lane == 0) {
-                stat[h][0] = m_new;
-                stat[h][1] = expf(m_run[h] - m_new);  // 0 on the first chunk
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float f = stat[h][1];
-            m_run[h] = stat[h][0];
-            float e_sum = 0.0f;
-            acc[h][0] *= f;
-            acc[h][1] *= f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t pp = wave + 4 * (uint32_t)i;
-                if (pp < n) {
-                    const float e = sc[h][pp];
-                    acc[h][0] += e * gh_h2f(vv[i] & 0xFFFFu);
-                    acc[h][1] += e * gh_h2f(vv[i] >> 16);
-                }
-            }
-            for (uint32_t pp = lane; pp < n; pp += 64) e_sum += sc[h][pp];
-            l_run[h] = l_run[h] * f + gh_wave_sum(e_sum);
-        }
-        __syncthreads();  // sc is rewritten by the next chunk
+    // chunks split, split + nsplit, ...; a wave whose 16 positions of a chunk all lie past
+    // the row's length still runs it (every weight is 0) so the loop stays wave-uniform
+    ChunkRegs<G> ra, rb;
+    load_chunk<G>(kc, vc, kv_row, split, len, ra);
+    for (uint32_t c = split; c < nchunk; c += 2 * nsplit) {
+        const uint32_t c1 = c + nsplit, c2 = c + 2 * nsplit;
+        load_chunk<G>(kc, vc, kv_row, min(c1, nchunk - 1), len, rb);
+        if (c * kChunk + wave * 16 < len) chunk_step<G>(ra, qv, a.scale, c, len, m, l, acc);
+        if (c1 >= nchunk) break;
+        load_chunk<G>(kc, vc, kv_row, min(c2, nchunk - 1), len, ra);
+        if (c1 * kChunk + wave * 16 < len) chunk_step<G>(rb, qv, a.scale, c1, len, m, l, acc);
     }
 
-    // this workgroup's partial: (m, l) per head, acc summed over the waves
+    // merge the four waves: M = max m_w, L = Σ l_w e^{m_w - M}, ACC = Σ acc_w e^{m_w - M}
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        red[wave][h][2 * lane] = acc[h][0];
-        red[wave][h][2 * lane + 1] = acc[h][1];
+        const float lt = gh_wave_sum(l[h]);
+        if (lane == 0) {
+            wm[wave][h] = m[h];
+            wl[wave][h] = lt;
+        }
+        wacc[wave][h][2 * lane] = acc[h][0];
+        wacc[wave][h][2 * lane + 1] = acc[h][1];
     }
     __syncthreads();
+    const size_t pbase = ((size_t)row * a.q_heads + h0) * a.splits;
     for (uint32_t i = tid; i < (uint32_t)G * 128; i += blockDim.x) {
         const uint32_t h = i >> 7, d = i & 127u;
-        const float v = (red[0][h][d] + red[1][h][d]) + (red[2][h][d] + red[3][h][d]);
-        const size_t pi = ((size_t)row * a.q_heads + h0 + h) * a.splits + split;
-        gh_gpw<float>(a.part_acc)[pi * 128 + d] = v;
-        if (d == 0) {
-            gh_gpw<float>(a.part_m)[pi] = m_run[h];
-            gh_gpw<float>(a.part_l)[pi] = l_run[h];
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w][h]);
+        float L = 0.0f, v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float e = wm[w][h] == -__builtin_inff() ? 0.0f : expf(wm[w][h] - M);
+            L += e * wl[w][h];
+            v += e * wacc[w][h][d];
+        }
+        if (nsplit == 1) {
+            gh_gpw<uint16_t>(a.out)[((size_t)row * a.q_heads + h0 + h) * 128 + d] = gh_f2h(v / L);
+        } else {
+            const size_t pi = pbase + (size_t)h * a.splits + split;
+            gh_gpw<float>(a.part_acc)[pi * 128 + d] = v;
+            if (d == 0) {
+                gh_gpw<float>(a.part_m)[pi] = M;
+                gh_gpw<float>(a.part_l)[pi] = L;
+            }
         }
     }
+    if (nsplit == 1) return;
 
     // the last workgroup of this (row, kv head) merges the splits
     __syncthreads();
@@ -154,28 +189,48 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
     __syncthreads();
     if (!last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // weights e^{m_s - M} per (head, split), and L = Σ_s w_s l_s
+    // every partial this workgroup needs is requested before any is used (indexes past
+    // nsplit re-read split nsplit - 1 and get weight 0)
+    constexpr uint32_t kOut = (uint32_t)G * 128 / 256;  // outputs per thread (G >= 2)
+    float pv[kOut > 0 ? kOut : 1][kMaxSplits];
+#pragma unroll
+    for (uint32_t o = 0; o < kOut; ++o) {
+        const uint32_t i = tid + 256 * o, h = i >> 7, d = i & 127u;
+        const GH_GLOBAL float* pa = gh_gp<float>(a.part_acc) + (pbase + (size_t)h * a.splits) * 128 + d;
+#pragma unroll
+        for (uint32_t j = 0; j < kMaxSplits; ++j) pv[o][j] = pa[(size_t)min(j, nsplit - 1) * 128];
+    }
+    // weights e^{m_s - M} / L per (head, split): lanes are splits, wave h handles head h
     for (uint32_t h = wave; h < (uint32_t)G; h += kWaves) {
-        const size_t base = ((size_t)row * a.q_heads + h0 + h) * a.splits;
-        const float ms = lane < nsplit ? gh_gp<float>(a.part_m)[base + lane] : -__builtin_inff();
-        const float M = gh_wave_max(ms);
+        const size_t base = pbase + (size_t)h * a.splits;
+        const uint32_t s2 = min(lane, nsplit - 1);
+        const float ms = gh_gp<float>(a.part_m)[base + s2];
+        const float ls = gh_gp<float>(a.part_l)[base + s2];
+        const float M = gh_wave_max(lane < nsplit ? ms : -__builtin_inff());
         const float w = lane < nsplit ? expf(ms - M) : 0.0f;
-        const float L = gh_wave_sum(lane < nsplit ? w * gh_gp<float>(a.part_l)[base + lane] : 0.0f);
-        if (lane < nsplit) wsplit[h][lane] = w / L;
+        const float L = gh_wave_sum(w * ls);
+        if (lane < kMaxSplits) wsplit[h][lane] = w / L;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < (uint32_t)G * 128; i += blockDim.x) {
-        const uint32_t h = i >> 7, d = i & 127u;
-        const size_t base = ((size_t)row * a.q_heads + h0 + h) * a.splits;
-        const GH_GLOBAL float* pa = gh_gp<float>(a.part_acc) + base * 128 + d;
-        float pv[kMaxSplits];
+    if constexpr (kOut > 0) {
 #pragma unroll
-        for (uint32_t s2 = 0; s2 < kMaxSplits; ++s2) pv[s2] = s2 < nsplit ? pa[(size_t)s2 * 128] : 0.0f;
-        float o = 0.0f;
+        for (uint32_t o = 0; o < kOut; ++o) {
+            const uint32_t i = tid + 256 * o, h = i >> 7, d = i & 127u;
+            float acc_o = 0.0f;
 #pragma unroll
-        for (uint32_t s2 = 0; s2 < kMaxSplits; ++s2)
-            if (s2 < nsplit) o += wsplit[h][s2] * pv[s2];
-        gh_gpw<uint16_t>(a.out)[((size_t)row * a.q_heads + h0 + h) * 128 + d] = gh_f2h(o);
+            for (uint32_t j = 0; j < kMaxSplits; ++j) acc_o += wsplit[h][j] * pv[o][j];
+            gh_gpw<uint16_t>(a.out)[((size_t)row * a.q_heads + h0 + h) * 128 + d] = gh_f2h(acc_o);
+        }
+    } else {
+        // G = 1: 128 outputs, threads 0..127
+        if (tid < 128) {
+            const GH_GLOBAL float* pa = gh_gp<float>(a.part_acc) + pbase * 128 + tid;
+            float acc_o = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < kMaxSplits; ++j)
+                acc_o += wsplit[0][j] * pa[(size_t)min(j, nsplit - 1) * 128];
+            gh_gpw<uint16_t>(a.out)[((size_t)row * a.q_heads + h0) * 128 + tid] = gh_f2h(acc_o);
+        }
     }
 }
 
