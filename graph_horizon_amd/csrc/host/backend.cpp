@@ -28,6 +28,10 @@ const KernelName kKernels[] = {
     {K_GEMV_Q6K_R2, "gh_gemv_q6k_r2"},     {K_GEMV_Q6K_R4, "gh_gemv_q6k_r4"},
     {K_GEMV_MIXED_R2, "gh_gemv_mixed_r2"}, {K_GEMV_SWIGLU_R1, "gh_gemv_swiglu_r1"},
     {K_GEMV_SWIGLU_R2, "gh_gemv_swiglu_r2"},
+    {K_GEMV_Q4K_R1_N, "gh_gemv_q4k_r1_n"}, {K_GEMV_Q4K_R2_N, "gh_gemv_q4k_r2_n"},
+    {K_GEMV_Q6K_R1_N, "gh_gemv_q6k_r1_n"}, {K_GEMV_Q6K_R2_N, "gh_gemv_q6k_r2_n"},
+    {K_GEMV_MIXED_R2_N, "gh_gemv_mixed_r2_n"},
+    {K_GEMV_SWIGLU_R1_N, "gh_gemv_swiglu_r1_n"}, {K_GEMV_SWIGLU_R2_N, "gh_gemv_swiglu_r2_n"},
     {K_RMSNORM, "gh_rmsnorm_x"},           {K_ROPE, "gh_rope"},
     {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
     {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
@@ -402,7 +406,8 @@ uint32_t resident_wgs(gh_backend* b, GhKernel k, uint32_t block, uint32_t shmem)
 }
 
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
-            uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up) {
+            uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up,
+            const gh_buf* norm, float eps) {
     if (nseg == 0 || nseg > 3) return fail(b, GH_E_INVALID, "gemv: 1..3 segments");
     GhGemvArgs a{};
     const uint32_t in_dim = segs[0].w->cols;
@@ -422,6 +427,7 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
                 return fail(b, GH_E_INVALID, "gemv: fused epilogues are single-token");
     uint32_t r = gemv_rows(total_rows);
     if (rope || mixed) r = 2;  // RoPE needs row pairs; the mixed kernel is compiled for R = 2
+    if (norm) r = std::min<uint32_t>(r, 2);  // the RMSNorm variants exist for R = 1, 2
     GhKernel k;
     if (swiglu) {
         if (nseg != 1 || !up || up->format != GH_FMT_Q4_K || segs[0].w->format != GH_FMT_Q4_K ||
@@ -437,6 +443,18 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     } else {
         k = r == 4 ? K_GEMV_Q6K_R4 : r == 2 ? K_GEMV_Q6K_R2 : K_GEMV_Q6K_R1;
     }
+    if (norm) {
+        switch (k) {
+            case K_GEMV_Q4K_R1: k = K_GEMV_Q4K_R1_N; break;
+            case K_GEMV_Q4K_R2: k = K_GEMV_Q4K_R2_N; break;
+            case K_GEMV_Q6K_R1: k = K_GEMV_Q6K_R1_N; break;
+            case K_GEMV_Q6K_R2: k = K_GEMV_Q6K_R2_N; break;
+            case K_GEMV_MIXED_R2: k = K_GEMV_MIXED_R2_N; break;
+            case K_GEMV_SWIGLU_R1: k = K_GEMV_SWIGLU_R1_N; break;
+            case K_GEMV_SWIGLU_R2: k = K_GEMV_SWIGLU_R2_N; break;
+            default: return fail(b, GH_E_UNSUPPORTED, "gemv: no RMSNorm variant");
+        }
+    }
     uint32_t task = 0;
     for (uint32_t i = 0; i < nseg; ++i) {
         a.seg[i].w = segs[i].w->addr;
@@ -448,6 +466,12 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
         task += ceil_div(segs[i].w->rows, r);
     }
     a.x = x->addr;
+    if (norm) {
+        if (norm->format != GH_FMT_F16 || norm->bytes < (uint64_t)in_dim * 2 || in_dim % 8 || in_dim > 8192)
+            return fail(b, GH_E_INVALID, "gemv: fused norm needs an F16[in_dim] weight and in_dim <= 8192");
+        a.norm_w = norm->addr;
+        a.eps = eps;
+    }
     a.table = (uint64_t)b->rope.table;
     a.post = (uint64_t)b->rope.post;
     a.pos_ptr = (uint64_t)pos_ptr;
@@ -462,7 +486,8 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     if (in_dim / 64 > 256) return fail(b, GH_E_UNSUPPORTED, "gemv: in_dim above 16384");
     // x staged once per workgroup in LDS (144 B per 64-weight unit; both layouts if mixed);
     // the persistent grid (at most what is resident at once) loops its waves over the tasks.
-    const uint32_t shmem = (in_dim / 64) * 144 * (mixed ? 2 : 1);
+    // + the normalized FP16 row and 16 bytes of reduction scratch when RMSNorm is fused
+    const uint32_t shmem = (in_dim / 64) * 144 * (mixed ? 2 : 1) + (norm ? in_dim * 2 + 16 : 0);
     static const uint32_t max_wg = [] {
         const char* e = std::getenv("GH_GEMV_MAX_WG");
         return e ? (uint32_t)std::atoi(e) : 0u;
@@ -776,7 +801,7 @@ int gh_rmsnorm_x(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf
         return latch(enc, fail(b, GH_E_RANGE, "rmsnorm_x: buffer too small"));
     if (dim % 4) return latch(enc, fail(b, GH_E_INVALID, "rmsnorm_x: dim must be a multiple of 4"));
     GhRmsnormArgs a{out->addr, x->addr, w->addr, dim, rows, eps, 0};
-    return latch(enc, launch(b, K_RMSNORM, rows, 1, 1, 1024, &a));
+    return latch(enc, launch(b, K_RMSNORM, rows, 1, 1, 256, &a));
 }
 
 int gh_rope_yarn(gh_backend* b, gh_encoder* enc, const gh_buf* x, uint32_t heads,

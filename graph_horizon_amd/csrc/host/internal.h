@@ -24,6 +24,14 @@ enum GhKernel : int {
     K_GEMV_MIXED_R2,
     K_GEMV_SWIGLU_R1,
     K_GEMV_SWIGLU_R2,
+    // RMSNorm-staging variants (same order as the seven kernels they extend)
+    K_GEMV_Q4K_R1_N,
+    K_GEMV_Q4K_R2_N,
+    K_GEMV_Q6K_R1_N,
+    K_GEMV_Q6K_R2_N,
+    K_GEMV_MIXED_R2_N,
+    K_GEMV_SWIGLU_R1_N,
+    K_GEMV_SWIGLU_R2_N,
     K_RMSNORM,
     K_ROPE,
     K_SILU_MUL,
@@ -105,8 +113,10 @@ struct GemvSeg {
     uint64_t out;
     uint32_t epi;
 };
+// norm: x is the FP32 residual and rmsnorm_x(norm, eps) is applied while staging it.
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
-            uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up);
+            uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up,
+            const gh_buf* norm = nullptr, float eps = 0.0f);
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
 uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows);
 int ensure_counters(gh_backend* b, size_t slots);

@@ -84,23 +84,24 @@ int layer_decode_fused(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t 
     gh_backend* b = m->b;
     const gh_model_config& c = m->cfg;
     const auto& w = m->layers[li];
-    const uint32_t d = c.embedding_length;
     const uint64_t kv_row_k = (uint64_t)c.kv_head_count * c.key_length;
     const uint64_t kv_row_v = (uint64_t)c.kv_head_count * c.value_length;
     const uint64_t kbase = m->kv.k.addr + (uint64_t)li * m->kv.context * kv_row_k * 2;
     const uint64_t vbase = m->kv.v.addr + (uint64_t)li * m->kv.context * kv_row_v * 2;
-    int rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_ATTN_NORM], d, c.rms_epsilon, 1);
+    // attention RMSNorm fused into the QKV launch's staging of x
     const GemvSeg qkv[3] = {{&w[GH_T_ATTN_Q], s.q.addr, GH_EPI_ROPE},
                             {&w[GH_T_ATTN_K], kbase, GH_EPI_ROPE_CACHE},
                             {&w[GH_T_ATTN_V], vbase, GH_EPI_CACHE}};
-    if (!rc) rc = op_gemv(b, qkv, 3, &s.normed, 1, base, pos_ptr, c.key_length, nullptr);
+    int rc = op_gemv(b, qkv, 3, &s.x, 1, base, pos_ptr, c.key_length, nullptr, &w[GH_T_ATTN_NORM],
+                     c.rms_epsilon);
     const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base;
     if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, 1, li, pos_ptr, max_pos);
     const GemvSeg o{&w[GH_T_ATTN_OUTPUT], s.x.addr, GH_EPI_RESID};
     if (!rc) rc = op_gemv(b, &o, 1, &s.attn, 1, 0, nullptr, 0, nullptr);
-    if (!rc) rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_FFN_NORM], d, c.rms_epsilon, 1);
+    // FFN RMSNorm fused into the gate/up launch
     const GemvSeg gu{&w[GH_T_FFN_GATE], s.act.addr, GH_EPI_SWIGLU};
-    if (!rc) rc = op_gemv(b, &gu, 1, &s.normed, 1, 0, nullptr, 0, &w[GH_T_FFN_UP]);
+    if (!rc) rc = op_gemv(b, &gu, 1, &s.x, 1, 0, nullptr, 0, &w[GH_T_FFN_UP], &w[GH_T_FFN_NORM],
+                          c.rms_epsilon);
     const GemvSeg dn{&w[GH_T_FFN_DOWN], s.x.addr, GH_EPI_RESID};
     if (!rc) rc = op_gemv(b, &dn, 1, &s.act, 1, 0, nullptr, 0, nullptr);
     return latch_rc(enc, rc);
@@ -154,12 +155,20 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
 }
 
 // tail::record_buffers (tail.rs:22-59): output_norm then FP32 logits (dedicated or tied).
+// output_norm is fused into the logits launch's staging of x.
 int tail(gh_model* m, gh_encoder* enc, const gh_buf* xrow, const gh_buf* normed_row) {
     const gh_model_config& c = m->cfg;
-    int rc = gh_rmsnorm_x(m->b, enc, normed_row, xrow, &m->output_norm, c.embedding_length, c.rms_epsilon, 1);
     const gh_buf* out = m->output.addr ? &m->output : &m->token_embd;
-    if (!rc) rc = gh_logits(m->b, enc, &m->logits, normed_row, out, c.embedding_length, c.vocab_size);
-    return rc;
+    const bool quant = out->format == GH_FMT_Q4_K || out->format == GH_FMT_Q6_K;
+    if (!quant || out->cols != c.embedding_length || out->rows != c.vocab_size) {
+        int rc = gh_rmsnorm_x(m->b, enc, normed_row, xrow, &m->output_norm, c.embedding_length,
+                              c.rms_epsilon, 1);
+        if (!rc) rc = gh_logits(m->b, enc, &m->logits, normed_row, out, c.embedding_length, c.vocab_size);
+        return rc;
+    }
+    const GemvSeg lg{out, m->logits.addr, GH_EPI_F32};
+    return latch_rc(enc, op_gemv(m->b, &lg, 1, xrow, 1, 0, nullptr, 0, nullptr, &m->output_norm,
+                                 c.rms_epsilon));
 }
 
 bool weights_ready(const gh_model* m) {

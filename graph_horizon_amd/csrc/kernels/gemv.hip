@@ -62,15 +62,15 @@ __device__ __forceinline__ void pair16(const uint4& a, const uint4& b, uint4& p0
     sum = s;
 }
 
-template <uint32_t FMT>
-__device__ __forceinline__ void stage_x(const uint16_t* x, uint32_t units, uint4* xs, float4* sums) {
+// x8(e) returns FP16 x[e .. e+8) as a uint4 (e a multiple of 8).
+template <uint32_t FMT, class X8>
+__device__ __forceinline__ void stage_x(const X8& x8, uint32_t units, uint4* xs, float4* sums) {
     for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
-        const GH_GLOBAL uint4* p;
         if constexpr (FMT == kQ4K) {
-            p = gh_gp<uint4>((uint64_t)(x + (size_t)(u >> 2) * 256 + (u & 3u) * 64));
+            const uint32_t e0 = (u >> 2) * 256 + (u & 3u) * 64;
             uint4 v[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = p[i];
+            for (int i = 0; i < 8; ++i) v[i] = x8(e0 + 8 * i);
             float s[4];
             pair16(v[0], v[1], xs[0 * units + u], xs[2 * units + u], s[0]);
             pair16(v[2], v[3], xs[1 * units + u], xs[3 * units + u], s[1]);
@@ -82,8 +82,8 @@ __device__ __forceinline__ void stage_x(const uint16_t* x, uint32_t units, uint4
             float s[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                p = gh_gp<uint4>((uint64_t)(x + (size_t)b * 256 + sg * 128 + q * 32 + h * 16));
-                pair16(p[0], p[1], xs[q * units + u], xs[(4 + q) * units + u], s[q]);
+                const uint32_t e = b * 256 + sg * 128 + q * 32 + h * 16;
+                pair16(x8(e), x8(e + 8), xs[q * units + u], xs[(4 + q) * units + u], s[q]);
             }
             sums[u] = make_float4(s[0], s[1], s[2], s[3]);
         }
@@ -346,7 +346,7 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // Staged x lives in dynamic LDS: 144 B per 64-weight unit (twice for the mixed kernel).
 // Waves are split between the segments in proportion to their tasks (args: seg.task0 is the
 // first task index, the wave split is recomputed here), so a wave only ever runs one format.
-template <int R, int MODE>
+template <int R, int MODE, bool NORM>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
     extern __shared__ uint4 lds[];
     constexpr int M = MODE == kModeSwiglu ? 2 : 1;
@@ -390,13 +390,57 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
         load_step<F0, R, M>(w, sg.rows, nb, first * R, min(threadIdx.x & 63u, units - 1), w0r);
     }
     for (uint32_t t = 0; t < a.n; ++t) {
-        const uint16_t* x = (const uint16_t*)a.x + (size_t)t * a.in_dim;
         if (t) __syncthreads();
-        if constexpr (MODE == kModeQ6) {
-            stage_x<kQ6K>(x, units, xs4, xsum4);
+        auto stage = [&](const auto& x8) {
+            if constexpr (MODE == kModeQ6) {
+                stage_x<kQ6K>(x8, units, xs4, xsum4);
+            } else {
+                stage_x<kQ4K>(x8, units, xs4, xsum4);
+                if constexpr (MODE == kModeMixed) stage_x<kQ6K>(x8, units, xs6, xsum6);
+            }
+        };
+        if constexpr (NORM) {
+            // rmsnorm_x fused: x is the FP32 residual row. Each thread loads its float4 chunks
+            // (tid + 256 k) and their norm weights once, the row's Σx² is reduced in the order
+            // of gh_rms_inverse_256, and the normalized FP16 row f16((x · inverse) · f16 w) —
+            // the bits gh_rmsnorm_x stores — goes to LDS, from which x is staged.
+            constexpr uint32_t kMaxChunks = 8;  // in_dim <= 8192
+            const uint32_t n4 = a.in_dim >> 2;
+            const GH_GLOBAL float4* xr = gh_gp<float4>(a.x + (uint64_t)t * a.in_dim * 4);
+            const GH_GLOBAL uint2* wn = gh_gp<uint2>(a.norm_w);
+            uint2* xn = (uint2*)(lds + (MODE == kModeMixed ? 18 : 9) * units);
+            float* red = (float*)(xn + n4);
+            float4 v[kMaxChunks];
+            uint2 wv[kMaxChunks];
+#pragma unroll
+            for (uint32_t k = 0; k < kMaxChunks; ++k) {
+                const uint32_t i = min(threadIdx.x + 256 * k, n4 - 1);
+                v[k] = xr[i];
+                wv[k] = wn[i];
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (uint32_t k = 0; k < kMaxChunks; ++k)
+                if (threadIdx.x + 256 * k < n4) ss = gh_rms_add(ss, v[k]);
+            const float inv = gh_rms_finish_256(ss, a.in_dim, a.eps, red);
+#pragma unroll
+            for (uint32_t k = 0; k < kMaxChunks; ++k) {
+#pragma clang fp contract(off)
+                const uint32_t i = threadIdx.x + 256 * k;
+                if (i < n4) {
+                    auto n2 = [&](float a0, float a1, uint32_t wp) {
+                        return (uint32_t)gh_f2h(a0 * inv * gh_h2f(wp & 0xFFFFu)) |
+                               ((uint32_t)gh_f2h(a1 * inv * gh_h2f(wp >> 16)) << 16);
+                    };
+                    xn[i] = make_uint2(n2(v[k].x, v[k].y, wv[k].x), n2(v[k].z, v[k].w, wv[k].y));
+                }
+            }
+            __syncthreads();
+            const uint4* xn4 = (const uint4*)xn;
+            stage([&](uint32_t e) { return xn4[e >> 3]; });
         } else {
-            stage_x<kQ4K>(x, units, xs4, xsum4);
-            if constexpr (MODE == kModeMixed) stage_x<kQ6K>(x, units, xs6, xsum6);
+            const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x + (uint64_t)t * a.in_dim * 2);
+            stage([&](uint32_t e) { return xh[e >> 3]; });
         }
         __syncthreads();
         if constexpr (MODE == kModeQ6) {
@@ -416,14 +460,16 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
 
 }  // namespace
 
-#define GH_GEMV(NAME, R, MODE) \
-    GH_KERNEL __launch_bounds__(256) void NAME(GhGemvArgs a) { gemv_body<R, MODE>(a); }
+// NORM kernels (suffix _n) stage the RMSNorm of an FP32 x (norm_w set); the others read FP16 x.
+#define GH_GEMV(NAME, R, MODE)                                                                 \
+    GH_KERNEL __launch_bounds__(256) void NAME(GhGemvArgs a) { gemv_body<R, MODE, false>(a); } \
+    GH_KERNEL __launch_bounds__(256) void NAME##_n(GhGemvArgs a) { gemv_body<R, MODE, true>(a); }
 GH_GEMV(gh_gemv_q4k_r1, 1, kModeQ4)
 GH_GEMV(gh_gemv_q4k_r2, 2, kModeQ4)
-GH_GEMV(gh_gemv_q4k_r4, 4, kModeQ4)
 GH_GEMV(gh_gemv_q6k_r1, 1, kModeQ6)
 GH_GEMV(gh_gemv_q6k_r2, 2, kModeQ6)
-GH_GEMV(gh_gemv_q6k_r4, 4, kModeQ6)
 GH_GEMV(gh_gemv_mixed_r2, 2, kModeMixed)
 GH_GEMV(gh_gemv_swiglu_r1, 1, kModeSwiglu)
 GH_GEMV(gh_gemv_swiglu_r2, 2, kModeSwiglu)
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4(GhGemvArgs a) { gemv_body<4, kModeQ4, false>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4(GhGemvArgs a) { gemv_body<4, kModeQ6, false>(a); }

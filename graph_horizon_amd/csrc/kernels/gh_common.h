@@ -66,6 +66,32 @@ __device__ __forceinline__ float gh_wave_sum63(float v) {
     return v;
 }
 
+// RMSNorm scale of one FP32 row over a 256-thread workgroup, in one fixed order (each thread
+// sums its float4 chunks tid, tid + 256, ... as (x²+y²)+(z²+w²); DPP wave sums; the four wave
+// sums added in wave order), so every kernel that uses it gets the same bits:
+// 1 / sqrt(Σx²/dim + eps) (normalization.rs:12-40). `red` is 4 floats of LDS; `s` is the
+// thread's own partial. Ends with a workgroup barrier.
+__device__ __forceinline__ float gh_rms_add(float s, const float4& v) {
+#pragma clang fp contract(off)
+    return s + ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
+}
+
+__device__ __forceinline__ float gh_rms_finish_256(float s, uint32_t dim, float eps, float* red) {
+#pragma clang fp contract(off)
+    s = gh_wave_sum63(s);
+    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float sum = ((red[0] + red[1]) + red[2]) + red[3];
+    return 1.0f / __builtin_sqrtf(sum / (float)dim + eps);
+}
+
+__device__ __forceinline__ float gh_rms_inverse_256(const __attribute__((address_space(1))) float4* x,
+                                                   uint32_t dim, float eps, float* red) {
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < (dim >> 2); i += 256) s = gh_rms_add(s, x[i]);
+    return gh_rms_finish_256(s, dim, eps, red);
+}
+
 // Byte `i` (runtime, 0..15) of a 16-byte register block.
 __device__ __forceinline__ uint32_t gh_byte(const uint4& v, uint32_t i) {
     uint32_t w = (i < 4) ? v.x : (i < 8) ? v.y : (i < 12) ? v.z : v.w;

@@ -65,6 +65,10 @@ struct GhGemvArgs {
     uint64_t post;     // GH_EPI_ROPE: f32 post-scale [positions] (0 = 1.0, keys)
     uint64_t pos_ptr;  // optional u32* position on the device (added to base)
     uint64_t aux;      // GH_EPI_SWIGLU: the up matrix (same shape/format as seg[0])
+    uint64_t norm_w;   // nonzero: x is the FP32 residual row and the launch stages
+                       // f16(x · 1/sqrt(Σx²/in_dim + eps) · norm_w) (rmsnorm_x fused)
+    float eps;
+    uint32_t pad2;
     uint32_t in_dim;
     uint32_t nseg;
     uint32_t n;        // tokens (> 1 only with GH_EPI_F16 / GH_EPI_F32)

@@ -4,27 +4,16 @@
 // rmsnorm_x (backend/cpu/kernels/elementwise/normalization.rs:12-40): one 1024-thread
 // workgroup per row, 4 consecutive FP32 values per thread per step, Σx² reduced with DPP and
 // LDS, inverse = 1/sqrt(Σx²/dim + eps), out = f16((x*inverse)*w). dim % 4 == 0.
-GH_KERNEL __launch_bounds__(1024) void gh_rmsnorm_x(GhRmsnormArgs a) {
+GH_KERNEL __launch_bounds__(256) void gh_rmsnorm_x(GhRmsnormArgs a) {
 #pragma clang fp contract(off)
     const uint32_t row = blockIdx.x;
     if (row >= a.rows) return;
     const GH_GLOBAL float4* x = gh_gp<float4>(a.x + (uint64_t)row * a.dim * 4);
     const GH_GLOBAL uint2* w = gh_gp<uint2>(a.w);
     GH_GLOBAL uint2* out = gh_gpw<uint2>(a.out + (uint64_t)row * a.dim * 2);
-    __shared__ float partial[16];
-    const uint32_t n4 = a.dim >> 2;
-    float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n4; i += blockDim.x) {
-        const float4 v = x[i];
-        s += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-    }
-    s = gh_wave_sum63(s);
-    if ((threadIdx.x & 63) == 63) partial[threadIdx.x >> 6] = s;
-    __syncthreads();
-    float sum = 0.0f;
-    for (uint32_t i = 0; i < (blockDim.x >> 6); ++i) sum += partial[i];
-    const float inverse = 1.0f / __builtin_sqrtf(sum / (float)a.dim + a.eps);
-    for (uint32_t i = threadIdx.x; i < n4; i += blockDim.x) {
+    __shared__ float red[4];
+    const float inverse = gh_rms_inverse_256(x, a.dim, a.eps, red);
+    for (uint32_t i = threadIdx.x; i < (a.dim >> 2); i += blockDim.x) {
         const float4 v = x[i];
         const uint2 wv = w[i];
         const uint32_t o0 = gh_f2h(v.x * inverse * gh_h2f(wv.x & 0xFFFFu));
