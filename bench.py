@@ -132,9 +132,13 @@ def main():
 
     rng = np.random.default_rng(7)
     prompt = rng.integers(0, shape.vocab_size, args.prompt).astype(np.uint32)
-    t0 = time.perf_counter()
+    model.prefill(prompt[:16], 0)  # first-use costs (workspace growth) outside the timing
+    hip.synchronize()
+    hip.timer_start()
     model.prefill(prompt, 0)
-    log(f"bench: prefill {args.prompt} tokens in {time.perf_counter() - t0:.2f} s")
+    prefill_ms = hip.timer_stop()
+    log(f"bench: prefill {args.prompt} tokens in {prefill_ms:.2f} ms "
+        f"({args.prompt / (prefill_ms / 1e3):.0f} tok/s)")
     first = model.read_argmax()
     pos = args.prompt
     if args.warmup:
@@ -190,11 +194,15 @@ def main():
         "data": "synthetic (seeded random-init Q4_K_M weights, random prompt ids)",
         "config": {
             "workload": f"{shape.name}-shaped Q4_K_M decoder, greedy decode bs=1 "
-                        f"({shape.block_count} blocks of BASELINE configs[1]: d {d}, FFN {ffn}, "
+                        f"({shape.block_count} blocks"
+                        f"{' of BASELINE configs[1]' if shape.name == '8b' else ''}"
+                        f"{'; BASELINE configs[4]' if shape.name == '14b' else ''}: d {d}, FFN {ffn}, "
                         f"32/8 heads x 128, Q/K/O/gate/up Q4_K, V/down Q6_K; Q6_K output "
                         f"{shape.vocab_size}x{d}); context {args.prompt}..{pos + args.steps}; "
                         f"{args.launch} launch",
             "weight_bytes_per_token": per_token,
+            "prefill": {"tokens": args.prompt, "ms": round(prefill_ms, 3),
+                        "tok_s": round(args.prompt / (prefill_ms / 1e3), 1)},
             "decode_weight_roofline_frac": round(per_token * tok_s / (HBM_PEAK_GBPS * 1e9), 4),
             "q4k_gemv_c1_shape": None,
         },
@@ -204,7 +212,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": ROOFLINE_TRAFFIC_BYTES,
+            "traffic": ROOFLINE_TRAFFIC_BYTES if (d, ffn) == (4096, 12288) else None,
             "kernel": f"gh_gemv_q4k (Q4_K GEMV {ffn}x{d}, {gemv_bytes} B/launch)",
             "avg_us": round(gemv_ms * 1e3, 3),
         },

@@ -470,9 +470,11 @@ def test_kv_layout(ora, goldens):
 
 
 # ---------------------------------------------------------------- graph
-def oracle_model(shape, seed, kv_context):
+def oracle_model(shape, seed, kv_context, generated=None):
+    """The oracle's model over synth.model_tensors(shape, seed) (or an already generated list
+    of the same tuples)."""
     tensors = {}
-    for layer, tid, fmt, data in synth.model_tensors(shape, seed):
+    for layer, tid, fmt, data in (generated if generated is not None else synth.model_tensors(shape, seed)):
         tensors[("g", tid) if layer == 0xFFFFFFFF else (layer, tid)] = (fmt, data)
     y = synth.yarn_params(shape)
     cfg = O.ModelCfg(shape.block_count, max(kv_context, 32768), shape.embedding_length,
