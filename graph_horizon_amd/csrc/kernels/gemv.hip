@@ -307,10 +307,13 @@ __device__ __forceinline__ uint32_t i_end(const GhGemvArgs& a, uint32_t si) {
 }
 
 // A wave's work: tasks first, first + stride, ... < ntask of one segment; a task is nch chunks
-// of 64 units. The weights of a chunk (all R rows, both matrices for SwiGLU) are requested
-// together before any arithmetic; lanes past the last unit re-read the last unit (addresses
-// stay valid, loads stay unconditional so the wait counts stay exact) and add nothing.
-// `primed`: the caller already loaded the first chunk of the first task into wa.
+// of 64 units. The (task, chunk) steps run as a two-stage pipeline: the weights of the next
+// step (all R rows, both matrices for SwiGLU) are requested into the other register set
+// before the current step is computed, so a wave keeps a step of loads in flight while its
+// VALUs work. Every load is unconditional — past the wave's last step it re-reads the current
+// step, and lanes past the last unit re-read the last unit (addresses stay valid, those lanes
+// add nothing) — so the compiler's wait counts stay exact.
+// `primed`: the caller already loaded the first step into wa.
 template <uint32_t FMT, int R, int M>
 __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg& sg,
                                             uint32_t first, uint32_t stride, uint32_t ntask,
@@ -319,27 +322,57 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
                                             WRow<FMT> (&wa)[M][R]) {
     const uint32_t lane = threadIdx.x & 63u, units = nb * 4;
     const uint32_t nch = (units + 63) / 64;
+    if (first >= ntask) return;
     const uint8_t* w[M];
     w[0] = (const uint8_t*)sg.w;
     if constexpr (M == 2) w[1] = (const uint8_t*)a.aux;
-    for (uint32_t k = first; k < ntask; k += stride) {
-        float acc[M][R];
+    auto load = [&](uint32_t k, uint32_t c, WRow<FMT> (&dst)[M][R]) {
+        load_step<FMT, R, M>(w, sg.rows, nb, k * R, min(c * 64 + lane, units - 1), dst);
+    };
+    if (!primed) load(first, 0, wa);
+    WRow<FMT> wb[M][R];
+    float acc[M][R];
 #pragma unroll
-        for (int m = 0; m < M; ++m)
+    for (int m = 0; m < M; ++m)
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
-        for (uint32_t c = 0; c < nch; ++c) {
-            const uint32_t u = c * 64 + lane, uc = min(u, units - 1);
-            if (!primed) load_step<FMT, R, M>(w, sg.rows, nb, k * R, uc, wa);
-            primed = false;
-            if (u < units) compute_step<FMT, R, M>(xs, sums, units, u, mk, wa, acc);
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+    uint32_t k = first, c = 0;              // current step
+    uint32_t kn = nch > 1 ? k : k + stride;  // next step
+    uint32_t cn = nch > 1 ? 1 : 0;
+    auto advance = [&]() {
+        k = kn;
+        c = cn;
+        if (++cn == nch) {
+            cn = 0;
+            kn += stride;
         }
-        float v[M][R];
+    };
+    auto step = [&](const WRow<FMT> (&cur)[M][R]) {
+        const uint32_t u = c * 64 + lane;
+        if (u < units) compute_step<FMT, R, M>(xs, sums, units, u, mk, cur, acc);
+        if (c == nch - 1) {
+            float v[M][R];
 #pragma unroll
-        for (int m = 0; m < M; ++m)
+            for (int m = 0; m < M; ++m)
 #pragma unroll
-            for (int r = 0; r < R; ++r) v[m][r] = gh_wave_sum63(acc[m][r]);
-        if (lane == 63u) epilogue<R>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr);
+                for (int r = 0; r < R; ++r) {
+                    v[m][r] = gh_wave_sum63(acc[m][r]);
+                    acc[m][r] = 0.0f;
+                }
+            if (lane == 63u) epilogue<R>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr);
+        }
+    };
+    while (true) {
+        bool more = kn < ntask;
+        load(more ? kn : k, more ? cn : c, wb);
+        step(wa);
+        if (!more) break;
+        advance();
+        more = kn < ntask;
+        load(more ? kn : k, more ? cn : c, wa);
+        step(wb);
+        if (!more) break;
+        advance();
     }
 }
 
