@@ -48,10 +48,12 @@ def _ptr(a: np.ndarray) -> C.c_void_p:
 class HipBackend:
     """One gfx950 device, one stream. Methods follow the trait's names and argument order."""
 
-    def __init__(self, device: int = 0):
+    def __init__(self, device: int = 0, code_objects: str | None = None):
+        """code_objects: directory of the gh_*_gfx950.co files (default: next to the library)."""
         self.lib = F.lib()
         h = C.c_void_p()
-        rc = self.lib.gh_create(C.byref(F.GhConfig(device, None)), C.byref(h))
+        path = code_objects.encode() if code_objects else None
+        rc = self.lib.gh_create(C.byref(F.GhConfig(device, path)), C.byref(h))
         if rc != F.GH_OK:
             raise GhError(rc, "gh_create", "(no gfx950 device, or code objects missing)")
         self.h = h

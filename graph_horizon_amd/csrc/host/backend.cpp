@@ -32,6 +32,9 @@ const KernelName kKernels[] = {
     {K_GEMV_Q6K_R1_N, "gh_gemv_q6k_r1_n"}, {K_GEMV_Q6K_R2_N, "gh_gemv_q6k_r2_n"},
     {K_GEMV_MIXED_R2_N, "gh_gemv_mixed_r2_n"},
     {K_GEMV_SWIGLU_R1_N, "gh_gemv_swiglu_r1_n"}, {K_GEMV_SWIGLU_R2_N, "gh_gemv_swiglu_r2_n"},
+    {K_GEMV_Q4K_R1_D, "gh_gemv_q4k_r1_d"}, {K_GEMV_Q4K_R2_D, "gh_gemv_q4k_r2_d"},
+    {K_GEMV_Q6K_R1_D, "gh_gemv_q6k_r1_d"}, {K_GEMV_Q6K_R2_D, "gh_gemv_q6k_r2_d"},
+    {K_GEMV_Q4K_R4_D, "gh_gemv_q4k_r4_d"}, {K_GEMV_Q6K_R4_D, "gh_gemv_q6k_r4_d"},
     {K_RMSNORM, "gh_rmsnorm_x"},           {K_ROPE, "gh_rope"},
     {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
     {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
@@ -433,7 +436,11 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
         if (nseg != 1 || !up || up->format != GH_FMT_Q4_K || segs[0].w->format != GH_FMT_Q4_K ||
             up->rows != segs[0].w->rows || up->cols != in_dim)
             return fail(b, GH_E_INVALID, "gemv: SwiGLU needs Q4_K gate/up of one shape");
-        r = std::min<uint32_t>(r, 2);
+        static const uint32_t swiglu_rows = [] {
+            const char* e = std::getenv("GH_SWIGLU_ROWS");
+            return e ? (uint32_t)std::atoi(e) : 0u;
+        }();
+        r = swiglu_rows == 1 || swiglu_rows == 2 ? swiglu_rows : std::min<uint32_t>(r, 2);
         k = r == 2 ? K_GEMV_SWIGLU_R2 : K_GEMV_SWIGLU_R1;
         a.aux = up->addr;
     } else if (mixed) {
@@ -442,6 +449,19 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
         k = r == 4 ? K_GEMV_Q4K_R4 : r == 2 ? K_GEMV_Q4K_R2 : K_GEMV_Q4K_R1;
     } else {
         k = r == 4 ? K_GEMV_Q6K_R4 : r == 2 ? K_GEMV_Q6K_R2 : K_GEMV_Q6K_R1;
+    }
+    static const bool no_direct = std::getenv("GH_GEMV_NO_DIRECT") != nullptr;
+    const bool direct = !no_direct && !norm && n == 1 && nseg == 1 && !swiglu && in_dim <= 4096;
+    if (direct) {
+        switch (k) {
+            case K_GEMV_Q4K_R1: k = K_GEMV_Q4K_R1_D; break;
+            case K_GEMV_Q4K_R2: k = K_GEMV_Q4K_R2_D; break;
+            case K_GEMV_Q4K_R4: k = K_GEMV_Q4K_R4_D; break;
+            case K_GEMV_Q6K_R1: k = K_GEMV_Q6K_R1_D; break;
+            case K_GEMV_Q6K_R2: k = K_GEMV_Q6K_R2_D; break;
+            case K_GEMV_Q6K_R4: k = K_GEMV_Q6K_R4_D; break;
+            default: break;
+        }
     }
     if (norm) {
         switch (k) {
@@ -487,11 +507,12 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     // x staged once per workgroup in LDS (144 B per 64-weight unit; both layouts if mixed);
     // the persistent grid (at most what is resident at once) loops its waves over the tasks.
     // + the normalized FP16 row and 16 bytes of reduction scratch when RMSNorm is fused
-    const uint32_t shmem = (in_dim / 64) * 144 * (mixed ? 2 : 1) + (norm ? in_dim * 2 + 16 : 0);
+    uint32_t shmem = (in_dim / 64) * 144 * (mixed ? 2 : 1) + (norm ? in_dim * 2 + 16 : 0);
     static const uint32_t max_wg = [] {
         const char* e = std::getenv("GH_GEMV_MAX_WG");
         return e ? (uint32_t)std::atoi(e) : 0u;
     }();
+    if (direct) shmem = 0;
     const uint32_t cap = max_wg ? max_wg : resident_wgs(b, k, 256, shmem);
     return launch(b, k, std::max<uint32_t>(1, std::min<uint32_t>(ceil_div(task, 4), cap)), 1, 1, 256, &a, shmem);
 }

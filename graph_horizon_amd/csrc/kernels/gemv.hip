@@ -55,38 +55,50 @@ __device__ __forceinline__ void pair16(const uint4& a, const uint4& b, uint4& p0
         const uint32_t lo = w[2 * j], hi = w[2 * j + 1];
         e[j] = (lo & 0xFFFFu) | (hi << 16);
         o[j] = (lo >> 16) | (hi & 0xFFFF0000u);
-        s += (gh_h2f(lo & 0xFFFFu) + gh_h2f(lo >> 16)) + (gh_h2f(hi & 0xFFFFu) + gh_h2f(hi >> 16));
+        // Σ of the 16 values with v_dot2_f32_f16 against (1, 1): exact products, FP32 sum
+        s = gh_dot2(lo, 0x3C003C00u, s);
+        s = gh_dot2(hi, 0x3C003C00u, s);
     }
     p02 = make_uint4(e[0], e[1], e[2], e[3]);
     p13 = make_uint4(o[0], o[1], o[2], o[3]);
     sum = s;
 }
 
-// x8(e) returns FP16 x[e .. e+8) as a uint4 (e a multiple of 8).
+// x8(e) returns FP16 x[e .. e+8) as a uint4 (e a multiple of 8). The pairs and sums of unit u.
+template <uint32_t FMT, class X8>
+__device__ __forceinline__ void pair_unit(const X8& x8, uint32_t u, uint4 (&xv)[8], float4& sum) {
+    if constexpr (FMT == kQ4K) {
+        const uint32_t e0 = (u >> 2) * 256 + (u & 3u) * 64;
+        uint4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = x8(e0 + 8 * i);
+        float s[4];
+        pair16(v[0], v[1], xv[0], xv[2], s[0]);
+        pair16(v[2], v[3], xv[1], xv[3], s[1]);
+        pair16(v[4], v[5], xv[4], xv[6], s[2]);
+        pair16(v[6], v[7], xv[5], xv[7], s[3]);
+        sum = make_float4(s[0] + s[1], s[2] + s[3], 0.0f, 0.0f);
+    } else {
+        const uint32_t b = u >> 2, sg = (u >> 1) & 1u, h = u & 1u;
+        float s[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t e = b * 256 + sg * 128 + q * 32 + h * 16;
+            pair16(x8(e), x8(e + 8), xv[q], xv[4 + q], s[q]);
+        }
+        sum = make_float4(s[0], s[1], s[2], s[3]);
+    }
+}
+
 template <uint32_t FMT, class X8>
 __device__ __forceinline__ void stage_x(const X8& x8, uint32_t units, uint4* xs, float4* sums) {
     for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
-        if constexpr (FMT == kQ4K) {
-            const uint32_t e0 = (u >> 2) * 256 + (u & 3u) * 64;
-            uint4 v[8];
+        uint4 xv[8];
+        float4 sm;
+        pair_unit<FMT>(x8, u, xv, sm);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = x8(e0 + 8 * i);
-            float s[4];
-            pair16(v[0], v[1], xs[0 * units + u], xs[2 * units + u], s[0]);
-            pair16(v[2], v[3], xs[1 * units + u], xs[3 * units + u], s[1]);
-            pair16(v[4], v[5], xs[4 * units + u], xs[6 * units + u], s[2]);
-            pair16(v[6], v[7], xs[5 * units + u], xs[7 * units + u], s[3]);
-            sums[u] = make_float4(s[0] + s[1], s[2] + s[3], 0.0f, 0.0f);
-        } else {
-            const uint32_t b = u >> 2, sg = (u >> 1) & 1u, h = u & 1u;
-            float s[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t e = b * 256 + sg * 128 + q * 32 + h * 16;
-                pair16(x8(e), x8(e + 8), xs[q * units + u], xs[(4 + q) * units + u], s[q]);
-            }
-            sums[u] = make_float4(s[0], s[1], s[2], s[3]);
-        }
+        for (int k = 0; k < 8; ++k) xs[k * units + u] = xv[k];
+        sums[u] = sm;
     }
 }
 
@@ -197,13 +209,9 @@ __device__ __forceinline__ void load_step(const uint8_t* const (&w)[M], uint32_t
 }
 
 template <uint32_t FMT, int R, int M>
-__device__ __forceinline__ void compute_step(const uint4* xs, const float4* sums, uint32_t units,
-                                             uint32_t u, const Masks& mk,
-                                             const WRow<FMT> (&wr)[M][R], float (&acc)[M][R]) {
-    uint4 xv[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) xv[k] = xs[k * units + u];
-    const float4 xsum = sums[u];
+__device__ __forceinline__ void compute_regs(const uint4 (&xv)[8], const float4& xsum, uint32_t u,
+                                             const Masks& mk, const WRow<FMT> (&wr)[M][R],
+                                             float (&acc)[M][R]) {
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -213,6 +221,16 @@ __device__ __forceinline__ void compute_step(const uint4* xs, const float4* sums
             else
                 acc[m][r] += dot_q6(xv, xsum, wr[m][r], (u >> 1) & 1u, u & 1u, mk);
         }
+}
+
+template <uint32_t FMT, int R, int M>
+__device__ __forceinline__ void compute_step(const uint4* xs, const float4* sums, uint32_t units,
+                                             uint32_t u, const Masks& mk,
+                                             const WRow<FMT> (&wr)[M][R], float (&acc)[M][R]) {
+    uint4 xv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xv[k] = xs[k * units + u];
+    compute_regs<FMT, R, M>(xv, sums[u], u, mk, wr, acc);
 }
 
 __device__ __forceinline__ uint32_t position(const GhGemvArgs& a) {
@@ -307,13 +325,10 @@ __device__ __forceinline__ uint32_t i_end(const GhGemvArgs& a, uint32_t si) {
 }
 
 // A wave's work: tasks first, first + stride, ... < ntask of one segment; a task is nch chunks
-// of 64 units. The (task, chunk) steps run as a two-stage pipeline: the weights of the next
-// step (all R rows, both matrices for SwiGLU) are requested into the other register set
-// before the current step is computed, so a wave keeps a step of loads in flight while its
-// VALUs work. Every load is unconditional — past the wave's last step it re-reads the current
-// step, and lanes past the last unit re-read the last unit (addresses stay valid, those lanes
-// add nothing) — so the compiler's wait counts stay exact.
-// `primed`: the caller already loaded the first step into wa.
+// of 64 units. The weights of a chunk (all R rows, both matrices for SwiGLU) are requested
+// together before any arithmetic; lanes past the last unit re-read the last unit (addresses
+// stay valid, loads stay unconditional so the wait counts stay exact) and add nothing.
+// `primed`: the caller already loaded the first chunk of the first task into wa.
 template <uint32_t FMT, int R, int M>
 __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg& sg,
                                             uint32_t first, uint32_t stride, uint32_t ntask,
@@ -322,57 +337,27 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
                                             WRow<FMT> (&wa)[M][R]) {
     const uint32_t lane = threadIdx.x & 63u, units = nb * 4;
     const uint32_t nch = (units + 63) / 64;
-    if (first >= ntask) return;
     const uint8_t* w[M];
     w[0] = (const uint8_t*)sg.w;
     if constexpr (M == 2) w[1] = (const uint8_t*)a.aux;
-    auto load = [&](uint32_t k, uint32_t c, WRow<FMT> (&dst)[M][R]) {
-        load_step<FMT, R, M>(w, sg.rows, nb, k * R, min(c * 64 + lane, units - 1), dst);
-    };
-    if (!primed) load(first, 0, wa);
-    WRow<FMT> wb[M][R];
-    float acc[M][R];
+    for (uint32_t k = first; k < ntask; k += stride) {
+        float acc[M][R];
 #pragma unroll
-    for (int m = 0; m < M; ++m)
+        for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
-    uint32_t k = first, c = 0;              // current step
-    uint32_t kn = nch > 1 ? k : k + stride;  // next step
-    uint32_t cn = nch > 1 ? 1 : 0;
-    auto advance = [&]() {
-        k = kn;
-        c = cn;
-        if (++cn == nch) {
-            cn = 0;
-            kn += stride;
+            for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+        for (uint32_t c = 0; c < nch; ++c) {
+            const uint32_t u = c * 64 + lane, uc = min(u, units - 1);
+            if (!primed) load_step<FMT, R, M>(w, sg.rows, nb, k * R, uc, wa);
+            primed = false;
+            if (u < units) compute_step<FMT, R, M>(xs, sums, units, u, mk, wa, acc);
         }
-    };
-    auto step = [&](const WRow<FMT> (&cur)[M][R]) {
-        const uint32_t u = c * 64 + lane;
-        if (u < units) compute_step<FMT, R, M>(xs, sums, units, u, mk, cur, acc);
-        if (c == nch - 1) {
-            float v[M][R];
+        float v[M][R];
 #pragma unroll
-            for (int m = 0; m < M; ++m)
+        for (int m = 0; m < M; ++m)
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    v[m][r] = gh_wave_sum63(acc[m][r]);
-                    acc[m][r] = 0.0f;
-                }
-            if (lane == 63u) epilogue<R>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr);
-        }
-    };
-    while (true) {
-        bool more = kn < ntask;
-        load(more ? kn : k, more ? cn : c, wb);
-        step(wa);
-        if (!more) break;
-        advance();
-        more = kn < ntask;
-        load(more ? kn : k, more ? cn : c, wa);
-        step(wb);
-        if (!more) break;
-        advance();
+            for (int r = 0; r < R; ++r) v[m][r] = gh_wave_sum63(acc[m][r]);
+        if (lane == 63u) epilogue<R>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr);
     }
 }
 
@@ -491,6 +476,38 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
     }
 }
 
+// Single-token launch of one Q4_K or Q6_K matrix with in_dim <= 4096 (one unit per lane):
+// each wave loads and pairs its own lane's slice of x in registers, together with the first
+// task's weights — no LDS, no workgroup barrier; waves run independently from the first load.
+template <int R, uint32_t FMT>
+__device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
+    const uint32_t lane = threadIdx.x & 63u, nb = a.in_dim >> 8, units = nb * 4;
+    const uint32_t waves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const GhGemvSeg sg = a.seg[0];
+    if (gw >= a.tasks) return;  // wave-uniform; this kernel has no barrier
+    const uint32_t u = min(lane, units - 1);
+    const uint8_t* w[1] = {(const uint8_t*)sg.w};
+    WRow<FMT> wr[1][R];
+    load_step<FMT, R, 1>(w, sg.rows, nb, gw * R, u, wr);
+    const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x);
+    uint4 xv[8];
+    float4 xsum;
+    pair_unit<FMT>([&](uint32_t e) { return xh[e >> 3]; }, u, xv, xsum);
+    const Masks mk = make_masks();
+    for (uint32_t k = gw; k < a.tasks; k += waves) {
+        if (k != gw) load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
+        float acc[1][R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[0][r] = 0.0f;
+        if (lane < units) compute_regs<FMT, R, 1>(xv, xsum, u, mk, wr, acc);
+        float v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = gh_wave_sum63(acc[0][r]);
+        if (lane == 63u) epilogue<R>(a, sg, 0, k * R, v, nullptr);
+    }
+}
+
 }  // namespace
 
 // NORM kernels (suffix _n) stage the RMSNorm of an FP32 x (norm_w set); the others read FP16 x.
@@ -505,4 +522,11 @@ GH_GEMV(gh_gemv_mixed_r2, 2, kModeMixed)
 GH_GEMV(gh_gemv_swiglu_r1, 1, kModeSwiglu)
 GH_GEMV(gh_gemv_swiglu_r2, 2, kModeSwiglu)
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4(GhGemvArgs a) { gemv_body<4, kModeQ4, false>(a); }
+// direct-x variants (suffix _d): single token, one matrix, in_dim <= 4096, no RMSNorm
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_d(GhGemvArgs a) { gemv_direct<1, kQ4K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_d(GhGemvArgs a) { gemv_direct<2, kQ4K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_d(GhGemvArgs a) { gemv_direct<1, kQ6K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_d(GhGemvArgs a) { gemv_direct<2, kQ6K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4_d(GhGemvArgs a) { gemv_direct<4, kQ4K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4_d(GhGemvArgs a) { gemv_direct<4, kQ6K>(a); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4(GhGemvArgs a) { gemv_body<4, kModeQ6, false>(a); }
