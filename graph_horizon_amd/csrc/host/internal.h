@@ -120,7 +120,9 @@ struct GemvSeg {
     uint64_t out;
     uint32_t epi;
 };
-// norm: x is the FP32 residual and rmsnorm_x(norm, eps) is applied while staging it.
+// norm: x is the FP32 residual and rmsnorm_x(norm, eps) is applied while staging it
+// (in_dim <= kFusedNormMaxDim).
+constexpr uint32_t kFusedNormMaxDim = 5120;
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
             uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up,
             const gh_buf* norm = nullptr, float eps = 0.0f);

@@ -88,20 +88,31 @@ int layer_decode_fused(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t 
     const uint64_t kv_row_v = (uint64_t)c.kv_head_count * c.value_length;
     const uint64_t kbase = m->kv.k.addr + (uint64_t)li * m->kv.context * kv_row_k * 2;
     const uint64_t vbase = m->kv.v.addr + (uint64_t)li * m->kv.context * kv_row_v * 2;
-    // attention RMSNorm fused into the QKV launch's staging of x
+    // RMSNorm fused into the QKV and gate/up launches' staging of x (up to kFusedNormMaxDim)
+    const bool fuse_norm = c.embedding_length <= kFusedNormMaxDim;
+    auto normed = [&](const gh_buf* nw, const gh_buf** x_in, const gh_buf** norm_w) {
+        if (fuse_norm) {
+            *x_in = &s.x;
+            *norm_w = nw;
+            return 0;
+        }
+        *x_in = &s.normed;
+        *norm_w = nullptr;
+        return gh_rmsnorm_x(b, enc, &s.normed, &s.x, nw, c.embedding_length, c.rms_epsilon, 1);
+    };
     const GemvSeg qkv[3] = {{&w[GH_T_ATTN_Q], s.q.addr, GH_EPI_ROPE},
                             {&w[GH_T_ATTN_K], kbase, GH_EPI_ROPE_CACHE},
                             {&w[GH_T_ATTN_V], vbase, GH_EPI_CACHE}};
-    int rc = op_gemv(b, qkv, 3, &s.x, 1, base, pos_ptr, c.key_length, nullptr, &w[GH_T_ATTN_NORM],
-                     c.rms_epsilon);
+    const gh_buf *xin = nullptr, *nw = nullptr;
+    int rc = normed(&w[GH_T_ATTN_NORM], &xin, &nw);
+    if (!rc) rc = op_gemv(b, qkv, 3, xin, 1, base, pos_ptr, c.key_length, nullptr, nw, c.rms_epsilon);
     const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base;
     if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, 1, li, pos_ptr, max_pos);
     const GemvSeg o{&w[GH_T_ATTN_OUTPUT], s.x.addr, GH_EPI_RESID};
     if (!rc) rc = op_gemv(b, &o, 1, &s.attn, 1, 0, nullptr, 0, nullptr);
-    // FFN RMSNorm fused into the gate/up launch
     const GemvSeg gu{&w[GH_T_FFN_GATE], s.act.addr, GH_EPI_SWIGLU};
-    if (!rc) rc = op_gemv(b, &gu, 1, &s.x, 1, 0, nullptr, 0, &w[GH_T_FFN_UP], &w[GH_T_FFN_NORM],
-                          c.rms_epsilon);
+    if (!rc) rc = normed(&w[GH_T_FFN_NORM], &xin, &nw);
+    if (!rc) rc = op_gemv(b, &gu, 1, xin, 1, 0, nullptr, 0, &w[GH_T_FFN_UP], nw, c.rms_epsilon);
     const GemvSeg dn{&w[GH_T_FFN_DOWN], s.x.addr, GH_EPI_RESID};
     if (!rc) rc = op_gemv(b, &dn, 1, &s.act, 1, 0, nullptr, 0, nullptr);
     return latch_rc(enc, rc);
@@ -160,7 +171,8 @@ int tail(gh_model* m, gh_encoder* enc, const gh_buf* xrow, const gh_buf* normed_
     const gh_model_config& c = m->cfg;
     const gh_buf* out = m->output.addr ? &m->output : &m->token_embd;
     const bool quant = out->format == GH_FMT_Q4_K || out->format == GH_FMT_Q6_K;
-    if (!quant || out->cols != c.embedding_length || out->rows != c.vocab_size) {
+    if (!quant || out->cols != c.embedding_length || out->rows != c.vocab_size ||
+        c.embedding_length > kFusedNormMaxDim) {
         int rc = gh_rmsnorm_x(m->b, enc, normed_row, xrow, &m->output_norm, c.embedding_length,
                               c.rms_epsilon, 1);
         if (!rc) rc = gh_logits(m->b, enc, &m->logits, normed_row, out, c.embedding_length, c.vocab_size);

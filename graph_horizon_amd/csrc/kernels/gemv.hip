@@ -220,6 +220,8 @@ __device__ __forceinline__ void compute_regs(const uint4 (&xv)[8], const float4&
                 acc[m][r] += dot_q4(xv, xsum, wr[m][r], u & 3u, mk);
             else
                 acc[m][r] += dot_q6(xv, xsum, wr[m][r], (u >> 1) & 1u, u & 1u, mk);
+            // one row at a time: keeps the temporaries of a single dot product live
+            if constexpr (M * R > 2) __builtin_amdgcn_sched_barrier(0);
         }
 }
 
@@ -257,10 +259,21 @@ __device__ __forceinline__ void rope_pair(const GhGemvArgs& a, uint32_t row, flo
     o1 = gh_f2h((x0 * cs.y + x1 * cs.x) * k);
 }
 
-template <int R>
+template <int R, bool SW>
 __device__ __forceinline__ void epilogue(const GhGemvArgs& a, const GhGemvSeg& sg, uint32_t t,
                                          uint32_t row0, const float (&v)[R], const float* up) {
 #pragma clang fp contract(off)
+    if constexpr (SW) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (row0 + r < sg.rows) {
+                    // silu_mul (activation.rs:16-29) on the FP16-rounded gate/up projections
+                    const float g = gh_h2f(gh_f2h(v[r])), u = gh_h2f(gh_f2h(up[r]));
+                    const float silu = g / (1.0f + expf(-g));
+                    gh_gpw<uint16_t>(sg.out)[row0 + r] = gh_f2h(gh_h2f(gh_f2h(silu)) * u);
+                }
+        return;
+    }
     switch (sg.epi) {
         case GH_EPI_F16:
 #pragma unroll
@@ -304,16 +317,6 @@ __device__ __forceinline__ void epilogue(const GhGemvArgs& a, const GhGemvSeg& s
             }
             break;
         }
-        case GH_EPI_SWIGLU:
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < sg.rows) {
-                    // silu_mul (activation.rs:16-29) on the FP16-rounded gate/up projections
-                    const float g = gh_h2f(gh_f2h(v[r])), u = gh_h2f(gh_f2h(up[r]));
-                    const float silu = g / (1.0f + expf(-g));
-                    gh_gpw<uint16_t>(sg.out)[row0 + r] = gh_f2h(gh_h2f(gh_f2h(silu)) * u);
-                }
-            break;
     }
 }
 
@@ -357,7 +360,7 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
         for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int r = 0; r < R; ++r) v[m][r] = gh_wave_sum63(acc[m][r]);
-        if (lane == 63u) epilogue<R>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr);
+        if (lane == 63u) epilogue<R, M == 2>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr);
     }
 }
 
@@ -400,7 +403,7 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
     // staged, so their latency overlaps the staging.
     constexpr uint32_t F0 = MODE == kModeQ6 ? kQ6K : kQ4K;
     WRow<F0> w0r[M][R];
-    const bool primed = sg.fmt == F0 && first < ntask;
+    const bool primed = !NORM && sg.fmt == F0 && first < ntask;
     if (primed) {
         const uint8_t* w[M];
         w[0] = (const uint8_t*)sg.w;
@@ -422,7 +425,7 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
             // (tid + 256 k) and their norm weights once, the row's Σx² is reduced in the order
             // of gh_rms_inverse_256, and the normalized FP16 row f16((x · inverse) · f16 w) —
             // the bits gh_rmsnorm_x stores — goes to LDS, from which x is staged.
-            constexpr uint32_t kMaxChunks = 8;  // in_dim <= 8192
+            constexpr uint32_t kMaxChunks = 5;  // in_dim <= 5120
             const uint32_t n4 = a.in_dim >> 2;
             const GH_GLOBAL float4* xr = gh_gp<float4>(a.x + (uint64_t)t * a.in_dim * 4);
             const GH_GLOBAL uint2* wn = gh_gp<uint2>(a.norm_w);
@@ -504,7 +507,7 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
         float v[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) v[r] = gh_wave_sum63(acc[0][r]);
-        if (lane == 63u) epilogue<R>(a, sg, 0, k * R, v, nullptr);
+        if (lane == 63u) epilogue<R, false>(a, sg, 0, k * R, v, nullptr);
     }
 }
 
