@@ -42,7 +42,11 @@ const KernelName kKernels[] = {
     {K_ATTN_G2, "gh_attn_g2"},             {K_ATTN_G4, "gh_attn_g4"},
     {K_ATTN_G8, "gh_attn_g8"},
     {K_STEP_ADVANCE, "gh_step_advance"},
-    {K_GEMM_Q4K, "gh_gemm_q4k"},           {K_GEMM_Q6K, "gh_gemm_q6k"},
+    {K_GEMM_Q4K_T128_R64, "gh_gemm_q4k_t128_r64"},   {K_GEMM_Q4K_T128_R128, "gh_gemm_q4k_t128_r128"},
+    {K_GEMM_Q4K_T256_R64, "gh_gemm_q4k_t256_r64"},   {K_GEMM_Q4K_T256_R96, "gh_gemm_q4k_t256_r96"},
+    {K_GEMM_Q4K_T256_R128, "gh_gemm_q4k_t256_r128"}, {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},
+    {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"}, {K_GEMM_Q6K_T256_R64, "gh_gemm_q6k_t256_r64"},
+    {K_GEMM_Q6K_T256_R96, "gh_gemm_q6k_t256_r96"},   {K_GEMM_Q6K_T256_R128, "gh_gemm_q6k_t256_r128"},
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
 };
 
@@ -754,19 +758,38 @@ int gh_embed(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* w, u
     return latch(enc, op_embed(b, x, w, token, embd, nullptr));
 }
 
-// Matrix-core GEMM for n >= kGemmMinTokens: 128 x 128 (tokens x rows) workgroup tiles; split-K
-// over the units when the tiles alone would leave resident workgroup slots idle.
+// Matrix-core GEMM for n >= kGemmMinTokens. Tile variants (tokens x rows per workgroup):
+// 128 x 64, 128 x 128, 256 x 64, 256 x 96, 256 x 128; split-K over the units when the tiles
+// alone would leave resident workgroup slots idle.
 constexpr uint32_t kGemmMinTokens = 8;
+
+struct GemmTile {
+    uint32_t tokens, rows, index;
+};
+constexpr GemmTile kGemmTiles[5] = {{128, 64, 0}, {128, 128, 1}, {256, 64, 2}, {256, 96, 3}, {256, 128, 4}};
 
 int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n) {
     const uint32_t in_dim = w->cols, rows = w->rows, units = in_dim / 64;
-    const GhKernel k = w->format == GH_FMT_Q4_K ? K_GEMM_Q4K : K_GEMM_Q6K;
-    const uint32_t tr = ceil_div(rows, 128), tt = ceil_div(n, 128), tiles = tr * tt;
-    static const uint32_t forced = [] {
+    static const int forced_tile = [] {
+        const char* e = std::getenv("GH_GEMM_TILE");
+        return e ? std::atoi(e) : -1;
+    }();
+    static const uint32_t forced_splits = [] {
         const char* e = std::getenv("GH_GEMM_SPLITS");
         return e ? (uint32_t)std::atoi(e) : 0u;
     }();
-    uint32_t splits = forced ? forced : std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles);
+    // default: 256-token tiles for long batches; rows per tile so the tile count fills the CUs
+    GemmTile tile;
+    if (forced_tile >= 0 && forced_tile < 5) {
+        tile = kGemmTiles[forced_tile];
+    } else if (n >= 256) {
+        tile = rows >= 8192 ? kGemmTiles[3] : kGemmTiles[2];
+    } else {
+        tile = rows >= 4096 ? kGemmTiles[1] : kGemmTiles[0];
+    }
+    const GhKernel k = (GhKernel)((w->format == GH_FMT_Q4_K ? K_GEMM_Q4K_T128_R64 : K_GEMM_Q6K_T128_R64) + tile.index);
+    const uint32_t tr = ceil_div(rows, tile.rows), tt = ceil_div(n, tile.tokens), tiles = tr * tt;
+    uint32_t splits = forced_splits ? forced_splits : std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles);
     splits = std::max<uint32_t>(1, std::min<uint32_t>({splits, std::max<uint32_t>(1, units / 8), 16u}));
     GhGemmArgs ga{a->addr, w->addr, out, 0, in_dim, rows, n, splits};
     if (splits > 1) {

@@ -51,8 +51,17 @@ enum GhKernel : int {
     K_ATTN_G4,
     K_ATTN_G8,
     K_STEP_ADVANCE,
-    K_GEMM_Q4K,
-    K_GEMM_Q6K,
+    // prefill GEMM tile variants (tokens x rows per workgroup), Q4_K then Q6_K
+    K_GEMM_Q4K_T128_R64,
+    K_GEMM_Q4K_T128_R128,
+    K_GEMM_Q4K_T256_R64,
+    K_GEMM_Q4K_T256_R96,
+    K_GEMM_Q4K_T256_R128,
+    K_GEMM_Q6K_T128_R64,
+    K_GEMM_Q6K_T128_R128,
+    K_GEMM_Q6K_T256_R64,
+    K_GEMM_Q6K_T256_R96,
+    K_GEMM_Q6K_T256_R128,
     K_GEMM_REDUCE,
     K_ATTN_PREFILL_G4,
     K_COUNT

@@ -1,14 +1,15 @@
 // Prefill GEMM on the matrix cores: out[t][r] = Σ_k x[t][k] · w[r][k] for n tokens of FP16
 // activations against Q4_K / Q6_K weights in the device layout (gh_kargs.h).
 //
-// Tiling: a 256-thread workgroup owns 128 tokens x 128 weight rows; its four waves own 64 x 64
-// each as 4 x 4 tiles of v_mfma_f32_16x16x32_f16 (A = activations, M = tokens; B = weights,
-// N = rows; FP32 accumulators). K advances one 64-weight unit per stage. Each stage, the
-// workgroup copies the x tile (128 x 64 FP16) and dequantizes the w tile (128 rows x 64) into
-// LDS: w = FP16(RNE(the reference's FP32 dequantized weight)), computed per weight exactly as
-// dequant_row does (Q4_K: (d·sc)·q - dmin·mn; Q6_K: (d·sc)·(q - 32); cpu/dequant.rs:93-123,
-// 274-308). LDS is double-buffered; the next unit's global loads are in flight while the
-// matrix cores run on the current one, and one barrier separates stages.
+// Tiling: a 256-thread workgroup owns 4·WT tokens x BR weight rows; wave w owns WT tokens x BR
+// rows as tiles of v_mfma_f32_32x32x16_f16 (A = activations, M = tokens, loaded from global
+// memory straight into registers; B = weights, N = rows; FP32 accumulators). K advances one
+// 64-weight unit per stage. Each stage the workgroup dequantizes the w tile (BR rows x 64)
+// into LDS: w = FP16(RNE(the reference's FP32 dequantized weight)), computed per weight
+// exactly as dequant_row does (Q4_K: (d·sc)·q - dmin·mn; Q6_K: (d·sc)·(q - 32);
+// cpu/dequant.rs:93-123, 274-308). The LDS tile is double-buffered; the next unit's weight
+// and activation loads are in flight while the matrix cores run on the current one, and one
+// barrier separates stages.
 //
 // A Q6_K unit's 64 weights are not contiguous in k (16 from each quarter of a 128-weight half
 // block); x is staged in the same permuted order, which leaves every dot product unchanged.
@@ -26,13 +27,11 @@
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kQ4K = 12, kQ6K = 14;
 constexpr int BK = 64;        // k per stage: one 64-weight unit
 constexpr int LDK = BK + 8;   // LDS row pitch in FP16 (144 B: conflict-free 16-byte reads)
-constexpr int BT = 128;       // tokens per workgroup
-constexpr int BR = 128;       // weight rows per workgroup
 
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)gh_f2h(a) | ((uint32_t)gh_f2h(b) << 16);
@@ -49,58 +48,34 @@ __device__ __forceinline__ uint32_t chunk_k(uint32_t u, uint32_t c) {
     }
 }
 
-struct XStage {
-    uint4 v0, v1, v2, v3;
-};
-
 struct WStage {
     uint4 q, hd, qh;  // Q4_K: q plane chunk + block header; Q6_K: ql chunk, scales, qh chunk
     uint32_t d;       // Q6_K: d (FP16 bits)
 };
 
-struct Tile {
-    uint32_t t0, r0, n, rows, in_dim, nb;
-};
-
+// Thread tid < 2·BR loads part (tid & 1) of weight row r0 + tid / 2 for unit u.
 template <uint32_t FMT>
-__device__ __forceinline__ void load_stage(const GhGemmArgs& a, const Tile& tl, uint32_t u,
-                                           XStage& xs, WStage& ws) {
-    const uint32_t tid = threadIdx.x;
-    // chunk c = tid + 256 i: token c / 8, FP16 chunk c % 8 (the same for every i)
-    const uint32_t kc = chunk_k<FMT>(u, tid & 7u);
-    auto xload = [&](uint32_t i) {
-        const uint32_t tok = min(tl.t0 + ((tid + 256u * i) >> 3), tl.n - 1);
-        return *gh_gp<uint4>(a.x + ((uint64_t)tok * tl.in_dim + kc) * 2);
-    };
-    xs.v0 = xload(0);
-    xs.v1 = xload(1);
-    xs.v2 = xload(2);
-    xs.v3 = xload(3);
-    const uint32_t row = min(tl.r0 + (tid >> 1), tl.rows - 1), part = tid & 1u;
-    const uint64_t nb = tl.nb, blk = (uint64_t)row * nb + (u >> 2);
+__device__ __forceinline__ void load_w(const GhGemmArgs& a, uint32_t r0, uint32_t u, WStage& ws) {
+    const uint32_t tid = threadIdx.x, nb = a.in_dim >> 8;
+    const uint32_t row = min(r0 + (tid >> 1), a.rows - 1), part = tid & 1u;
+    const uint64_t blk = (uint64_t)row * nb + (u >> 2);
     if constexpr (FMT == kQ4K) {
-        ws.q = *gh_gp<uint4>(a.w + (uint64_t)row * GH_Q4K_QS_BYTES * nb + part * nb * 64 + u * 16);
-        ws.hd = *gh_gp<uint4>(a.w + (uint64_t)tl.rows * GH_Q4K_QS_BYTES * nb + blk * 16);
+        ws.q = *gh_gp<uint4>(a.w + (uint64_t)row * GH_Q4K_QS_BYTES * nb + (uint64_t)part * nb * 64 + u * 16);
+        ws.hd = *gh_gp<uint4>(a.w + (uint64_t)a.rows * GH_Q4K_QS_BYTES * nb + blk * 16);
     } else {
         const uint64_t rq = a.w + (uint64_t)row * GH_Q6K_QLH_BYTES * nb + u * 16;
-        ws.q = *gh_gp<uint4>(rq + part * nb * 64);
-        ws.qh = *gh_gp<uint4>(rq + 2 * nb * 64);
-        ws.hd = *gh_gp<uint4>(a.w + (uint64_t)tl.rows * GH_Q6K_QLH_BYTES * nb + blk * 16);
-        ws.d = *gh_gp<uint16_t>(a.w + (uint64_t)tl.rows * 208 * nb + blk * 2);
+        ws.q = *gh_gp<uint4>(rq + (uint64_t)part * nb * 64);
+        ws.qh = *gh_gp<uint4>(rq + 2ull * nb * 64);
+        ws.hd = *gh_gp<uint4>(a.w + (uint64_t)a.rows * GH_Q6K_QLH_BYTES * nb + blk * 16);
+        ws.d = *gh_gp<uint16_t>(a.w + (uint64_t)a.rows * 208 * nb + blk * 2);
     }
 }
 
-// Copy x and dequantize w into one LDS buffer.
+// Dequantize the thread's 32 weights into its LDS row.
 template <uint32_t FMT>
-__device__ __forceinline__ void store_stage(uint32_t u, const XStage& xs, const WStage& ws,
-                                            _Float16* xb, _Float16* wb) {
+__device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* wb) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x;
-    _Float16* xd = xb + (tid >> 3) * LDK + (tid & 7u) * 8;  // + 32 tokens per i
-    *(uint4*)(xd) = xs.v0;
-    *(uint4*)(xd + 32 * LDK) = xs.v1;
-    *(uint4*)(xd + 64 * LDK) = xs.v2;
-    *(uint4*)(xd + 96 * LDK) = xs.v3;
     const uint32_t row = tid >> 1, part = tid & 1u;
     _Float16* dst = wb + row * LDK;
     const uint32_t qw[4] = {ws.q.x, ws.q.y, ws.q.z, ws.q.w};
@@ -121,11 +96,6 @@ __device__ __forceinline__ void store_stage(uint32_t u, const XStage& xs, const 
                 lo[2 * j + e / 2] = pack_h2(d1 * (float)(b0 & 0xFu) - m1, d1 * (float)(b1 & 0xFu) - m1);
                 hi[2 * j + e / 2] = pack_h2(d2 * (float)(b0 >> 4) - m2, d2 * (float)(b1 >> 4) - m2);
             }
-        // low nibbles: sub-block 2g, positions 16·part + i; high: sub-block 2g+1, 32 + 16·part + i
-        *(uint4*)(dst + 16 * part) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        *(uint4*)(dst + 16 * part + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-        *(uint4*)(dst + 32 + 16 * part) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *(uint4*)(dst + 40 + 16 * part) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
     } else {
         // part 0: ql plane a -> quarters 0 (low nibble, qh bits 0-1) and 2 (high, bits 4-5);
         // part 1: plane b -> quarters 1 (bits 2-3) and 3 (bits 6-7). Scale of quarter q:
@@ -151,85 +121,117 @@ __device__ __forceinline__ void store_stage(uint32_t u, const XStage& xs, const 
                 lo[2 * j + e / 2] = pack_h2(da * (float)qa0, da * (float)qa1);
                 hi[2 * j + e / 2] = pack_h2(db * (float)qb0, db * (float)qb1);
             }
-        *(uint4*)(dst + 16 * part) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        *(uint4*)(dst + 16 * part + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-        *(uint4*)(dst + 32 + 16 * part) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *(uint4*)(dst + 40 + 16 * part) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
     }
+    // low nibbles (quarter 2·part for Q6_K): positions 16·part + i; high: 32 + 16·part + i
+    *(uint4*)(dst + 16 * part) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *(uint4*)(dst + 16 * part + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+    *(uint4*)(dst + 32 + 16 * part) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *(uint4*)(dst + 40 + 16 * part) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
 }
 
-template <uint32_t FMT>
+// Tiling: 4 waves stacked along tokens; wave w owns tokens t0 + WT·w .. + WT, all BR rows of
+// the workgroup, as (WT/32) x (BR/32) tiles of v_mfma_f32_32x32x16_f16 (A = activations
+// straight from global memory into registers, B = weights from the LDS tile).
+template <uint32_t FMT, int WT, int BR>
 __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xbuf[2][BT * LDK];
+    constexpr int TI = WT / 32, TJ = BR / 32;
     __shared__ __attribute__((aligned(16))) _Float16 wbuf[2][BR * LDK];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    Tile tl{blockIdx.y * BT, blockIdx.x * BR, a.n, a.rows, a.in_dim, a.in_dim >> 8};
+    const uint32_t r0 = blockIdx.x * BR, t0 = blockIdx.y * (4 * WT) + wave * WT;
     const uint32_t units = a.in_dim / 64;
     const uint32_t per = (units + gridDim.z - 1) / gridDim.z;
     const uint32_t u0 = blockIdx.z * per, u1 = min(units, u0 + per);
-    const uint32_t wt = (wave & 1u) * 64, wr = (wave >> 1) * 64;  // this wave's sub-tile
-    const uint32_t fm = lane & 15u, fk = (lane >> 4) * 8;        // fragment row, k offset
+    const uint32_t fm = lane & 31u, fg = lane >> 5;  // fragment row, k half
+    const bool wload = threadIdx.x < 2 * BR;
 
-    f4 acc[4][4];
+    // A fragments of a unit: [i][sub-step ks of 16]: tokens t0 + 32 i + fm, LDS-order k chunk
+    // 2 ks + fg (8 halves)
+    const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
+    uint32_t trow[TI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TI; ++i) trow[i] = min(t0 + 32 * i + fm, a.n - 1) * a.in_dim;
+    auto load_x = [&](uint32_t u, h8 (&xf)[TI][4]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                xf[i][ks] = *(const GH_GLOBAL h8*)(x + trow[i] + chunk_k<FMT>(u, 2 * ks + fg));
+    };
+
+    f16v acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f16v{};
 
     if (u0 < u1) {
-        XStage xs;
         WStage ws;
-        load_stage<FMT>(a, tl, u0, xs, ws);
-        store_stage<FMT>(u0, xs, ws, xbuf[0], wbuf[0]);
+        h8 xf[TI][4], xn[TI][4];
+        if (wload) load_w<FMT>(a, r0, u0, ws);
+        load_x(u0, xf);
+        if (wload) store_w<FMT>(u0, ws, wbuf[0]);
         __syncthreads();
         for (uint32_t u = u0; u < u1; ++u) {
             const uint32_t cur = (u - u0) & 1u;
             const bool more = u + 1 < u1;
-            if (more) load_stage<FMT>(a, tl, u + 1, xs, ws);
-            const _Float16* xb = xbuf[cur];
+            if (more) {
+                if (wload) load_w<FMT>(a, r0, u + 1, ws);
+                load_x(u + 1, xn);
+            }
             const _Float16* wb = wbuf[cur];
 #pragma unroll
-            for (int kk = 0; kk < BK; kk += 32) {
-                h8 af[4], bf[4];
+            for (int ks = 0; ks < 4; ++ks) {
+                h8 bf[TJ];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) af[i] = *(const h8*)(xb + (wt + 16 * i + fm) * LDK + kk + fk);
+                for (int j = 0; j < TJ; ++j) bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) bf[j] = *(const h8*)(wb + (wr + 16 * j + fm) * LDK + kk + fk);
+                for (int i = 0; i < TI; ++i)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[i][ks], bf[j], acc[i][j], 0, 0, 0);
             }
-            if (more) store_stage<FMT>(u + 1, xs, ws, xbuf[cur ^ 1u], wbuf[cur ^ 1u]);
+            if (more && wload) store_w<FMT>(u + 1, ws, wbuf[cur ^ 1u]);
             __syncthreads();
+            if (more) {
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) xf[i][ks] = xn[i][ks];
+            }
         }
     }
 
-    // D[m][n] of tile (i, j): lane holds m = 4·(lane/16) + e, n = lane % 16.
-    const uint32_t row = tl.r0 + wr + fm;
+    // D of tile (i, j), register r: token t0 + 32 i + 8 (r / 4) + 4 fg + r % 4, row
+    // r0 + 32 j + fm
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t t = tl.t0 + wt + 16 * i + 4 * (lane >> 4) + e;
-            if (t >= tl.n) continue;
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t t = t0 + 32 * i + 8 * (r >> 2) + 4 * fg + (r & 3);
+            if (t >= a.n) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t r = row + 16 * j;
-                if (r >= tl.rows) continue;
+            for (int j = 0; j < TJ; ++j) {
+                const uint32_t row = r0 + 32 * j + fm;
+                if (row >= a.rows) continue;
                 if (gridDim.z == 1)
-                    gh_gpw<uint16_t>(a.out)[(uint64_t)t * tl.rows + r] = gh_f2h(acc[i][j][e]);
+                    gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] = gh_f2h(acc[i][j][r]);
                 else
-                    gh_gpw<float>(a.part)[((uint64_t)blockIdx.z * tl.n + t) * tl.rows + r] = acc[i][j][e];
+                    gh_gpw<float>(a.part)[((uint64_t)blockIdx.z * a.n + t) * a.rows + row] = acc[i][j][r];
             }
         }
 }
 
 }  // namespace
 
-GH_KERNEL __launch_bounds__(256) void gh_gemm_q4k(GhGemmArgs a) { gemm_body<kQ4K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemm_q6k(GhGemmArgs a) { gemm_body<kQ6K>(a); }
+// Tile variants: tokens per workgroup (4 waves x 32 or 64) x weight rows (64, 96, 128).
+#define GH_GEMM(SUF, WT, BR)                                                                       \
+    GH_KERNEL __launch_bounds__(256) void gh_gemm_q4k_##SUF(GhGemmArgs a) { gemm_body<kQ4K, WT, BR>(a); } \
+    GH_KERNEL __launch_bounds__(256) void gh_gemm_q6k_##SUF(GhGemmArgs a) { gemm_body<kQ6K, WT, BR>(a); }
+GH_GEMM(t128_r64, 32, 64)
+GH_GEMM(t128_r128, 32, 128)
+GH_GEMM(t256_r64, 64, 64)
+GH_GEMM(t256_r96, 64, 96)
+GH_GEMM(t256_r128, 64, 128)
 
 // Sum split-K partials in split order, round to FP16: out[i] = f16(Σ_s part[s][i]).
 GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce(GhGemmArgs a) {
