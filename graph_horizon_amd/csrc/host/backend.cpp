@@ -35,6 +35,8 @@ const KernelName kKernels[] = {
     {K_GEMV_Q4K_R1_D, "gh_gemv_q4k_r1_d"}, {K_GEMV_Q4K_R2_D, "gh_gemv_q4k_r2_d"},
     {K_GEMV_Q6K_R1_D, "gh_gemv_q6k_r1_d"}, {K_GEMV_Q6K_R2_D, "gh_gemv_q6k_r2_d"},
     {K_GEMV_Q4K_R4_D, "gh_gemv_q4k_r4_d"}, {K_GEMV_Q6K_R4_D, "gh_gemv_q6k_r4_d"},
+    {K_GEMV_Q4K_R1_K, "gh_gemv_q4k_r1_k"}, {K_GEMV_Q4K_R2_K, "gh_gemv_q4k_r2_k"},
+    {K_GEMV_Q6K_R1_K, "gh_gemv_q6k_r1_k"}, {K_GEMV_Q6K_R2_K, "gh_gemv_q6k_r2_k"},
     {K_RMSNORM, "gh_rmsnorm_x"},           {K_ROPE, "gh_rope"},
     {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
     {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
@@ -467,6 +469,18 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
             default: break;
         }
     }
+    static const bool no_splitk = std::getenv("GH_GEMV_NO_SPLITK") != nullptr;
+    const bool splitk = !no_splitk && !norm && n == 1 && nseg == 1 && !swiglu && in_dim > 4096 &&
+                        in_dim <= 16384;
+    if (splitk) {
+        switch (k) {
+            case K_GEMV_Q4K_R1: k = K_GEMV_Q4K_R1_K; break;
+            case K_GEMV_Q4K_R2: case K_GEMV_Q4K_R4: k = K_GEMV_Q4K_R2_K; r = 2; break;
+            case K_GEMV_Q6K_R1: k = K_GEMV_Q6K_R1_K; break;
+            case K_GEMV_Q6K_R2: case K_GEMV_Q6K_R4: k = K_GEMV_Q6K_R2_K; r = 2; break;
+            default: break;
+        }
+    }
     if (norm) {
         switch (k) {
             case K_GEMV_Q4K_R1: k = K_GEMV_Q4K_R1_N; break;
@@ -516,9 +530,11 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
         const char* e = std::getenv("GH_GEMV_MAX_WG");
         return e ? (uint32_t)std::atoi(e) : 0u;
     }();
-    if (direct) shmem = 0;
+    if (direct || splitk) shmem = 0;
     const uint32_t cap = max_wg ? max_wg : resident_wgs(b, k, 256, shmem);
-    return launch(b, k, std::max<uint32_t>(1, std::min<uint32_t>(ceil_div(task, 4), cap)), 1, 1, 256, &a, shmem);
+    // split-K: one task per workgroup (four waves share it); otherwise one per wave
+    const uint32_t want = splitk ? task : ceil_div(task, 4);
+    return launch(b, k, std::max<uint32_t>(1, std::min<uint32_t>(want, cap)), 1, 1, 256, &a, shmem);
 }
 
 int op_step_advance(gh_backend* b, void* scalars, void* history) {

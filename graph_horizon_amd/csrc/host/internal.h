@@ -39,6 +39,11 @@ enum GhKernel : int {
     K_GEMV_Q6K_R2_D,
     K_GEMV_Q4K_R4_D,
     K_GEMV_Q6K_R4_D,
+    // split-K variants (single token, one matrix, 4096 < in_dim <= 16384, no RMSNorm)
+    K_GEMV_Q4K_R1_K,
+    K_GEMV_Q4K_R2_K,
+    K_GEMV_Q6K_R1_K,
+    K_GEMV_Q6K_R2_K,
     K_RMSNORM,
     K_ROPE,
     K_SILU_MUL,

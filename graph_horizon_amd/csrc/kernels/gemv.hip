@@ -511,6 +511,50 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
     }
 }
 
+// Single-token launch of one matrix with 4096 < in_dim <= 16384: the four waves of a
+// workgroup split the in-dimension into quarters (wave w: units w·q .. w·q + q, one per lane,
+// q = ceil(units / 4)), each pairs its lanes' x slices in registers once, and every task's
+// loads go out from all four waves at once — one memory round trip per task instead of one
+// per 64-unit chunk. The four partial sums of a row are added in wave order through LDS.
+template <int R, uint32_t FMT>
+__device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a) {
+    __shared__ float part[4][R];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nb = a.in_dim >> 8;
+    const uint32_t units = nb * 4, q = (units + 3) / 4;
+    const uint32_t uw = wave * q + lane;                    // this lane's unit
+    const bool active = lane < q && uw < units;
+    const uint32_t u = min(uw, units - 1);
+    const GhGemvSeg sg = a.seg[0];
+    const uint8_t* w[1] = {(const uint8_t*)sg.w};
+    WRow<FMT> wr[1][R];
+    if (blockIdx.x < a.tasks) load_step<FMT, R, 1>(w, sg.rows, nb, blockIdx.x * R, u, wr);
+    const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x);
+    uint4 xv[8];
+    float4 xsum;
+    pair_unit<FMT>([&](uint32_t e) { return xh[e >> 3]; }, u, xv, xsum);
+    const Masks mk = make_masks();
+    for (uint32_t k = blockIdx.x; k < a.tasks; k += gridDim.x) {
+        if (k != blockIdx.x) load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
+        float acc[1][R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[0][r] = 0.0f;
+        if (active) compute_regs<FMT, R, 1>(xv, xsum, u, mk, wr, acc);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = gh_wave_sum63(acc[0][r]);
+            if (lane == 63u) part[wave][r] = v;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float v[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) v[r] = ((part[0][r] + part[1][r]) + part[2][r]) + part[3][r];
+            epilogue<R, false>(a, sg, 0, k * R, v, nullptr);
+        }
+        __syncthreads();
+    }
+}
+
 }  // namespace
 
 // NORM kernels (suffix _n) stage the RMSNorm of an FP32 x (norm_w set); the others read FP16 x.
@@ -532,4 +576,9 @@ GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_d(GhGemvArgs a) { gemv_dire
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_d(GhGemvArgs a) { gemv_direct<2, kQ6K>(a); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4_d(GhGemvArgs a) { gemv_direct<4, kQ4K>(a); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4_d(GhGemvArgs a) { gemv_direct<4, kQ6K>(a); }
+// split-K variants (suffix _k): single token, one matrix, 4096 < in_dim <= 16384, no RMSNorm
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_k(GhGemvArgs a) { gemv_splitk<1, kQ4K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_k(GhGemvArgs a) { gemv_splitk<2, kQ4K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_k(GhGemvArgs a) { gemv_splitk<1, kQ6K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_k(GhGemvArgs a) { gemv_splitk<2, kQ6K>(a); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4(GhGemvArgs a) { gemv_body<4, kModeQ6, false>(a); }
