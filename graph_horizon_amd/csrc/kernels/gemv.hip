@@ -90,15 +90,29 @@ __device__ __forceinline__ void pair_unit(const X8& x8, uint32_t u, uint4 (&xv)[
     }
 }
 
+// LDS staging, one (unit, quarter) per thread: unit u's 8 uint4 of pairs at xs[k * units + u]
+// (conflict-free b128 reads), its four quarter sums at sums[u] (Q4_K: quarters of its two
+// 32-weight halves, added pairwise by the reader in the order pair_unit adds them).
 template <uint32_t FMT, class X8>
 __device__ __forceinline__ void stage_x(const X8& x8, uint32_t units, uint4* xs, float4* sums) {
-    for (uint32_t u = threadIdx.x; u < units; u += blockDim.x) {
-        uint4 xv[8];
-        float4 sm;
-        pair_unit<FMT>(x8, u, xv, sm);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) xs[k * units + u] = xv[k];
-        sums[u] = sm;
+    for (uint32_t item = threadIdx.x; item < units * 4; item += blockDim.x) {
+        const uint32_t u = item >> 2, q = item & 3u;
+        uint4 p02, p13;
+        float sq;
+        if constexpr (FMT == kQ4K) {
+            // quarter q: chunks 2q, 2q+1 -> k = {0,2} (q=0), {1,3} (q=1), {4,6} (q=2), {5,7} (q=3)
+            const uint32_t e = (u >> 2) * 256 + (u & 3u) * 64 + 16 * q;
+            pair16(x8(e), x8(e + 8), p02, p13, sq);
+            const uint32_t k0 = (q & 1u) + 4 * (q >> 1);
+            xs[k0 * units + u] = p02;
+            xs[(k0 + 2) * units + u] = p13;
+        } else {
+            const uint32_t e = (u >> 2) * 256 + ((u >> 1) & 1u) * 128 + q * 32 + (u & 1u) * 16;
+            pair16(x8(e), x8(e + 8), p02, p13, sq);
+            xs[q * units + u] = p02;
+            xs[(4 + q) * units + u] = p13;
+        }
+        ((float*)&sums[u])[q] = sq;
     }
 }
 
@@ -232,7 +246,9 @@ __device__ __forceinline__ void compute_step(const uint4* xs, const float4* sums
     uint4 xv[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) xv[k] = xs[k * units + u];
-    compute_regs<FMT, R, M>(xv, sums[u], u, mk, wr, acc);
+    float4 xsum = sums[u];
+    if constexpr (FMT == kQ4K) xsum = make_float4(xsum.x + xsum.y, xsum.z + xsum.w, 0.0f, 0.0f);
+    compute_regs<FMT, R, M>(xv, xsum, u, mk, wr, acc);
 }
 
 __device__ __forceinline__ uint32_t position(const GhGemvArgs& a) {
