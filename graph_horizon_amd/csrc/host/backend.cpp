@@ -50,6 +50,7 @@ const KernelName kKernels[] = {
     {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"}, {K_GEMM_Q6K_T256_R64, "gh_gemm_q6k_t256_r64"},
     {K_GEMM_Q6K_T256_R96, "gh_gemm_q6k_t256_r96"},   {K_GEMM_Q6K_T256_R128, "gh_gemm_q6k_t256_r128"},
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
+    {K_ATTN_PREFILL_G4_Q16, "gh_attn_prefill_g4_q16"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -326,7 +327,13 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.base = base;
         a.rows = rows;
         a.scale = 1.0f / std::sqrt((float)kv->head_dim);
-        return launch(b, K_ATTN_PREFILL_G4, ceil_div(rows, 32), kv->kv_heads, 1, 256, &a);
+        // 16 query rows per workgroup (two resident workgroups per CU) or 32 (one)
+        static const uint32_t qrows = [] {
+            const char* e = std::getenv("GH_ATTN_PREFILL_ROWS");
+            return e && std::atoi(e) == 32 ? 32u : 16u;
+        }();
+        return launch(b, qrows == 16 ? K_ATTN_PREFILL_G4_Q16 : K_ATTN_PREFILL_G4, ceil_div(rows, qrows),
+                      kv->kv_heads, 1, 256, &a);
     }
     const uint32_t splits = attention_splits(b, max_pos + 1, kv->kv_heads, rows);
     // bound the partials: rows in groups that fit a 256 MiB workspace

@@ -69,6 +69,7 @@ enum GhKernel : int {
     K_GEMM_Q6K_T256_R128,
     K_GEMM_REDUCE,
     K_ATTN_PREFILL_G4,
+    K_ATTN_PREFILL_G4_Q16,
     K_COUNT
 };
 

@@ -245,8 +245,8 @@ GH_KERNEL __launch_bounds__(256) void gh_attn_g8(GhAttnArgs a) { attn_body<8>(a)
 // Causal GQA prefill attention on the matrix cores (flash attention, G = 4 query heads per kv
 // head, head_dim = value_dim = 128).
 //
-// Grid (query blocks of 32 rows, kv heads), 256 threads; wave w owns query head 4·kvh + w for
-// the block's 32 rows, so every K/V tile staged in LDS serves all four heads. Per tile of 64
+// Grid (query blocks of 16·QT rows, kv heads), 256 threads; wave w owns query head 4·kvh + w
+// for the block's rows, so every K/V tile staged in LDS serves all four heads. Per tile of 64
 // key positions, with v_mfma_f32_16x16x32_f16 and FP32 accumulators:
 //   S^T = K · Q^T   A = K rows (LDS), B = the wave's FP16 query rows (registers); the output
 //                   layout gives each lane one query row (lane % 16) and four key positions
@@ -262,7 +262,6 @@ namespace {
 typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPQ = 32;          // query rows per workgroup
 constexpr int kPK = 64;          // key positions per tile
 constexpr int kKP = 128 + 8;     // K tile pitch (FP16): [64 keys][128 dims]
 constexpr int kVP = kPK + 8;     // V^T tile pitch (FP16): [128 dims][64 keys]
@@ -327,7 +326,9 @@ __device__ __forceinline__ float xor_sum(float v) {
     return v + __shfl_xor(v, 32, 64);
 }
 
+template <int QT>  // query tiles of 16 rows per wave
 __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
+    constexpr uint32_t kPQ = 16 * QT;  // query rows per workgroup
     __shared__ __attribute__((aligned(16))) _Float16 kt[2][kPK * kKP];
     __shared__ __attribute__((aligned(16))) _Float16 vt[2][128 * kVP];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -344,20 +345,27 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
     const float sl2 = a.scale * 1.4426950408889634f;  // scores in base-2 units
 
     // this wave's query rows as B operands: [q tile t][k step ks] = dims 32 ks + 8 fg .. + 8
-    ah8 qf[2][4];
+    ah8 qf[QT][4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < QT; ++t) {
         const uint32_t r = min(q0 + 16 * t + fr, a.rows - 1);
         const GH_GLOBAL uint4* qp = gh_gp<uint4>(a.q + (((uint64_t)r * a.q_heads + h) * 128 + 8 * fg) * 2);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qf[t][ks] = __builtin_bit_cast(ah8, qp[4 * ks]);
     }
-    const uint32_t qpos[2] = {a.base + q0 + fr, a.base + q0 + 16 + fr};
-
-    af4 o[8][2];
+    uint32_t qpos[QT];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j][0] = o[j][1] = af4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m[2] = {-__builtin_inff(), -__builtin_inff()}, l[2] = {0.0f, 0.0f};
+    for (int t = 0; t < QT; ++t) qpos[t] = a.base + q0 + 16 * t + fr;
+
+    af4 o[8][QT];
+    float m[QT], l[QT];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j][t] = af4{0.0f, 0.0f, 0.0f, 0.0f};
+        m[t] = -__builtin_inff();
+        l[t] = 0.0f;
+    }
 
     KVStage st;
     kv_load(a, kc, vc, kv_row, 0, kv_end, st);
@@ -370,21 +378,23 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
         const _Float16* kb = kt[cur];
         const _Float16* vb = vt[cur];
         // S^T tiles: [key tile kk][q tile t], lane holds keys 16 kk + 4 fg + e of query fr
-        af4 s[4][2];
+        af4 s[4][QT];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            s[kk][0] = s[kk][1] = af4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < QT; ++t) s[kk][t] = af4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const ah8 kf = *(const ah8*)(kb + (16 * kk + fr) * kKP + 32 * ks + 8 * fg);
-                s[kk][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][ks], s[kk][0], 0, 0, 0);
-                s[kk][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][ks], s[kk][1], 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < QT; ++t)
+                    s[kk][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[t][ks], s[kk][t], 0, 0, 0);
             }
         }
         // online softmax per query row (lane), P as FP16 hi/lo B operands in key-slot order
-        ah8 ph[2][2], pl[2][2];  // [k step (keys 32 ks2 ..)][q tile]
+        ah8 ph[2][QT], pl[2][QT];  // [k step (keys 32 ks2 ..)][q tile]
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < QT; ++t) {
             float v[4][4];
             float mx = -__builtin_inff();
 #pragma unroll
@@ -429,7 +439,7 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
                 const uint2 va = *(const uint2*)vr, vb2 = *(const uint2*)(vr + 16);
                 const ah8 vf = __builtin_bit_cast(ah8, make_uint4(va.x, va.y, vb2.x, vb2.y));
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
+                for (int t = 0; t < QT; ++t) {
                     o[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[ks2][t], o[j][t], 0, 0, 0);
                     o[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[ks2][t], o[j][t], 0, 0, 0);
                 }
@@ -439,7 +449,7 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
     }
     // O^T tile (j, t): lane holds dims 16 j + 4 fg + e of query row q0 + 16 t + fr
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < QT; ++t) {
         const uint32_t r = q0 + 16 * t + fr;
         const float inv = 1.0f / xor_sum(l[t]);
         if (r >= a.rows) continue;
@@ -454,4 +464,5 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
 }
 }  // namespace
 
-GH_KERNEL __launch_bounds__(256) void gh_attn_prefill_g4(GhAttnArgs a) { attn_prefill_g4(a); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_prefill_g4(GhAttnArgs a) { attn_prefill_g4<2>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_prefill_g4_q16(GhAttnArgs a) { attn_prefill_g4<1>(a); }
