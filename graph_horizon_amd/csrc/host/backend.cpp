@@ -327,10 +327,11 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.base = base;
         a.rows = rows;
         a.scale = 1.0f / std::sqrt((float)kv->head_dim);
-        // 16 query rows per workgroup (two resident workgroups per CU) or 32 (one)
+        // 32 query rows per workgroup (K/V tiles shared by twice the rows; 248 VGPRs keep two
+        // workgroups resident per CU) or 16 (GH_ATTN_PREFILL_ROWS=16, for comparison)
         static const uint32_t qrows = [] {
             const char* e = std::getenv("GH_ATTN_PREFILL_ROWS");
-            return e && std::atoi(e) == 32 ? 32u : 16u;
+            return e && std::atoi(e) == 16 ? 16u : 32u;
         }();
         return launch(b, qrows == 16 ? K_ATTN_PREFILL_G4_Q16 : K_ATTN_PREFILL_G4, ceil_div(rows, qrows),
                       kv->kv_heads, 1, 256, &a);

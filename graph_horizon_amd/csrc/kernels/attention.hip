@@ -263,8 +263,21 @@ typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPK = 64;          // key positions per tile
-constexpr int kKP = 128 + 8;     // K tile pitch (FP16): [64 keys][128 dims]
-constexpr int kVP = kPK + 8;     // V^T tile pitch (FP16): [128 dims][64 keys]
+// LDS pitches, chosen so that every 16-byte fragment read is free of bank conflicts on gfx950
+// (ds_read_b128 serves 32 lanes per pass over 128 four-byte banks): 16 key rows x 2 chunks or
+// 16 dim rows x 2 chunks per pass land on 32 distinct bank quads.
+constexpr int kKP = 128 + 16;    // K tile pitch (FP16): [64 keys][128 dims], 288 B
+constexpr int kVP = kPK + 16;    // V^T tile pitch (FP16): [128 dims][64 keys, slot order], 160 B
+
+// V^T keeps keys in MFMA k-slot order: within each group of 32 keys, key 16h + 4f + i sits at
+// slot 8f + 4h + i, so lane group f's eight slots (keys 4f .. 4f+3 and 16+4f .. 16+4f+3, the
+// keys its P values belong to) are one contiguous 16-byte run.
+__device__ __forceinline__ uint32_t vt_slot(uint32_t key) {
+    return (key & ~31u) + 8 * ((key >> 2) & 3u) + 4 * ((key >> 4) & 1u) + (key & 3u);
+}
+
+// Buffer resource word 3 for gfx9-family raw buffers (32-bit data format, no swizzle).
+constexpr int kBufWord3 = 0x00020000;
 
 struct KVStage {
     uint4 k0, k1, k2, k3;  // K: chunk (key c/16, dims 8·(c%16)), c = tid + 256 i
@@ -274,26 +287,45 @@ struct KVStage {
 __device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xFFFF0000u); }
 
-__device__ __forceinline__ void kv_load(const GhAttnArgs& a, const uint16_t* kc, const uint16_t* vc,
-                                        size_t kv_row, uint32_t t0, uint32_t kv_end, KVStage& s) {
-    const uint32_t tid = threadIdx.x;
-    auto kld = [&](uint32_t i) {
-        const uint32_t c = tid + 256u * i, p = min(t0 + (c >> 4), kv_end - 1);
-        return *gh_gp<uint4>((uint64_t)(kc + (size_t)p * kv_row + (c & 15u) * 8));
+// Per-thread byte offsets of the K / V chunks a thread stages, relative to the tile's first key.
+struct KVOffsets {
+    uint32_t k[4], v[4];
+};
+
+__device__ __forceinline__ KVOffsets kv_offsets(uint32_t kv_row) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t dg = (lane >> 4) + 4 * (tid >> 6), kg = lane & 15u;
+    KVOffsets o;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t c = tid + 256u * i;  // K: key c / 16, dims 8·(c % 16)
+        o.k[i] = ((c >> 4) * kv_row + (c & 15u) * 8) * 2;
+        o.v[i] = ((4 * kg + i) * kv_row + dg * 8) * 2;  // V: key 4·kg + i, dims 8·dg
+    }
+    return o;
+}
+
+// Stage keys t0 .. t0+63 through buffer loads whose range ends at key kv_end: the hardware
+// returns zeros past it (those keys are causally masked and carry zero weight), so no per-load
+// clamp or 64-bit address arithmetic is needed.
+__device__ __forceinline__ void kv_load(const uint16_t* kc, const uint16_t* vc, uint32_t kv_row,
+                                        uint32_t t0, uint32_t kv_end, const KVOffsets& off, KVStage& s) {
+    const uint32_t bytes = (kv_end - t0) * kv_row * 2;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(kc + (size_t)t0 * kv_row), 0, (int)bytes, kBufWord3);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(vc + (size_t)t0 * kv_row), 0, (int)bytes, kBufWord3);
+    auto ld = [](__amdgpu_buffer_rsrc_t r, uint32_t o) {
+        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
     };
-    s.k0 = kld(0);
-    s.k1 = kld(1);
-    s.k2 = kld(2);
-    s.k3 = kld(3);
-    const uint32_t lane = tid & 63u, dg = (lane >> 4) + 4 * (tid >> 6), kg = lane & 15u;
-    auto vld = [&](uint32_t i) {
-        const uint32_t p = min(t0 + 4 * kg + i, kv_end - 1);
-        return *gh_gp<uint4>((uint64_t)(vc + (size_t)p * kv_row + dg * 8));
-    };
-    s.v0 = vld(0);
-    s.v1 = vld(1);
-    s.v2 = vld(2);
-    s.v3 = vld(3);
+    s.k0 = ld(rk, off.k[0]);
+    s.k1 = ld(rk, off.k[1]);
+    s.k2 = ld(rk, off.k[2]);
+    s.k3 = ld(rk, off.k[3]);
+    s.v0 = ld(rv, off.v[0]);
+    s.v1 = ld(rv, off.v[1]);
+    s.v2 = ld(rv, off.v[2]);
+    s.v3 = ld(rv, off.v[3]);
 }
 
 __device__ __forceinline__ void kv_store(const KVStage& s, _Float16* kt, _Float16* vt) {
@@ -309,7 +341,7 @@ __device__ __forceinline__ void kv_store(const KVStage& s, _Float16* kt, _Float1
     const uint32_t r1[4] = {s.v1.x, s.v1.y, s.v1.z, s.v1.w};
     const uint32_t r2[4] = {s.v2.x, s.v2.y, s.v2.z, s.v2.w};
     const uint32_t r3[4] = {s.v3.x, s.v3.y, s.v3.z, s.v3.w};
-    _Float16* vd = vt + (dg * 8) * kVP + kg * 4;
+    _Float16* vd = vt + (dg * 8) * kVP + vt_slot(kg * 4);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         *(uint2*)(vd + (2 * c) * kVP) = make_uint2(lo_pair(r0[c], r1[c]), lo_pair(r2[c], r3[c]));
@@ -317,14 +349,29 @@ __device__ __forceinline__ void kv_store(const KVStage& s, _Float16* kt, _Float1
     }
 }
 
+// Reductions over the four lanes l, l^16, l^32, l^48 (one query row's lane group) with the
+// gfx950 row-swap moves: v_permlane16_swap pairs rows 0/1 and 2/3, v_permlane32_swap pairs the
+// wave halves; each swap leaves both partners' values in the two registers, in the same order
+// in every lane, so all four lanes end with bit-identical results.
 __device__ __forceinline__ float xor_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float xor_sum(float v) {
-    v += __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+
+template <bool B>
+struct Flag {
+    static constexpr bool value = B;
+};
+typedef float af2 __attribute__((ext_vector_type(2)));
+typedef _Float16 ah2 __attribute__((ext_vector_type(2)));
 
 template <int QT>  // query tiles of 16 rows per wave
 __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
@@ -367,14 +414,20 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
         l[t] = 0.0f;
     }
 
+    const uint32_t kv_row32 = (uint32_t)kv_row;
+    const KVOffsets off = kv_offsets(kv_row32);
     KVStage st;
-    kv_load(a, kc, vc, kv_row, 0, kv_end, st);
+    kv_load(kc, vc, kv_row32, 0, kv_end, off, st);
     kv_store(st, kt[0], vt[0]);
     __syncthreads();
-    for (uint32_t tile = 0; tile < ntiles; ++tile) {
+    // Tiles whose last key is at or before the block's first query position need no causal
+    // mask (nor do they hold the clamped duplicates past kv_end); only the diagonal ones do.
+    const uint32_t first_pos = a.base + q0;
+    auto step = [&](uint32_t tile, auto masked) {
+        constexpr bool kMask = decltype(masked)::value;
         const uint32_t cur = tile & 1u, t0 = tile * kPK;
         const bool more = tile + 1 < ntiles;
-        if (more) kv_load(a, kc, vc, kv_row, t0 + kPK, kv_end, st);
+        if (more) kv_load(kc, vc, kv_row32, t0 + kPK, kv_end, off, st);
         const _Float16* kb = kt[cur];
         const _Float16* vb = vt[cur];
         // S^T tiles: [key tile kk][q tile t], lane holds keys 16 kk + 4 fg + e of query fr
@@ -401,19 +454,23 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
             for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t p = t0 + 16 * kk + 4 * fg + e;
-                    v[kk][e] = p <= qpos[t] ? s[kk][t][e] * sl2 : -__builtin_inff();
+                    v[kk][e] = s[kk][t][e];
+                    if constexpr (kMask)
+                        if (t0 + 16 * kk + 4 * fg + e > qpos[t]) v[kk][e] = -__builtin_inff();
                     mx = fmaxf(mx, v[kk][e]);
                 }
-            const float m_new = fmaxf(m[t], xor_max(mx));  // finite: key 0 is in tile 0
-            const float f = exp2f(m[t] - m_new);
+            // sl2 > 0, so the row max of the scaled scores is sl2 · (row max of the raw ones);
+            // finite: key 0 is in tile 0. v_exp_f32 directly: weights below 2^-126 (flushed
+            // to zero) are far below the FP32 accumulation error of the sums they enter.
+            const float m_new = fmaxf(m[t], xor_max(mx) * sl2);
+            const float f = __builtin_amdgcn_exp2f(m[t] - m_new);
             m[t] = m_new;
             float sum = 0.0f;
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    v[kk][e] = exp2f(v[kk][e] - m_new);
+                    v[kk][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[kk][e], sl2, -m_new));
                     sum += v[kk][e];
                 }
             l[t] = l[t] * f + sum;
@@ -422,22 +479,23 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float pv = v[2 * ks2 + (e >> 2)][e & 3];
-                    const _Float16 hi = (_Float16)pv;
-                    ph[ks2][t][e] = hi;
-                    pl[ks2][t][e] = (_Float16)(pv - (float)hi);
+                for (int e = 0; e < 8; e += 2) {
+                    const af2 pv = {v[2 * ks2 + (e >> 2)][e & 3], v[2 * ks2 + (e >> 2)][(e & 3) + 1]};
+                    const ah2 hi = __builtin_convertvector(pv, ah2);  // round to nearest even
+                    const ah2 lo = __builtin_convertvector(pv - __builtin_convertvector(hi, af2), ah2);
+                    ph[ks2][t][e] = hi[0];
+                    ph[ks2][t][e + 1] = hi[1];
+                    pl[ks2][t][e] = lo[0];
+                    pl[ks2][t][e + 1] = lo[1];
                 }
         }
         // O^T += V^T P^T: A = V^T rows (dims 16 j + fr), k-slots = keys 32 ks2 + {4 fg .. +3,
-        // 16 + 4 fg .. +3}, the same keys the lane's P values belong to
+        // 16 + 4 fg .. +3} (one 16-byte run in slot order), the keys the lane's P values hold
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2) {
-                const _Float16* vr = vb + (16 * j + fr) * kVP + 32 * ks2 + 4 * fg;
-                const uint2 va = *(const uint2*)vr, vb2 = *(const uint2*)(vr + 16);
-                const ah8 vf = __builtin_bit_cast(ah8, make_uint4(va.x, va.y, vb2.x, vb2.y));
+                const ah8 vf = *(const ah8*)(vb + (16 * j + fr) * kVP + 32 * ks2 + 8 * fg);
 #pragma unroll
                 for (int t = 0; t < QT; ++t) {
                     o[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[ks2][t], o[j][t], 0, 0, 0);
@@ -446,7 +504,10 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
             }
         if (more) kv_store(st, kt[cur ^ 1u], vt[cur ^ 1u]);
         __syncthreads();
-    }
+    };
+    uint32_t tile = 0;
+    for (; tile < ntiles && tile * kPK + kPK - 1 <= first_pos; ++tile) step(tile, Flag<false>{});
+    for (; tile < ntiles; ++tile) step(tile, Flag<true>{});
     // O^T tile (j, t): lane holds dims 16 j + 4 fg + e of query row q0 + 16 t + fr
 #pragma unroll
     for (int t = 0; t < QT; ++t) {

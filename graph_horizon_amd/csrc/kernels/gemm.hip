@@ -53,11 +53,12 @@ struct WStage {
     uint32_t d;       // Q6_K: d (FP16 bits)
 };
 
-// Thread tid < 2·BR loads part (tid & 1) of weight row r0 + tid / 2 for unit u.
-template <uint32_t FMT>
+// Thread tid < 2·BR loads part tid / BR of weight row r0 + tid % BR for unit u (consecutive
+// lanes on consecutive rows: their 16-byte LDS stores, one row pitch apart, hit distinct banks).
+template <uint32_t FMT, int BR>
 __device__ __forceinline__ void load_w(const GhGemmArgs& a, uint32_t r0, uint32_t u, WStage& ws) {
     const uint32_t tid = threadIdx.x, nb = a.in_dim >> 8;
-    const uint32_t row = min(r0 + (tid >> 1), a.rows - 1), part = tid & 1u;
+    const uint32_t row = min(r0 + tid % BR, a.rows - 1), part = tid / BR;
     const uint64_t blk = (uint64_t)row * nb + (u >> 2);
     if constexpr (FMT == kQ4K) {
         ws.q = *gh_gp<uint4>(a.w + (uint64_t)row * GH_Q4K_QS_BYTES * nb + (uint64_t)part * nb * 64 + u * 16);
@@ -72,11 +73,11 @@ __device__ __forceinline__ void load_w(const GhGemmArgs& a, uint32_t r0, uint32_
 }
 
 // Dequantize the thread's 32 weights into its LDS row.
-template <uint32_t FMT>
+template <uint32_t FMT, int BR>
 __device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* wb) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x;
-    const uint32_t row = tid >> 1, part = tid & 1u;
+    const uint32_t row = tid % BR, part = tid / BR;
     _Float16* dst = wb + row * LDK;
     const uint32_t qw[4] = {ws.q.x, ws.q.y, ws.q.z, ws.q.w};
     uint32_t lo[8], hi[8];
@@ -167,15 +168,15 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
     if (u0 < u1) {
         WStage ws;
         h8 xf[TI][4], xn[TI][4];
-        if (wload) load_w<FMT>(a, r0, u0, ws);
+        if (wload) load_w<FMT, BR>(a, r0, u0, ws);
         load_x(u0, xf);
-        if (wload) store_w<FMT>(u0, ws, wbuf[0]);
+        if (wload) store_w<FMT, BR>(u0, ws, wbuf[0]);
         __syncthreads();
         for (uint32_t u = u0; u < u1; ++u) {
             const uint32_t cur = (u - u0) & 1u;
             const bool more = u + 1 < u1;
             if (more) {
-                if (wload) load_w<FMT>(a, r0, u + 1, ws);
+                if (wload) load_w<FMT, BR>(a, r0, u + 1, ws);
                 load_x(u + 1, xn);
             }
             const _Float16* wb = wbuf[cur];
@@ -190,7 +191,7 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
                     for (int j = 0; j < TJ; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[i][ks], bf[j], acc[i][j], 0, 0, 0);
             }
-            if (more && wload) store_w<FMT>(u + 1, ws, wbuf[cur ^ 1u]);
+            if (more && wload) store_w<FMT, BR>(u + 1, ws, wbuf[cur ^ 1u]);
             __syncthreads();
             if (more) {
 #pragma unroll

@@ -383,7 +383,10 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // Staged x lives in dynamic LDS: 144 B per 64-weight unit (twice for the mixed kernel).
 // Waves are split between the segments in proportion to their tasks (args: seg.task0 is the
 // first task index, the wave split is recomputed here), so a wave only ever runs one format.
-template <int R, int MODE, bool NORM>
+// PRIME: request the first step's weights before x is staged (their latency overlaps the
+// staging). Off for the RMSNorm variants: their staging is short (x and the norm weights are
+// cache-resident) and the held registers cost more than the overlap gains (measured on decode).
+template <int R, int MODE, bool NORM, bool PRIME = !NORM>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
     extern __shared__ uint4 lds[];
     constexpr int M = MODE == kModeSwiglu ? 2 : 1;
@@ -419,7 +422,7 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
     // staged, so their latency overlaps the staging.
     constexpr uint32_t F0 = MODE == kModeQ6 ? kQ6K : kQ4K;
     WRow<F0> w0r[M][R];
-    const bool primed = !NORM && sg.fmt == F0 && first < ntask;
+    const bool primed = PRIME && sg.fmt == F0 && first < ntask;
     if (primed) {
         const uint8_t* w[M];
         w[0] = (const uint8_t*)sg.w;
@@ -581,7 +584,13 @@ GH_GEMV(gh_gemv_q4k_r1, 1, kModeQ4)
 GH_GEMV(gh_gemv_q4k_r2, 2, kModeQ4)
 GH_GEMV(gh_gemv_q6k_r1, 1, kModeQ6)
 GH_GEMV(gh_gemv_q6k_r2, 2, kModeQ6)
-GH_GEMV(gh_gemv_mixed_r2, 2, kModeMixed)
+GH_KERNEL __launch_bounds__(256) void gh_gemv_mixed_r2(GhGemvArgs a) { gemv_body<2, kModeMixed, false>(a); }
+// The RMSNorm mixed (Q/K/V) kernel is held to 168 VGPRs, three waves per SIMD: with 3 x 256
+// CUs x 4 waves resident, an 8B-shaped QKV launch (4096 + 1024 + 1024 rows, R = 2) is one task
+// per wave instead of two rounds.
+GH_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gh_gemv_mixed_r2_n(GhGemvArgs a) {
+    gemv_body<2, kModeMixed, true>(a);
+}
 GH_GEMV(gh_gemv_swiglu_r1, 1, kModeSwiglu)
 GH_GEMV(gh_gemv_swiglu_r2, 2, kModeSwiglu)
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4(GhGemvArgs a) { gemv_body<4, kModeQ4, false>(a); }
