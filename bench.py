@@ -213,7 +213,7 @@ def main():
             "unit": "GB/s",
             "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
             "traffic": ROOFLINE_TRAFFIC_BYTES if (d, ffn) == (4096, 12288) else None,
-            "kernel": f"gh_gemv_q4k (Q4_K GEMV {ffn}x{d}, {gemv_bytes} B/launch)",
+            "kernel": f"gh_gemv_q4k_r2_d (Q4_K GEMV {ffn}x{d}, {gemv_bytes} B/launch)",
             "avg_us": round(gemv_ms * 1e3, 3),
         },
     }
@@ -221,6 +221,7 @@ def main():
     result["config"]["q4k_gemv_c1_shape"] = c1
     result["config"]["prefill_gemm_c3"] = prefill_gemm(hip, model, shape, 512)
     model.close()
+    result["config"]["attention_c4"] = c4_attention(hip, shape)
     hip.close()
     if not args.no_cpu:
         log("bench: CPU baseline ...")
@@ -228,11 +229,11 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-# HBM bytes per launch of the roofline kernel (gh_gemv_q4k_r2 at 12288x4096), from the two
+# HBM bytes per launch of the roofline kernel (gh_gemv_q4k_r2_d at 12288x4096), from the two
 # rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --traffic-probe`, each scaled by
 # the same counter's reading for a 256 MiB device-to-device copy (FETCH_SIZE x 2.0, WRITE_SIZE
 # x 1.0): profiles/q4k_gemv_12288x4096.txt. Re-measure whenever the kernel changes.
-ROOFLINE_TRAFFIC_BYTES = 28534276
+ROOFLINE_TRAFFIC_BYTES = 28513212
 
 
 def traffic_probe(shape):
@@ -315,6 +316,60 @@ def prefill_gemm(hip, model, shape, n):
         log(f"bench: prefill GEMM {name} {n}x{ind}->{outd}: {ms * 1e3:.1f} us, {tflops:.0f} TFLOP/s")
     for b in (a_d, a_f, y):
         hip.free_buffer(b)
+    return out
+
+
+def c4_attention(hip, shape):
+    """GQA attention over the f16 KV cache at the model's heads — the
+    2048-row causal prefill on the matrix cores, and single-token decode at ctx 4096 and 32768.
+    Decode rotates over distinct layers of a >= 671 MB cache (40 x 4096 / 5 x 32768 positions),
+    so the 256 MB MALL cannot serve the K/V stream. HIP-event timing on the backend stream."""
+    import ctypes as C
+
+    from graph_horizon_amd import _ffi as F
+
+    qh, kvh, hd = shape.head_count, shape.kv_head_count, shape.head_dim
+    rng = np.random.default_rng(13)
+    out = {}
+    for ctx, layers in ((2048, 8), (4096, 40), (32768, 5)):
+        per_layer = ctx * kvh * hd
+        k1, v1 = synth_f16(rng, per_layer), synth_f16(rng, per_layer)
+        kb, vb = hip.from_host(np.tile(k1, layers)), hip.from_host(np.tile(v1, layers))
+        del k1, v1
+        kv = F.GhKv(kb, vb, F.KV_F16, layers, ctx, kvh, hd, hd)
+        rows = ctx if ctx == 2048 else 1
+        qb = hip.from_host(synth_f16(rng, rows * qh * hd))
+        ob = hip.alloc_buffer(rows * qh * hd * 2)
+
+        def launch(enc, layer):
+            if rows > 1:
+                return hip.lib.gh_attention_prefill(hip.h, enc, C.byref(ob), C.byref(qb), C.byref(kv),
+                                                    qh, 0, rows, layer)
+            return hip.lib.gh_attention_decode(hip.h, enc, C.byref(ob), C.byref(qb), C.byref(kv),
+                                               qh, ctx - 1, layer)
+        enc = hip.begin()
+        launch(enc, 0)
+        hip.submit()
+        reps = 3 if rows > 1 else 5
+        enc = hip.begin()
+        hip.timer_start()
+        for _ in range(reps):
+            for layer in range(layers):
+                launch(enc, layer)
+        ms = hip.timer_stop() / (reps * layers)
+        hip.submit()
+        if rows > 1:
+            tflops = 4.0 * qh * hd * (rows * (rows + 1) / 2) / (ms * 1e-3) / 1e12
+            out["prefill_2048"] = {"avg_us": round(ms * 1e3, 1), "tflops": round(tflops, 1),
+                                   "frac_f16_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+            log(f"bench: attention prefill 2048 causal rows: {ms * 1e3:.1f} us, {tflops:.0f} TFLOP/s")
+        else:
+            gbps = 2 * per_layer * 2 / (ms * 1e-3) / 1e9
+            out[f"decode_{ctx}"] = {"avg_us": round(ms * 1e3, 2), "gbps": round(gbps, 1),
+                                    "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+            log(f"bench: attention decode ctx {ctx}: {ms * 1e3:.2f} us/layer, {gbps:.0f} GB/s")
+        for b in (kb, vb, qb, ob):
+            hip.free_buffer(b)
     return out
 
 

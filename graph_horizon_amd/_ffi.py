@@ -68,6 +68,12 @@ class GhModelConfig(C.Structure):
 MODEL_NO_GRAPH = 1
 
 
+class GhGgufTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_uint32), ("type", C.c_uint32),
+                ("dims", C.c_uint64 * 4), ("offset", C.c_uint64), ("nbytes", C.c_uint64),
+                ("data", C.c_void_p)]
+
+
 P = C.c_void_p
 BUFP = C.POINTER(GhBuf)
 U32, U64, F32, I32 = C.c_uint32, C.c_uint64, C.c_float, C.c_int
@@ -117,6 +123,19 @@ SIGNATURES = {
     "gh_model_kv": (I32, [P, C.POINTER(GhKv)]),
     "gh_model_read_x": (I32, [P, P]),
     "gh_model_weight": (I32, [P, U32, U32, BUFP]),
+    "gh_gguf_last_error": (C.c_char_p, []),
+    "gh_gguf_open": (I32, [C.c_char_p, C.POINTER(P)]),
+    "gh_gguf_close": (None, [P]),
+    "gh_gguf_info": (I32, [P, C.POINTER(U32), C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)]),
+    "gh_gguf_tensor": (I32, [P, U64, C.POINTER(GhGgufTensorInfo)]),
+    "gh_gguf_find": (I32, [P, C.c_char_p, C.POINTER(U64)]),
+    "gh_gguf_meta_u64": (I32, [P, C.c_char_p, C.POINTER(U64)]),
+    "gh_gguf_meta_f64": (I32, [P, C.c_char_p, C.POINTER(C.c_double)]),
+    "gh_gguf_meta_str": (C.c_char_p, [P, C.c_char_p]),
+    "gh_gguf_meta_array_len": (I32, [P, C.c_char_p, C.POINTER(U64)]),
+    "gh_gguf_model_config": (I32, [P, U32, U32, C.POINTER(GhModelConfig)]),
+    "gh_gguf_check_model": (I32, [P, C.POINTER(GhModelConfig)]),
+    "gh_gguf_load_model": (I32, [P, C.POINTER(GhModelConfig), P]),
 }
 
 _lib = None

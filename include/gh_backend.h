@@ -262,6 +262,48 @@ int gh_model_read_x(gh_model* m, float* dst);
  * time a single projection on the model's own resident weights */
 int gh_model_weight(gh_model* m, uint32_t layer, uint32_t tensor, gh_buf* out);
 
+/* ---- GGUF model files (host only; no device needed until gh_gguf_load_model) ----
+ * The file is mapped read-only and parsed with bounds-checked reads; every tensor span is
+ * validated against the file and the other spans at open (gguf/loader/mod.rs:44-186). On a
+ * failure the status is negative and gh_gguf_last_error() (thread-local) holds the message. */
+typedef struct gh_gguf gh_gguf;
+typedef struct gh_gguf_tensor_info {
+    const char* name;     /* valid until gh_gguf_close */
+    uint32_t n_dims;      /* <= 4 */
+    uint32_t type;        /* ggml type id (tensor_index.rs:36-54) */
+    uint64_t dims[4];     /* GGUF order: dims[0] = in (row length), dims[1] = out */
+    uint64_t offset;      /* relative to the data section */
+    uint64_t nbytes;      /* from the ggml block layout (TensorInfo::byte_len) */
+    const void* data;     /* the tensor bytes inside the mapping */
+} gh_gguf_tensor_info;
+
+const char* gh_gguf_last_error(void);
+/* GgufFile::open, gguf/loader/mod.rs:44-123 */
+int gh_gguf_open(const char* path, gh_gguf** out);
+void gh_gguf_close(gh_gguf* g);
+int gh_gguf_info(const gh_gguf* g, uint32_t* version, uint64_t* tensor_count, uint64_t* kv_count,
+                 uint64_t* data_offset);
+/* GgufFile::tensors / tensor_bytes, loader/mod.rs:133-143 */
+int gh_gguf_tensor(const gh_gguf* g, uint64_t index, gh_gguf_tensor_info* out);
+/* TensorIndex::get, tensor_index.rs:162-170 (duplicate names: the last one) */
+int gh_gguf_find(const gh_gguf* g, const char* name, uint64_t* index);
+/* metadata accessors (GgufValue::as_u64 / as_f32 / as_str, loader/value.rs:24-60) */
+int gh_gguf_meta_u64(const gh_gguf* g, const char* key, uint64_t* out);
+int gh_gguf_meta_f64(const gh_gguf* g, const char* key, double* out);
+const char* gh_gguf_meta_str(const gh_gguf* g, const char* key);
+int gh_gguf_meta_array_len(const gh_gguf* g, const char* key, uint64_t* out);
+/* MistralConfig::from_metadata (family/mistral/config.rs:43-125) into a model config, with the
+ * request's KV capacity (1..context_length) and prefill chunk rows */
+int gh_gguf_model_config(const gh_gguf* g, uint32_t kv_context, uint32_t prefill_rows,
+                         gh_model_config* cfg);
+/* MistralTensors::build (family/mistral/tensors.rs:40-102): every tensor present with its
+ * shape and an admitted type (F32 norms, Q4_K/Q6_K matrices) */
+int gh_gguf_check_model(const gh_gguf* g, const gh_model_config* cfg);
+/* load_weights (cpu/weights.rs:63-135): checks first, then uploads every tensor through
+ * gh_model_load_tensor in the canonical order; a missing output.weight is the tied case
+ * (the token table is uploaded as the output matrix as well) */
+int gh_gguf_load_model(const gh_gguf* g, const gh_model_config* cfg, gh_model* m);
+
 #ifdef __cplusplus
 }
 #endif
