@@ -802,18 +802,34 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         const char* e = std::getenv("GH_GEMM_SPLITS");
         return e ? (uint32_t)std::atoi(e) : 0u;
     }();
-    // default: 256-token tiles for long batches; rows per tile so the tile count fills the CUs
+    // default (measured at 512 tokens on the 8B and 14B shapes): 256 x 128 tiles where their
+    // count alone fills the CUs or the matrix is deep or wide, 256 x 96 for a wide output that
+    // 256 x 128 would leave short of the CUs, 128 x 128 (4 splits) for d x d at d = 4096 and for
+    // the narrow K/V projections; shorter batches take 128-token tiles
     GemmTile tile;
+    uint32_t pref_splits = 0;
+    const uint32_t t4_tiles = ceil_div(rows, 128u) * ceil_div(n, 256u);
     if (forced_tile >= 0 && forced_tile < 5) {
         tile = kGemmTiles[forced_tile];
     } else if (n >= 256) {
-        tile = rows >= 8192 ? kGemmTiles[3] : kGemmTiles[2];
+        if (in_dim >= 8192 || (rows >= 5120 && (rows < 8192 || t4_tiles >= b->cus))) {
+            tile = kGemmTiles[4];
+        } else if (rows >= 8192) {
+            tile = kGemmTiles[3];
+        } else if (rows >= 4096) {
+            tile = kGemmTiles[1];
+            pref_splits = 4;
+        } else {
+            tile = kGemmTiles[1];
+        }
     } else {
         tile = rows >= 4096 ? kGemmTiles[1] : kGemmTiles[0];
     }
     const GhKernel k = (GhKernel)((w->format == GH_FMT_Q4_K ? K_GEMM_Q4K_T128_R64 : K_GEMM_Q6K_T128_R64) + tile.index);
     const uint32_t tr = ceil_div(rows, tile.rows), tt = ceil_div(n, tile.tokens), tiles = tr * tt;
-    uint32_t splits = forced_splits ? forced_splits : std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles);
+    uint32_t splits = forced_splits ? forced_splits
+                      : pref_splits ? pref_splits
+                                    : std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles);
     splits = std::max<uint32_t>(1, std::min<uint32_t>({splits, std::max<uint32_t>(1, units / 8), 16u}));
     GhGemmArgs ga{a->addr, w->addr, out, 0, in_dim, rows, n, splits};
     if (splits > 1) {

@@ -65,34 +65,47 @@ __device__ __forceinline__ void pair16(const uint4& a, const uint4& b, uint4& p0
 }
 
 // x8(e) returns FP16 x[e .. e+8) as a uint4 (e a multiple of 8). The pairs and sums of unit u.
+// The 8 uint4 of FP16 x that unit u pairs, in pairing order (Q4_K: x[256b + 64g .. +64);
+// Q6_K: quarter q's 16 values at 256b + 128s + 32q + 16h, as two uint4 each).
 template <uint32_t FMT, class X8>
-__device__ __forceinline__ void pair_unit(const X8& x8, uint32_t u, uint4 (&xv)[8], float4& sum) {
+__device__ __forceinline__ void load_unit_x(const X8& x8, uint32_t u, uint4 (&v)[8]) {
     if constexpr (FMT == kQ4K) {
         const uint32_t e0 = (u >> 2) * 256 + (u & 3u) * 64;
-        uint4 v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = x8(e0 + 8 * i);
-        float s[4];
+    } else {
+        const uint32_t b = u >> 2, sg = (u >> 1) & 1u, h = u & 1u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t e = b * 256 + sg * 128 + q * 32 + h * 16;
+            v[2 * q] = x8(e);
+            v[2 * q + 1] = x8(e + 8);
+        }
+    }
+}
+
+template <uint32_t FMT>
+__device__ __forceinline__ void pair_raw(const uint4 (&v)[8], uint4 (&xv)[8], float4& sum) {
+    float s[4];
+    if constexpr (FMT == kQ4K) {
         pair16(v[0], v[1], xv[0], xv[2], s[0]);
         pair16(v[2], v[3], xv[1], xv[3], s[1]);
         pair16(v[4], v[5], xv[4], xv[6], s[2]);
         pair16(v[6], v[7], xv[5], xv[7], s[3]);
         sum = make_float4(s[0] + s[1], s[2] + s[3], 0.0f, 0.0f);
     } else {
-        const uint32_t b = u >> 2, sg = (u >> 1) & 1u, h = u & 1u;
-        float s[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t e = b * 256 + sg * 128 + q * 32 + h * 16;
-            pair16(x8(e), x8(e + 8), xv[q], xv[4 + q], s[q]);
-        }
+        for (int q = 0; q < 4; ++q) pair16(v[2 * q], v[2 * q + 1], xv[q], xv[4 + q], s[q]);
         sum = make_float4(s[0], s[1], s[2], s[3]);
     }
 }
 
-// LDS staging, one (unit, quarter) per thread: unit u's 8 uint4 of pairs at xs[k * units + u]
-// (conflict-free b128 reads), its four quarter sums at sums[u] (Q4_K: quarters of its two
-// 32-weight halves, added pairwise by the reader in the order pair_unit adds them).
+template <uint32_t FMT, class X8>
+__device__ __forceinline__ void pair_unit(const X8& x8, uint32_t u, uint4 (&xv)[8], float4& sum) {
+    uint4 v[8];
+    load_unit_x<FMT>(x8, u, v);
+    pair_raw<FMT>(v, xv, sum);
+}
 template <uint32_t FMT, class X8>
 __device__ __forceinline__ void stage_x(const X8& x8, uint32_t units, uint4* xs, float4* sums) {
     for (uint32_t item = threadIdx.x; item < units * 4; item += blockDim.x) {
@@ -255,10 +268,48 @@ __device__ __forceinline__ uint32_t position(const GhGemvArgs& a) {
     return (a.pos_ptr ? *gh_gp<uint32_t>(a.pos_ptr) : 0u) + a.base;
 }
 
+__device__ __forceinline__ bool epi_needs_pos(uint32_t epi) {
+    return epi == GH_EPI_ROPE || epi == GH_EPI_ROPE_CACHE || epi == GH_EPI_CACHE;
+}
+
+// Epilogue inputs that do not depend on the task's dot products — the residual rows, the RoPE
+// (cos, sin) of the position and the query post-scale — requested together with the task's
+// weights, so their latency overlaps the weight stream instead of following the reduction.
+template <int R>
+struct EpiIn {
+    float res[R];
+    float2 cs[R / 2 > 0 ? R / 2 : 1];
+    float k;
+};
+
+// Branch-free (loads inside branches cost exact wait counts): every value is requested; an
+// epilogue that does not use one reads it from x instead, which is always valid memory.
+template <int R, bool SW>
+__device__ __forceinline__ void epi_load(const GhGemvArgs& a, const GhGemvSeg& sg, uint32_t t,
+                                         uint32_t row0, uint32_t pos, EpiIn<R>& e) {
+    if constexpr (SW) return;
+    const bool resid = sg.epi == GH_EPI_RESID;
+    const bool rope = (sg.epi == GH_EPI_ROPE || sg.epi == GH_EPI_ROPE_CACHE) && a.table;
+    const bool post = sg.epi == GH_EPI_ROPE && a.post;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint64_t at = sg.out + ((uint64_t)t * sg.rows + min(row0 + r, sg.rows - 1)) * 4;
+        e.res[r] = *gh_gp<float>(resid ? at : a.x);
+    }
+#pragma unroll
+    for (int r = 0; r + 1 < R; r += 2) {
+        const uint32_t pair = min(((row0 + r) % a.head_dim) >> 1, a.pairs - 1);
+        const uint64_t at = a.table + ((uint64_t)pos * a.pairs + pair) * 8;
+        e.cs[r / 2] = *gh_gp<float2>(rope ? at : a.x);
+    }
+    const float k = *gh_gp<float>(post ? a.post + (uint64_t)pos * 4 : a.x);
+    e.k = post ? k : 1.0f;
+}
+
 // f16(acc) rotated pairwise: (y0, y1) -> ((y0 c - y1 s) k, (y0 s + y1 c) k), the reference's
 // rope_yarn on the FP16 matmul output (cpu/kernels/elementwise/rope.rs:14-39).
 __device__ __forceinline__ void rope_pair(const GhGemvArgs& a, uint32_t row, float acc0,
-                                          float acc1, bool post, uint32_t pos, uint16_t& o0,
+                                          float acc1, float2 cs, float k, uint16_t& o0,
                                           uint16_t& o1) {
 #pragma clang fp contract(off)
     const uint16_t h0 = gh_f2h(acc0), h1 = gh_f2h(acc1);
@@ -268,8 +319,6 @@ __device__ __forceinline__ void rope_pair(const GhGemvArgs& a, uint32_t row, flo
         o1 = h1;
         return;
     }
-    const float2 cs = gh_gp<float2>(a.table)[(size_t)pos * a.pairs + pair];
-    const float k = post ? gh_gp<float>(a.post)[pos] : 1.0f;
     const float x0 = gh_h2f(h0), x1 = gh_h2f(h1);
     o0 = gh_f2h((x0 * cs.x - x1 * cs.y) * k);
     o1 = gh_f2h((x0 * cs.y + x1 * cs.x) * k);
@@ -277,7 +326,8 @@ __device__ __forceinline__ void rope_pair(const GhGemvArgs& a, uint32_t row, flo
 
 template <int R, bool SW>
 __device__ __forceinline__ void epilogue(const GhGemvArgs& a, const GhGemvSeg& sg, uint32_t t,
-                                         uint32_t row0, const float (&v)[R], const float* up) {
+                                         uint32_t row0, const float (&v)[R], const float* up,
+                                         uint32_t pos, const EpiIn<R>& e) {
 #pragma clang fp contract(off)
     if constexpr (SW) {
 #pragma unroll
@@ -304,13 +354,11 @@ __device__ __forceinline__ void epilogue(const GhGemvArgs& a, const GhGemvSeg& s
         case GH_EPI_RESID:
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (row0 + r < sg.rows) {
-                    GH_GLOBAL float* xr = gh_gpw<float>(sg.out) + row0 + r;
-                    *xr = *xr + gh_h2f(gh_f2h(v[r]));
-                }
+                if (row0 + r < sg.rows)
+                    gh_gpw<float>(sg.out)[(size_t)t * sg.rows + row0 + r] = e.res[r] + gh_h2f(gh_f2h(v[r]));
             break;
         case GH_EPI_CACHE: {
-            const size_t off = (size_t)position(a) * sg.rows;
+            const size_t off = (size_t)pos * sg.rows;
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if (row0 + r < sg.rows) gh_gpw<uint16_t>(sg.out)[off + row0 + r] = gh_f2h(v[r]);
@@ -318,14 +366,13 @@ __device__ __forceinline__ void epilogue(const GhGemvArgs& a, const GhGemvSeg& s
         }
         case GH_EPI_ROPE:
         case GH_EPI_ROPE_CACHE: {
-            const uint32_t pos = position(a);
             const bool q = sg.epi == GH_EPI_ROPE;
             const size_t off = q ? 0 : (size_t)pos * sg.rows;
 #pragma unroll
             for (int r = 0; r + 1 < R; r += 2) {
                 if (row0 + r + 1 < sg.rows) {
                     uint16_t o0, o1;
-                    rope_pair(a, row0 + r, v[r], v[r + 1], q, pos, o0, o1);
+                    rope_pair(a, row0 + r, v[r], v[r + 1], e.cs[r / 2], e.k, o0, o1);
                     GH_GLOBAL uint16_t* dst = gh_gpw<uint16_t>(sg.out) + off + row0 + r;
                     dst[0] = o0;
                     dst[1] = o1;
@@ -356,19 +403,26 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
                                             WRow<FMT> (&wa)[M][R]) {
     const uint32_t lane = threadIdx.x & 63u, units = nb * 4;
     const uint32_t nch = (units + 63) / 64;
+    first = __builtin_amdgcn_readfirstlane(first);  // wave-uniform: per-task values go to SGPRs
     const uint8_t* w[M];
     w[0] = (const uint8_t*)sg.w;
     if constexpr (M == 2) w[1] = (const uint8_t*)a.aux;
+    const uint32_t pos = epi_needs_pos(sg.epi) ? position(a) : 0u;
     for (uint32_t k = first; k < ntask; k += stride) {
         float acc[M][R];
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+        EpiIn<R> ei;
         for (uint32_t c = 0; c < nch; ++c) {
             const uint32_t u = c * 64 + lane, uc = min(u, units - 1);
             if (!primed) load_step<FMT, R, M>(w, sg.rows, nb, k * R, uc, wa);
             primed = false;
+            if (c == 0) {
+                __builtin_amdgcn_sched_barrier(0);  // the weights go out before anything waits
+                epi_load<R, M == 2>(a, sg, t, k * R, pos, ei);
+            }
             if (u < units) compute_step<FMT, R, M>(xs, sums, units, u, mk, wa, acc);
         }
         float v[M][R];
@@ -376,7 +430,7 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
         for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int r = 0; r < R; ++r) v[m][r] = gh_wave_sum63(acc[m][r]);
-        if (lane == 63u) epilogue<R, M == 2>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr);
+        if (lane == 63u) epilogue<R, M == 2>(a, sg, t, k * R, v[0], M == 2 ? v[M - 1] : nullptr, pos, ei);
     }
 }
 
@@ -396,7 +450,7 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
     uint4* xs6 = lds + 9 * units;
     float4* xsum6 = (float4*)(lds + 17 * units);
     const uint32_t waves = gridDim.x * (blockDim.x >> 6);
-    const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t gw = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
     // segment of this wave and its position among the segment's waves
     uint32_t si = 0, w0 = 0, nw = waves;
     if (a.nseg > 1) {
@@ -510,15 +564,27 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
     if (gw >= a.tasks) return;  // wave-uniform; this kernel has no barrier
     const uint32_t u = min(lane, units - 1);
     const uint8_t* w[1] = {(const uint8_t*)sg.w};
+    // x first, then the weights: the pairing below waits only for the x loads (in-order
+    // counters) while the weight stream is in flight
+    const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x);
+    uint4 xraw[8];
+    load_unit_x<FMT>([&](uint32_t e) { return xh[e >> 3]; }, u, xraw);
+    __builtin_amdgcn_sched_barrier(0);
     WRow<FMT> wr[1][R];
     load_step<FMT, R, 1>(w, sg.rows, nb, gw * R, u, wr);
-    const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t pos = epi_needs_pos(sg.epi) ? position(a) : 0u;
+    EpiIn<R> ei;
+    epi_load<R, false>(a, sg, 0, gw * R, pos, ei);
     uint4 xv[8];
     float4 xsum;
-    pair_unit<FMT>([&](uint32_t e) { return xh[e >> 3]; }, u, xv, xsum);
+    pair_raw<FMT>(xraw, xv, xsum);
     const Masks mk = make_masks();
     for (uint32_t k = gw; k < a.tasks; k += waves) {
-        if (k != gw) load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
+        if (k != gw) {
+            load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
+            epi_load<R, false>(a, sg, 0, k * R, pos, ei);
+        }
         float acc[1][R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[0][r] = 0.0f;
@@ -526,7 +592,7 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
         float v[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) v[r] = gh_wave_sum63(acc[0][r]);
-        if (lane == 63u) epilogue<R, false>(a, sg, 0, k * R, v, nullptr);
+        if (lane == 63u) epilogue<R, false>(a, sg, 0, k * R, v, nullptr, pos, ei);
     }
 }
 
@@ -545,15 +611,26 @@ __device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a) {
     const uint32_t u = min(uw, units - 1);
     const GhGemvSeg sg = a.seg[0];
     const uint8_t* w[1] = {(const uint8_t*)sg.w};
-    WRow<FMT> wr[1][R];
-    if (blockIdx.x < a.tasks) load_step<FMT, R, 1>(w, sg.rows, nb, blockIdx.x * R, u, wr);
     const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x);
+    uint4 xraw[8];
+    load_unit_x<FMT>([&](uint32_t e) { return xh[e >> 3]; }, u, xraw);
+    __builtin_amdgcn_sched_barrier(0);
+    WRow<FMT> wr[1][R];
+    // unconditional (clamped task): loads outside branches keep the wait counts exact
+    load_step<FMT, R, 1>(w, sg.rows, nb, min(blockIdx.x, a.tasks - 1) * R, u, wr);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t pos = epi_needs_pos(sg.epi) ? position(a) : 0u;
+    EpiIn<R> ei;
+    if (blockIdx.x < a.tasks) epi_load<R, false>(a, sg, 0, blockIdx.x * R, pos, ei);
     uint4 xv[8];
     float4 xsum;
-    pair_unit<FMT>([&](uint32_t e) { return xh[e >> 3]; }, u, xv, xsum);
+    pair_raw<FMT>(xraw, xv, xsum);
     const Masks mk = make_masks();
     for (uint32_t k = blockIdx.x; k < a.tasks; k += gridDim.x) {
-        if (k != blockIdx.x) load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
+        if (k != blockIdx.x) {
+            load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
+            epi_load<R, false>(a, sg, 0, k * R, pos, ei);
+        }
         float acc[1][R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[0][r] = 0.0f;
@@ -568,7 +645,7 @@ __device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a) {
             float v[R];
 #pragma unroll
             for (int r = 0; r < R; ++r) v[r] = ((part[0][r] + part[1][r]) + part[2][r]) + part[3][r];
-            epilogue<R, false>(a, sg, 0, k * R, v, nullptr);
+            epilogue<R, false>(a, sg, 0, k * R, v, nullptr, pos, ei);
         }
         __syncthreads();
     }
