@@ -51,6 +51,8 @@ const KernelName kKernels[] = {
     {K_GEMM_Q6K_T256_R96, "gh_gemm_q6k_t256_r96"},   {K_GEMM_Q6K_T256_R128, "gh_gemm_q6k_t256_r128"},
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
     {K_ATTN_PREFILL_G4_Q16, "gh_attn_prefill_g4_q16"},
+    {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
+    {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -782,15 +784,41 @@ int gh_embed(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* w, u
     return latch(enc, op_embed(b, x, w, token, embd, nullptr));
 }
 
-// Matrix-core GEMM for n >= kGemmMinTokens. Tile variants (tokens x rows per workgroup):
-// 128 x 64, 128 x 128, 256 x 64, 256 x 96, 256 x 128; split-K over the units when the tiles
-// alone would leave resident workgroup slots idle.
+// Matrix-core GEMM for n >= kGemmMinTokens. Batches of 256 tokens or more take the
+// warp-specialized kernels (256 tokens x 128 or 96 rows per 512-thread workgroup); shorter
+// batches take the 256-thread tiles (tokens x rows: 128 x 64, 128 x 128, 256 x 64, 256 x 96,
+// 256 x 128). Either splits K over the units when the tiles alone would leave CUs idle.
 constexpr uint32_t kGemmMinTokens = 8;
 
 struct GemmTile {
     uint32_t tokens, rows, index;
 };
 constexpr GemmTile kGemmTiles[5] = {{128, 64, 0}, {128, 128, 1}, {256, 64, 2}, {256, 96, 3}, {256, 128, 4}};
+
+// One GEMM launch over tr x tt tiles and `splits` K ranges; with splits > 1 the kernel writes
+// FP32 partials to the workspace and gh_gemm_reduce sums them in split order.
+static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, uint32_t tt,
+                       uint32_t splits, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n) {
+    // the kernels give split z the units [z per, min(units, (z + 1) per)), per = ceil(units /
+    // splits): shrink splits to ceil(units / per) until every split is non-empty
+    const uint32_t units = w->cols / 64;
+    for (;;) {
+        const uint32_t per = ceil_div(units, splits), s = ceil_div(units, per);
+        if (s == splits) break;
+        splits = s;
+    }
+    GhGemmArgs ga{a->addr, w->addr, out, 0, w->cols, w->rows, n, splits};
+    if (splits > 1) {
+        int rc = ensure_workspace(b, (size_t)splits * n * w->rows * 4);
+        if (rc) return rc;
+        ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
+    }
+    int rc = launch(b, k, tr, tt, splits, block, &ga);
+    if (rc || splits == 1) return rc;
+    const uint64_t total = (uint64_t)n * w->rows;
+    return launch(b, K_GEMM_REDUCE, (uint32_t)std::min<uint64_t>(ceil_div(total, (uint64_t)256), 4096), 1, 1,
+                  256, &ga);
+}
 
 int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n) {
     const uint32_t in_dim = w->cols, rows = w->rows, units = in_dim / 64;
@@ -802,46 +830,42 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         const char* e = std::getenv("GH_GEMM_SPLITS");
         return e ? (uint32_t)std::atoi(e) : 0u;
     }();
-    // default (measured at 512 tokens on the 8B and 14B shapes): 256 x 128 tiles where their
-    // count alone fills the CUs or the matrix is deep or wide, 256 x 96 for a wide output that
-    // 256 x 128 would leave short of the CUs, 128 x 128 (4 splits) for d x d at d = 4096 and for
-    // the narrow K/V projections; shorter batches take 128-token tiles
+    // splits: at most 16 and at least 8 units of 64 k per split
+    auto clamp_splits = [&](uint32_t s) {
+        return std::max<uint32_t>(1, std::min<uint32_t>({forced_splits ? forced_splits : s,
+                                                         std::max<uint32_t>(1, units / 8), 16u}));
+    };
+    const bool q4 = w->format == GH_FMT_Q4_K;
+    if (n >= 256 && forced_tile < 0) {
+        // Row height (measured at 512 tokens on the 8B and 14B shapes): one workgroup per CU,
+        // s = CUs / tiles splits, and the height whose tiles x splits fill the CUs' last wave
+        // better — 96 rows for 12288 x 4096 (256 tiles against 192 of 128 rows), 128 rows
+        // otherwise. Narrow outputs (<= 1024 rows) take 96 rows with two workgroups per CU
+        // and up to 16 splits: their few units per split leave latency for a second to hide.
+        const uint32_t tt = ceil_div(n, 256u), cus = b->cus;
+        auto fill = [&](uint32_t br) {
+            const uint32_t t = ceil_div(rows, br) * tt, s = std::max<uint32_t>(1, cus / t);
+            const uint64_t ts = (uint64_t)t * s;
+            return (double)ts / ((double)cus * (double)ceil_div(ts, cus));
+        };
+        const bool narrow = rows <= 1024;
+        const uint32_t br = narrow || fill(96) > fill(128) ? 96u : 128u;
+        const GhKernel k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96 : K_GEMM3_Q6K_R96)
+                                    : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
+        const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
+        const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
+        return gemm_launch(b, k, 512, tr, tt, clamp_splits(std::max<uint32_t>(1, slots / tiles)), out, a, w, n);
+    }
     GemmTile tile;
-    uint32_t pref_splits = 0;
-    const uint32_t t4_tiles = ceil_div(rows, 128u) * ceil_div(n, 256u);
     if (forced_tile >= 0 && forced_tile < 5) {
         tile = kGemmTiles[forced_tile];
-    } else if (n >= 256) {
-        if (in_dim >= 8192 || (rows >= 5120 && (rows < 8192 || t4_tiles >= b->cus))) {
-            tile = kGemmTiles[4];
-        } else if (rows >= 8192) {
-            tile = kGemmTiles[3];
-        } else if (rows >= 4096) {
-            tile = kGemmTiles[1];
-            pref_splits = 4;
-        } else {
-            tile = kGemmTiles[1];
-        }
     } else {
         tile = rows >= 4096 ? kGemmTiles[1] : kGemmTiles[0];
     }
-    const GhKernel k = (GhKernel)((w->format == GH_FMT_Q4_K ? K_GEMM_Q4K_T128_R64 : K_GEMM_Q6K_T128_R64) + tile.index);
+    const GhKernel k = (GhKernel)((q4 ? K_GEMM_Q4K_T128_R64 : K_GEMM_Q6K_T128_R64) + tile.index);
     const uint32_t tr = ceil_div(rows, tile.rows), tt = ceil_div(n, tile.tokens), tiles = tr * tt;
-    uint32_t splits = forced_splits ? forced_splits
-                      : pref_splits ? pref_splits
-                                    : std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles);
-    splits = std::max<uint32_t>(1, std::min<uint32_t>({splits, std::max<uint32_t>(1, units / 8), 16u}));
-    GhGemmArgs ga{a->addr, w->addr, out, 0, in_dim, rows, n, splits};
-    if (splits > 1) {
-        int rc = ensure_workspace(b, (size_t)splits * n * rows * 4);
-        if (rc) return rc;
-        ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
-    }
-    int rc = launch(b, k, tr, tt, splits, 256, &ga);
-    if (rc || splits == 1) return rc;
-    const uint64_t total = (uint64_t)n * rows;
-    return launch(b, K_GEMM_REDUCE, (uint32_t)std::min<uint64_t>(ceil_div(total, (uint64_t)256), 4096), 1, 1,
-                  256, &ga);
+    return gemm_launch(b, k, 256, tr, tt, clamp_splits(std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles)),
+                       out, a, w, n);
 }
 
 static int gemv_launch(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w,

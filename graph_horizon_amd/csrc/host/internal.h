@@ -70,6 +70,10 @@ enum GhKernel : int {
     K_GEMM_REDUCE,
     K_ATTN_PREFILL_G4,
     K_ATTN_PREFILL_G4_Q16,
+    K_GEMM3_Q4K_R128,
+    K_GEMM3_Q6K_R128,
+    K_GEMM3_Q4K_R96,
+    K_GEMM3_Q6K_R96,
     K_COUNT
 };
 

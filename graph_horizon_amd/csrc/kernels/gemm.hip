@@ -28,6 +28,7 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));  // a first-class vector (no struct copies)
 
 constexpr uint32_t kQ4K = 12, kQ6K = 14;
 constexpr int BK = 64;        // k per stage: one 64-weight unit
@@ -56,8 +57,9 @@ struct WStage {
 // Thread tid < 2·BR loads part tid / BR of weight row r0 + tid % BR for unit u (consecutive
 // lanes on consecutive rows: their 16-byte LDS stores, one row pitch apart, hit distinct banks).
 template <uint32_t FMT, int BR>
-__device__ __forceinline__ void load_w(const GhGemmArgs& a, uint32_t r0, uint32_t u, WStage& ws) {
-    const uint32_t tid = threadIdx.x, nb = a.in_dim >> 8;
+__device__ __forceinline__ void load_w(const GhGemmArgs& a, uint32_t r0, uint32_t u, WStage& ws,
+                                       uint32_t tid = threadIdx.x) {
+    const uint32_t nb = a.in_dim >> 8;
     const uint32_t row = min(r0 + tid % BR, a.rows - 1), part = tid / BR;
     const uint64_t blk = (uint64_t)row * nb + (u >> 2);
     if constexpr (FMT == kQ4K) {
@@ -74,9 +76,9 @@ __device__ __forceinline__ void load_w(const GhGemmArgs& a, uint32_t r0, uint32_
 
 // Dequantize the thread's 32 weights into its LDS row.
 template <uint32_t FMT, int BR>
-__device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* wb) {
+__device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* wb,
+                                        uint32_t tid = threadIdx.x) {
 #pragma clang fp contract(off)
-    const uint32_t tid = threadIdx.x;
     const uint32_t row = tid % BR, part = tid / BR;
     _Float16* dst = wb + row * LDK;
     const uint32_t qw[4] = {ws.q.x, ws.q.y, ws.q.z, ws.q.w};
@@ -222,6 +224,132 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
         }
 }
 
+// Warp-specialized variant for long batches: a 512-thread workgroup owns 256 tokens x BR rows.
+// Waves 0-3 (consumers) run the matrix cores exactly as gemm_body's waves do (64 tokens each,
+// A from registers one unit ahead, B from LDS). Waves 4-7 (producers) stream the weight bytes
+// kL units ahead of use — kL register sets, selected statically by unrolling the loop kL-fold —
+// and dequantize each unit into a kS-stage LDS ring, kS - 1 units ahead of the consumers. One
+// barrier per unit: in the interval of unit u the consumers read stage (u - u0) % kS while the
+// producers fill unit u + kS - 1 into the stage read during unit u - 1.
+template <uint32_t FMT, int BR>
+__device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
+    constexpr int WT = 64, TI = WT / 32, TJ = BR / 32;
+    constexpr int kS = 3, kL = 4;
+    // one LDS block: kS weight stages, then each consumer wave's activation rows
+    __shared__ __attribute__((aligned(16))) _Float16 lds3[kS * BR * LDK + 4 * WT * LDK];
+    auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t r0 = blockIdx.x * BR;
+    const uint32_t units = a.in_dim / 64;
+    const uint32_t per = (units + gridDim.z - 1) / gridDim.z;
+    const uint32_t u0 = blockIdx.z * per, u1 = min(units, u0 + per);
+    if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
+    auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };
+
+    if (wave >= 4) {
+        // ---- producers ----
+        const uint32_t pt = threadIdx.x - 256;
+        const bool wload = pt < 2 * BR;
+        WStage raw[kL];
+#pragma unroll
+        for (int i = 0; i < kL; ++i) load_w<FMT, BR>(a, r0, uc(u0 + i), raw[i], pt);
+#pragma unroll
+        for (int j = 0; j < kS - 1; ++j) {
+            if (wload && u0 + j < u1) store_w<FMT, BR>(u0 + j, raw[j], wstage(j), pt);
+            load_w<FMT, BR>(a, r0, uc(u0 + j + kL), raw[j], pt);
+        }
+        __syncthreads();
+        const uint32_t n_units = u1 - u0;
+        auto produce = [&](uint32_t kk, WStage& rs) __attribute__((always_inline)) {
+            const uint32_t p = u0 + kk + kS - 1;  // the unit produced in this interval
+            if (wload && p < u1) store_w<FMT, BR>(p, rs, wstage((kk + kS - 1) % kS), pt);
+            load_w<FMT, BR>(a, r0, uc(p + kL), rs, pt);
+            __syncthreads();
+        };
+        uint32_t k = 0;
+        for (; k + kL <= n_units; k += kL) {  // no exits inside the unrolled body
+#pragma unroll
+            for (int i = 0; i < kL; ++i) produce(k + i, raw[(i + kS - 1) % kL]);
+        }
+#pragma unroll
+        for (int i = 0; i < kL - 1; ++i)
+            if (k + i < n_units) produce(k + i, raw[(i + kS - 1) % kL]);
+        return;
+    }
+
+    // ---- consumers ----
+    // Activations are fetched as whole lines (lane l: token row 8 i + l / 8 of the wave's 64,
+    // 16-byte chunk l % 8 of the unit's 128 bytes) one unit ahead, and staged through the wave's
+    // own LDS rows (no barrier: only this wave touches them), from which the A fragments are
+    // read — each 128-byte line is requested once instead of once per 16-k step.
+    const uint32_t t0 = blockIdx.y * (4 * WT) + wave * WT;
+    const uint32_t fm = lane & 31u, fg = lane >> 5;
+    const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
+    uint32_t xrow[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xrow[i] = min(t0 + 8 * i + (lane >> 3), a.n - 1) * a.in_dim;
+    auto load_rows = [&](uint32_t u, u4v (&r)[8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = *(const GH_GLOBAL u4v*)(x + xrow[i] + chunk_k<FMT>(u, lane & 7u));
+    };
+    _Float16* xw = lds3 + kS * BR * LDK + wave * (WT * LDK);
+    auto put_rows = [&](const u4v (&r)[8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *(u4v*)(xw + (8 * i + (lane >> 3)) * LDK + (lane & 7u) * 8) = r[i];
+    };
+    f16v acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f16v{};
+    u4v ra[8], rb[8];
+    load_rows(u0, ra);
+    __syncthreads();
+    auto step = [&](uint32_t u, const u4v (&rcur)[8], u4v (&rnext)[8]) __attribute__((always_inline)) {
+        load_rows(uc(u + 1), rnext);
+        __builtin_amdgcn_sched_barrier(0);  // the loads go out before anything waits
+        put_rows(rcur);
+        const _Float16* wb = wstage((u - u0) % kS);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            h8 af[TI], bf[TJ];
+#pragma unroll
+            for (int i = 0; i < TI; ++i) af[i] = *(const h8*)(xw + (32 * i + fm) * LDK + 16 * ks + 8 * fg);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    };
+    // the unrolled body has no exits (exact wait counts across the back edge); tail after
+    uint32_t u = u0;
+    for (; u + 2 <= u1; u += 2) {
+        step(u, ra, rb);
+        step(u + 1, rb, ra);
+    }
+    if (u < u1) step(u, ra, rb);
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t t = t0 + 32 * i + 8 * (r >> 2) + 4 * fg + (r & 3);
+            if (t >= a.n) continue;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const uint32_t row = r0 + 32 * j + fm;
+                if (row >= a.rows) continue;
+                if (gridDim.z == 1)
+                    gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] = gh_f2h(acc[i][j][r]);
+                else
+                    gh_gpw<float>(a.part)[((uint64_t)blockIdx.z * a.n + t) * a.rows + row] = acc[i][j][r];
+            }
+        }
+}
+
 }  // namespace
 
 // Tile variants: tokens per workgroup (4 waves x 32 or 64) x weight rows (64, 96, 128).
@@ -233,6 +361,11 @@ GH_GEMM(t128_r128, 32, 128)
 GH_GEMM(t256_r64, 64, 64)
 GH_GEMM(t256_r96, 64, 96)
 GH_GEMM(t256_r128, 64, 128)
+// warp-specialized 256-token tiles (512 threads)
+GH_KERNEL __launch_bounds__(512) void gh_gemm3_q4k_r128(GhGemmArgs a) { gemm3_body<kQ4K, 128>(a); }
+GH_KERNEL __launch_bounds__(512) void gh_gemm3_q6k_r128(GhGemmArgs a) { gemm3_body<kQ6K, 128>(a); }
+GH_KERNEL __launch_bounds__(512) void gh_gemm3_q4k_r96(GhGemmArgs a) { gemm3_body<kQ4K, 96>(a); }
+GH_KERNEL __launch_bounds__(512) void gh_gemm3_q6k_r96(GhGemmArgs a) { gemm3_body<kQ6K, 96>(a); }
 
 // Sum split-K partials in split order, round to FP16: out[i] = f16(Σ_s part[s][i]).
 GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce(GhGemmArgs a) {

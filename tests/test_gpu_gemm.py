@@ -77,6 +77,12 @@ def _reference_bar(got, want, what):
     (F.FMT_Q4_K, 200, 4096, 129),   # split-K
     (F.FMT_Q6_K, 130, 12288, 64),   # down-projection depth, 16 splits
     (F.FMT_Q6_K, 1024, 5120, 200),  # 14B-shaped V projection
+    # 256 tokens and more: the warp-specialized kernels
+    (F.FMT_Q4_K, 96, 256, 257),     # smallest: one row tile, a one-token second token tile
+    (F.FMT_Q4_K, 1000, 2048, 300),  # narrow output, 96-row tiles, split-K, ragged rows/tokens
+    (F.FMT_Q6_K, 2000, 3072, 256),  # one token tile, ragged rows
+    (F.FMT_Q6_K, 640, 8448, 700),   # 132 units: 16 splits shrunk to 15 (none empty)
+    (F.FMT_Q4_K, 4096, 4096, 384),  # 128-row tiles with split-K
 ])
 def test_gemm_parity(hip, fmt, rows, in_dim, n):
     w, a16, got = _run(hip, fmt, rows, in_dim, n, 7 + rows + n)
