@@ -7,4 +7,5 @@ native reader's binding and a writer), seeded synthetic GGUF tensors (`synth`) a
 build (`build`).
 """
 from . import _ffi  # noqa: F401
+from ._ffi import GhSampling  # noqa: F401
 from .backend import GhError, HipBackend, HipModel, Yarn  # noqa: F401

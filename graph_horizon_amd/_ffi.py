@@ -55,6 +55,14 @@ class GhKv(C.Structure):
                 ("value_dim", C.c_uint32)]
 
 
+class GhSampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_uint32),
+                ("min_p", C.c_float), ("repeat_penalty", C.c_float), ("seed", C.c_uint64)]
+
+
+SAMPLE_GREEDY, SAMPLE_TOPK, SAMPLE_FALLBACK = 0, 1, 2
+
+
 class GhModelConfig(C.Structure):
     _fields_ = [("block_count", C.c_uint32), ("context_length", C.c_uint32),
                 ("embedding_length", C.c_uint32), ("feed_forward_length", C.c_uint32),
@@ -123,6 +131,14 @@ SIGNATURES = {
     "gh_model_kv": (I32, [P, C.POINTER(GhKv)]),
     "gh_model_read_x": (I32, [P, P]),
     "gh_model_weight": (I32, [P, U32, U32, BUFP]),
+    "gh_model_read_topk": (I32, [P, U64, P, P, C.POINTER(U64)]),
+    "gh_model_generate": (I32, [P, P, U32, C.POINTER(GhSampling), U32, U32, P, C.POINTER(U32)]),
+    "gh_sampling_plan": (I32, [C.POINTER(GhSampling), C.POINTER(U32)]),
+    "gh_rng_seed": (U64, [U64]),
+    "gh_rng_next_f32": (C.c_float, [C.POINTER(U64)]),
+    "gh_sample": (I32, [P, U64, C.POINTER(GhSampling), P, U64, C.POINTER(U64), C.POINTER(U32)]),
+    "gh_sample_from_candidates": (I32, [P, P, U64, C.POINTER(GhSampling), C.POINTER(U64),
+                                        C.POINTER(U32)]),
     "gh_gguf_last_error": (C.c_char_p, []),
     "gh_gguf_open": (I32, [C.c_char_p, C.POINTER(P)]),
     "gh_gguf_close": (None, [P]),

@@ -13,7 +13,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _ffi as F
-from ._ffi import GhBuf, GhKv, GhModelConfig, GhYarn
+from ._ffi import GhBuf, GhKv, GhModelConfig, GhSampling, GhYarn
 
 
 class GhError(RuntimeError):
@@ -200,7 +200,7 @@ class HipBackend:
         cnt = C.c_uint64()
         self._ok(self.lib.gh_read_topk(self.h, C.byref(logits), vocab, k, _ptr(idx), _ptr(val),
                                        C.byref(cnt)), "read_topk")
-        return [(int(i), float(v)) for i, v in zip(idx[:cnt.value], val[:cnt.value])]
+        return [(int(i), v) for i, v in zip(idx[:cnt.value], val[:cnt.value])]  # np.float32: raw bits
 
     # ---- measurement ----
     def timer_start(self):
@@ -257,6 +257,24 @@ class HipModel:
         self.b._ok(self.b.lib.gh_model_decode_greedy(self.h, token, pos, steps, _ptr(out)),
                    "model_decode_greedy")
         return out[:steps]
+
+    def read_topk(self, k: int):
+        idx = np.zeros(max(k, 1), dtype=np.uint32)
+        val = np.zeros(max(k, 1), dtype=np.float32)
+        cnt = C.c_uint64()
+        self.b._ok(self.b.lib.gh_model_read_topk(self.h, k, _ptr(idx), _ptr(val), C.byref(cnt)),
+                   "model_read_topk")
+        return [(int(i), v) for i, v in zip(idx[:cnt.value], val[:cnt.value])]
+
+    def generate(self, prompt, sampling: "GhSampling", max_tokens: int, eos: int = 0xFFFFFFFF):
+        """generation::drive: prefill `prompt` at 0.., then up to max_tokens sampled tokens."""
+        t = np.ascontiguousarray(np.asarray(prompt, dtype=np.uint32))
+        out = np.zeros(max(max_tokens, 1), dtype=np.uint32)
+        n = C.c_uint32()
+        self.b._ok(self.b.lib.gh_model_generate(self.h, _ptr(t), len(t), C.byref(sampling),
+                                                max_tokens, eos, _ptr(out), C.byref(n)),
+                   "model_generate")
+        return out[:n.value]
 
     def kv(self) -> GhKv:
         kv = GhKv()

@@ -53,6 +53,7 @@ const KernelName kKernels[] = {
     {K_ATTN_PREFILL_G4_Q16, "gh_attn_prefill_g4_q16"},
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
+    {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -137,13 +138,6 @@ uint16_t f32_to_f16_rne(float f) {
     }
     const uint32_t q = (ax - 0x38000000u) >> 13, rem = ax & 0x1FFFu;
     return (uint16_t)(sign | (q + (rem > 0x1000u || (rem == 0x1000u && (q & 1)))));
-}
-
-int total_key(float f) {
-    int32_t b;
-    std::memcpy(&b, &f, 4);
-    b ^= (int32_t)(((uint32_t)(b >> 31)) >> 1);
-    return b;
 }
 
 }  // namespace
@@ -1010,14 +1004,57 @@ int gh_read_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, uint32_t
     return hip_check(b, hipMemcpy(out, (char*)b->ws + 2048, 4, hipMemcpyDeviceToHost), "hipMemcpy argmax");
 }
 
+// read_topk: k <= 128 on the device (gh_topk_partial over stripes of at most kTopkChunk
+// logits per step, at most 128 stripes, then gh_topk_final; 8 k bytes come back), larger k
+// on the host over the read-back logits. Both give exactly the reference's selection and
+// order (cpu/readback.rs:59-69): (logit desc by f32 total order, index asc).
+constexpr uint64_t kTopkDeviceMax = 128, kTopkChunk = 2048, kTopkStripes = 128;
+
 int gh_read_topk(gh_backend* b, const gh_buf* logits, uint64_t vocab, uint64_t k, uint32_t* idx,
                  float* val, uint64_t* count) {
     if (!b || !logits || !count) return GH_E_INVALID;
     if (vocab == 0) return fail(b, GH_E_INVALID, "read_topk on empty logits");
+    if (vocab > 0xFFFFFFFFull) return fail(b, GH_E_UNSUPPORTED, "read_topk: vocab beyond 32-bit indices");
+    if (!fits(logits, vocab * 4)) return fail(b, GH_E_RANGE, "read_topk: buffer smaller than vocab");
+    k = std::min<uint64_t>(k, vocab);
+    *count = 0;
+    if (k == 0) return GH_OK;
+    if (k <= kTopkDeviceMax) {
+        uint32_t width = 1;
+        while (width < k) width <<= 1;
+        // stripes of kTopkChunk logits, widened (in whole chunks) to keep at most 128 stripes
+        const uint64_t chunks = (vocab + kTopkChunk - 1) / kTopkChunk;
+        const uint64_t per = kTopkChunk * ((chunks + kTopkStripes - 1) / kTopkStripes);
+        GhTopkArgs a{};
+        a.logits = logits->addr;
+        a.n = (uint32_t)vocab;
+        a.per = (uint32_t)std::min<uint64_t>(per, 0xFFFFFFFFull);
+        a.stripes = (uint32_t)((vocab + per - 1) / per);
+        a.width = width;
+        a.k = (uint32_t)k;
+        const size_t part_bytes = (size_t)a.stripes * width * 8;
+        int rc = ensure_workspace(b, part_bytes + 8 * k);
+        if (rc) return rc;
+        char* ws = (char*)b->ws + kArgmaxBytes;
+        a.part = (uint64_t)ws;
+        a.out = (uint64_t)(ws + part_bytes);
+        rc = launch(b, K_TOPK_PARTIAL, a.stripes, 1, 1, 512, &a);
+        if (!rc) rc = launch(b, K_TOPK_FINAL, 1, 1, 1, 1024, &a);
+        if (!rc) rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+        std::vector<uint32_t> pairs(2 * k);
+        if (!rc) rc = hip_check(b, hipMemcpy(pairs.data(), ws + part_bytes, 8 * k, hipMemcpyDeviceToHost),
+                                "hipMemcpy topk");
+        if (rc) return rc;
+        for (uint64_t i = 0; i < k; ++i) {
+            if (idx) idx[i] = pairs[i];
+            if (val) std::memcpy(&val[i], &pairs[k + i], 4);
+        }
+        *count = k;
+        return GH_OK;
+    }
     std::vector<float> l(vocab);
     int rc = gh_read_logits(b, logits, vocab, l.data());
     if (rc) return rc;
-    k = std::min<uint64_t>(k, vocab);
     std::vector<uint32_t> cand(vocab);
     for (uint64_t i = 0; i < vocab; ++i) cand[i] = (uint32_t)i;
     auto order = [&](uint32_t x, uint32_t y) {

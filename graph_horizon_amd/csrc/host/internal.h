@@ -4,6 +4,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -74,6 +75,8 @@ enum GhKernel : int {
     K_GEMM3_Q6K_R128,
     K_GEMM3_Q4K_R96,
     K_GEMM3_Q6K_R96,
+    K_TOPK_PARTIAL,
+    K_TOPK_FINAL,
     K_COUNT
 };
 
@@ -112,6 +115,14 @@ struct gh_backend {
 };
 
 namespace gh {
+// f32::total_cmp as a signed key: the bit pattern as i32, low 31 bits flipped when negative
+inline int total_key(float f) {
+    int32_t b;
+    std::memcpy(&b, &f, 4);
+    b ^= (int32_t)(((uint32_t)(b >> 31)) >> 1);
+    return b;
+}
+
 int fail(gh_backend* b, int code, const std::string& msg);
 int hip_check(gh_backend* b, hipError_t e, const char* what);
 int launch(gh_backend* b, GhKernel k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,

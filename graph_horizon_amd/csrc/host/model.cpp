@@ -204,6 +204,61 @@ int record_step(gh_model* m, gh_encoder* enc) {
     return rc;
 }
 
+// Runs `steps` decode steps from (token, pos): the captured step graph replayed (captured on
+// first use, again after the backend's workspace or RoPE table moved), or with
+// GH_MODEL_NO_GRAPH the same kernels launched on the stream. Each step leaves its logits,
+// its argmax in history[pos] and the next (token, pos) in m->scalars.
+int run_steps(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps) {
+    gh_backend* b = m->b;
+    const uint32_t init[4] = {pos, token, 0, 0};
+    int rc = GH_OK;
+    if (m->cfg.flags & GH_MODEL_NO_GRAPH) {
+        rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
+        gh_encoder* enc = nullptr;
+        if (!rc) rc = gh_begin(b, &enc);
+        for (uint32_t i = 0; i < steps && !rc; ++i) rc = record_step(m, enc);
+        if (enc) {
+            int rs = gh_submit(b, enc);
+            rc = rc ? rc : rs;
+        }
+        m->last_rows = 1;
+        m->last_prefill = false;
+        return rc;
+    }
+    if (m->step && m->step_gen != b->gen) {
+        (void)hipGraphExecDestroy(m->step);
+        (void)hipGraphDestroy(m->step_graph);
+        m->step = nullptr;
+        m->step_graph = nullptr;
+    }
+    if (!m->step) {
+        gh_encoder* enc = nullptr;
+        rc = gh_begin(b, &enc);
+        if (rc) return rc;
+        rc = hip_check(b, hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        if (!rc) {
+            b->capturing = true;
+            int rec = record_step(m, enc);
+            b->capturing = false;
+            hipGraph_t g = nullptr;
+            int end = hip_check(b, hipStreamEndCapture(b->stream, &g), "hipStreamEndCapture");
+            rc = rec ? rec : end;
+            if (!rc) rc = hip_check(b, hipGraphInstantiate(&m->step, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+            if (rc && g) (void)hipGraphDestroy(g);
+            else m->step_graph = g;
+            m->step_gen = b->gen;
+        }
+        b->enc_open = false;
+        if (rc) return rc;
+    }
+    rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
+    for (uint32_t i = 0; i < steps && !rc; ++i)
+        rc = hip_check(b, hipGraphLaunch(m->step, b->stream), "hipGraphLaunch");
+    m->last_rows = 1;
+    m->last_prefill = false;
+    return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -377,56 +432,63 @@ int gh_model_decode_greedy(gh_model* m, uint32_t token, uint32_t pos, uint32_t s
     if ((uint64_t)pos + steps > m->kv.context || (uint64_t)pos + steps > c.context_length)
         return fail(m->b, GH_E_RANGE, "model: decode beyond context");
     if (steps == 0) return GH_OK;
-    gh_backend* b = m->b;
-    int rc = GH_OK;
-    const uint32_t init[4] = {pos, token, 0, 0};
-    if (c.flags & GH_MODEL_NO_GRAPH) {
-        rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
-        gh_encoder* enc = nullptr;
-        if (!rc) rc = gh_begin(b, &enc);
-        for (uint32_t i = 0; i < steps && !rc; ++i) rc = record_step(m, enc);
-        if (enc) {
-            int rs = gh_submit(b, enc);
-            rc = rc ? rc : rs;
-        }
-        if (!rc) rc = gh_download(b, &m->history, (uint64_t)pos * 4, tokens_out, (uint64_t)steps * 4);
-        m->last_rows = 1;
-        m->last_prefill = false;
-        return rc;
-    }
-    if (m->step && m->step_gen != b->gen) {  // workspace or rope table moved: capture again
-        (void)hipGraphExecDestroy(m->step);
-        (void)hipGraphDestroy(m->step_graph);
-        m->step = nullptr;
-        m->step_graph = nullptr;
-    }
-    if (!m->step) {
-        gh_encoder* enc = nullptr;
-        rc = gh_begin(b, &enc);
-        if (rc) return rc;
-        rc = hip_check(b, hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-        if (!rc) {
-            b->capturing = true;
-            int rec = record_step(m, enc);
-            b->capturing = false;
-            hipGraph_t g = nullptr;
-            int end = hip_check(b, hipStreamEndCapture(b->stream, &g), "hipStreamEndCapture");
-            rc = rec ? rec : end;
-            if (!rc) rc = hip_check(b, hipGraphInstantiate(&m->step, g, nullptr, nullptr, 0), "hipGraphInstantiate");
-            if (rc && g) (void)hipGraphDestroy(g);
-            else m->step_graph = g;
-            m->step_gen = b->gen;
-        }
-        b->enc_open = false;
-        if (rc) return rc;
-    }
-    rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
-    for (uint32_t i = 0; i < steps && !rc; ++i)
-        rc = hip_check(b, hipGraphLaunch(m->step, b->stream), "hipGraphLaunch");
-    if (!rc) rc = gh_download(b, &m->history, (uint64_t)pos * 4, tokens_out, (uint64_t)steps * 4);
-    m->last_rows = 1;
-    m->last_prefill = false;
+    int rc = run_steps(m, token, pos, steps);
+    if (!rc) rc = gh_download(m->b, &m->history, (uint64_t)pos * 4, tokens_out, (uint64_t)steps * 4);
     return rc;
+}
+
+int gh_model_read_topk(gh_model* m, uint64_t k, uint32_t* idx, float* val, uint64_t* count) {
+    if (!m) return GH_E_INVALID;
+    return gh_read_topk(m->b, &m->logits, m->cfg.vocab_size, k, idx, val, count);
+}
+
+int gh_model_generate(gh_model* m, const uint32_t* prompt, uint32_t n_prompt, const gh_sampling* p,
+                      uint32_t max_tokens, uint32_t eos, uint32_t* out, uint32_t* n_out) {
+    if (!m || !prompt || !p || !n_out || (max_tokens && !out)) return GH_E_INVALID;
+    *n_out = 0;
+    const gh_model_config& c = m->cfg;
+    const uint64_t context = std::min<uint64_t>(c.context_length, m->kv.context);
+    if (n_prompt == 0) return fail(m->b, GH_E_INVALID, "generate: empty prompt");
+    if (n_prompt > context) return fail(m->b, GH_E_RANGE, "generate: prompt beyond context");
+    int rc = gh_model_prefill(m, prompt, n_prompt, 0);
+    if (rc) return rc;
+    uint32_t k = 0;
+    const int path = gh_sampling_plan(p, &k);
+    uint64_t rng = gh_rng_seed(p->seed);
+    std::vector<uint32_t> recent(prompt, prompt + n_prompt);
+    std::vector<uint32_t> idx;
+    std::vector<float> val;
+    uint32_t produced = 0;
+    while (produced < max_tokens && n_prompt + produced < context) {
+        uint32_t token = 0;
+        if (path == GH_SAMPLE_GREEDY) {
+            rc = gh_model_read_argmax(m, &token);
+        } else if (path == GH_SAMPLE_TOPK) {
+            // the raw top-k (read_topk's order), scaled by 1/temperature, straight into the
+            // shared tail (generation/mod.rs:113-120)
+            idx.resize(k);
+            val.resize(k);
+            uint64_t cnt = 0;
+            rc = gh_model_read_topk(m, k, idx.data(), val.data(), &cnt);
+            const float inv = 1.0f / p->temperature;
+            for (uint64_t i = 0; i < cnt; ++i) val[i] *= inv;
+            if (!rc) rc = gh_sample_from_candidates(idx.data(), val.data(), cnt, p, &rng, &token);
+        } else {
+            val.resize(c.vocab_size);
+            rc = gh_model_read_logits(m, val.data());
+            if (!rc) rc = gh_sample(val.data(), c.vocab_size, p, recent.data(), recent.size(), &rng, &token);
+        }
+        if (rc) return rc;
+        if (token == eos) break;
+        out[produced++] = token;
+        *n_out = produced;
+        recent.push_back(token);
+        if (produced < max_tokens && n_prompt + produced < context) {
+            rc = run_steps(m, token, n_prompt + produced - 1, 1);
+            if (rc) return rc;
+        }
+    }
+    return GH_OK;
 }
 
 int gh_model_kv(gh_model* m, gh_kv* out) {

@@ -29,20 +29,31 @@ struct ChunkRegs {
     uint32_t v[16];   // V dims 2·lane, 2·lane+1 of positions 16·wave + i
 };
 
+// Positions are clamped to lim - 1: the row's last position (lim = len), or for the first
+// chunk, whose loads go out before the position is read, the cache's last slot (lim = context).
 template <int G>
 __device__ __forceinline__ void load_chunk(const uint16_t* kc, const uint16_t* vc, size_t kv_row,
-                                           uint32_t c, uint32_t len, ChunkRegs<G>& r) {
+                                           uint32_t c, uint32_t lim, ChunkRegs<G>& r) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t p0 = c * kChunk + wave * 16;
-    const uint32_t pk = min(p0 + (lane >> 2), len - 1);
+    const uint32_t pk = min(p0 + (lane >> 2), lim - 1);
     const GH_GLOBAL uint4* src = gh_gp<uint4>((uint64_t)(kc + (size_t)pk * kv_row + (lane & 3u) * 32));
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.k[i] = src[i];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const uint32_t pv = min(p0 + (uint32_t)i, len - 1);
+        const uint32_t pv = min(p0 + (uint32_t)i, lim - 1);
         r.v[i] = gh_gp<uint32_t>((uint64_t)(vc + (size_t)pv * kv_row))[lane];
     }
+}
+
+// Zero the V values of positions >= len (slots past the row may hold anything, and their
+// weight 0 times a NaN would not be 0); their scores are replaced by -inf in chunk_step.
+template <int G>
+__device__ __forceinline__ void mask_chunk(uint32_t c, uint32_t len, ChunkRegs<G>& r) {
+    const uint32_t p0 = c * kChunk + (threadIdx.x >> 6) * 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r.v[i] = p0 + (uint32_t)i < len ? r.v[i] : 0u;
 }
 
 template <int G>
@@ -109,15 +120,18 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) qv[h][i] = qp[i];
     }
+    const size_t kv_row = (size_t)a.kv_heads * 128;
+    const size_t cache0 = (size_t)a.layer * a.context * kv_row + (size_t)kvh * 128;
+    const uint16_t* kc = (const uint16_t*)a.kc + cache0;
+    const uint16_t* vc = (const uint16_t*)a.vc + cache0;
+    // this split's first chunk (chunk `split`) is requested before the position arrives
+    ChunkRegs<G> ra, rb;
+    load_chunk<G>(kc, vc, kv_row, split, a.context, ra);
     const uint32_t pos = (a.pos_ptr ? *gh_gp<uint32_t>(a.pos_ptr) : 0u) + a.base + row;
     const uint32_t len = pos + 1;
     const uint32_t nchunk = (len + kChunk - 1) / kChunk;
     const uint32_t nsplit = min(nchunk, a.splits);
     if (split >= nsplit) return;  // fixed grids (replayed graphs) may exceed the causal range
-    const size_t kv_row = (size_t)a.kv_heads * 128;
-    const size_t cache0 = (size_t)a.layer * a.context * kv_row + (size_t)kvh * 128;
-    const uint16_t* kc = (const uint16_t*)a.kc + cache0;
-    const uint16_t* vc = (const uint16_t*)a.vc + cache0;
 
     float m[G], l[G], acc[G][2];
 #pragma unroll
@@ -128,11 +142,10 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
     }
     // chunks split, split + nsplit, ...; a wave whose 16 positions of a chunk all lie past
     // the row's length still runs it (every weight is 0) so the loop stays wave-uniform
-    ChunkRegs<G> ra, rb;
-    load_chunk<G>(kc, vc, kv_row, split, len, ra);
     for (uint32_t c = split; c < nchunk; c += 2 * nsplit) {
         const uint32_t c1 = c + nsplit, c2 = c + 2 * nsplit;
         load_chunk<G>(kc, vc, kv_row, min(c1, nchunk - 1), len, rb);
+        if (c == split) mask_chunk<G>(c, len, ra);  // after the next chunk's loads are out
         if (c * kChunk + wave * 16 < len) chunk_step<G>(ra, qv, a.scale, c, len, m, l, acc);
         if (c1 >= nchunk) break;
         load_chunk<G>(kc, vc, kv_row, min(c2, nchunk - 1), len, ra);

@@ -165,6 +165,20 @@ struct GhAttnArgs {
     float scale;
 };
 
+// Device top-k (read_topk): gh_topk_partial keeps the `width` smallest keys of each stripe of
+// `per` logits (grid = stripes); gh_topk_final merges the stripes' lists and writes the first
+// k as (u32 index, f32 bits) pairs.
+struct GhTopkArgs {
+    uint64_t logits;   // f32 [n]
+    uint64_t part;     // u64 keys [stripes][width]
+    uint64_t out;      // u32 [2][k]: indices, then raw logit bits
+    uint32_t n;
+    uint32_t per;      // logits per stripe
+    uint32_t stripes;
+    uint32_t width;    // power of 2 >= k, <= 128
+    uint32_t k;
+};
+
 struct GhArgmaxArgs {
     uint64_t logits;   // f32 [n]
     uint64_t part_v;   // f32 [blocks]

@@ -146,3 +146,102 @@ GH_KERNEL void gh_step_advance(GhStepArgs a) {
     s[1] = r;
     s[0] = pos + 1;
 }
+
+// ---- top-k: read_topk (backend/contract.rs:303-318, cpu/readback.rs:59-69) on the device ----
+// The min(k, n) largest logits under (logit descending by f32 total order, i.e.
+// f32::total_cmp, then index ascending). Each logit becomes one 64-bit key that sorts
+// ascending in exactly that order:
+//   key = (~ord(bits) << 32) | index,   ord(b) = b ^ (b >> 31 ? 0xFFFFFFFF : 0x80000000),
+// ord mapping the total order of f32 bit patterns (-NaN < -inf < ... < -0 < +0 < ... < +inf <
+// +NaN) onto unsigned order. The all-ones key pads short stripes and sorts after every real
+// key. Both kernels sort with bitonic networks in LDS.
+constexpr uint32_t kTopkChunk = 2048;  // keys sorted per step of the partial pass
+constexpr uint32_t kTopkWidth = 128;   // largest list width (k <= 128 on the device path)
+constexpr uint32_t kTopkStripes = 128; // largest stripe count
+
+__device__ __forceinline__ uint64_t topk_key(uint32_t bits, uint32_t idx) {
+    const uint32_t ord = bits ^ ((bits >> 31) ? 0xFFFFFFFFu : 0x80000000u);
+    return ((uint64_t)~ord << 32) | idx;
+}
+
+// Ascending bitonic sort of s[0, n), n a power of 2, by the whole workgroup.
+__device__ void topk_sort(uint64_t* s, uint32_t n) {
+    for (uint32_t size = 2; size <= n; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (uint32_t t = threadIdx.x; t < n / 2; t += blockDim.x) {
+                const uint32_t i = 2 * t - (t & (stride - 1)), j = i + stride;
+                const uint64_t x = s[i], y = s[j];
+                if ((x > y) == ((i & size) == 0)) {
+                    s[i] = y;
+                    s[j] = x;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// `lists` independent sorted lists of width w at s + l * w: sorts each bitonic list ascending
+// (compare-exchanges at strides w/2 .. 1, all ascending).
+__device__ void topk_bitonic_merge(uint64_t* s, uint32_t lists, uint32_t w) {
+    for (uint32_t stride = w >> 1; stride > 0; stride >>= 1) {
+        __syncthreads();
+        for (uint32_t t = threadIdx.x; t < lists * (w / 2); t += blockDim.x) {
+            const uint32_t l = t / (w / 2), u = t % (w / 2);
+            const uint32_t i = l * w + 2 * u - (u & (stride - 1)), j = i + stride;
+            const uint64_t x = s[i], y = s[j];
+            if (x > y) {
+                s[i] = y;
+                s[j] = x;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+GH_KERNEL __launch_bounds__(512) void gh_topk_partial(GhTopkArgs a) {
+    __shared__ uint64_t s[kTopkChunk];
+    __shared__ uint64_t r[kTopkWidth];
+    const uint32_t w = a.width;
+    const uint64_t b0 = (uint64_t)blockIdx.x * a.per, e = min((uint64_t)a.n, b0 + a.per);
+    const uint32_t* bits = (const uint32_t*)a.logits;
+    for (uint32_t t = threadIdx.x; t < w; t += blockDim.x) r[t] = ~0ull;
+    for (uint64_t c = b0; c < e; c += kTopkChunk) {
+        __syncthreads();
+        for (uint32_t t = threadIdx.x; t < kTopkChunk; t += blockDim.x)
+            s[t] = c + t < e ? topk_key(bits[c + t], (uint32_t)(c + t)) : ~0ull;
+        topk_sort(s, kTopkChunk);
+        // the w smallest of (r, s[0, w)): r[i] = min(r[i], s[w - 1 - i]) is bitonic; sort it
+        for (uint32_t t = threadIdx.x; t < w; t += blockDim.x) r[t] = min(r[t], s[w - 1 - t]);
+        topk_bitonic_merge(r, 1, w);
+    }
+    for (uint32_t t = threadIdx.x; t < w; t += blockDim.x)
+        ((uint64_t*)a.part)[(size_t)blockIdx.x * w + t] = r[t];
+}
+
+// One workgroup: the stripes' lists (padded to a power of 2 with all-ones lists) are merged
+// pairwise, halving the list count per level, keeping the w smallest keys of each pair.
+GH_KERNEL __launch_bounds__(1024) void gh_topk_final(GhTopkArgs a) {
+    __shared__ uint64_t s[kTopkStripes * kTopkWidth];
+    const uint32_t w = a.width;
+    uint32_t lists = 1;
+    while (lists < a.stripes) lists <<= 1;
+    for (uint32_t t = threadIdx.x; t < lists * w; t += blockDim.x)
+        s[t] = t < a.stripes * w ? ((const uint64_t*)a.part)[t] : ~0ull;
+    for (uint32_t half = lists >> 1; half > 0; half >>= 1) {
+        __syncthreads();
+        // list l (< half) takes the w smallest of itself and list l + half
+        for (uint32_t t = threadIdx.x; t < half * w; t += blockDim.x) {
+            const uint32_t l = t / w, i = t % w;
+            s[t] = min(s[t], s[(l + half) * w + (w - 1 - i)]);
+        }
+        topk_bitonic_merge(s, half, w);
+    }
+    for (uint32_t t = threadIdx.x; t < a.k; t += blockDim.x) {
+        const uint64_t key = s[t];
+        const uint32_t ord = ~(uint32_t)(key >> 32);
+        ((uint32_t*)a.out)[t] = (uint32_t)key;
+        ((uint32_t*)a.out)[a.k + t] = ord ^ ((ord >> 31) ? 0x80000000u : 0xFFFFFFFFu);
+    }
+}

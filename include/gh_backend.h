@@ -178,7 +178,9 @@ int gh_attention_prefill(gh_backend* b, gh_encoder* enc, const gh_buf* out, cons
 int gh_read_logits(gh_backend* b, const gh_buf* logits, uint64_t vocab, float* dst);
 /* lowest index wins on equal logits (strict `>`) */
 int gh_read_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, uint32_t* out);
-/* min(k, vocab) pairs ordered by (logit desc by IEEE total order, index asc) */
+/* min(k, vocab) pairs ordered by (logit desc by IEEE total order, index asc); k <= 128 is
+ * reduced on the device (the Vulkan backend's partial scan, vulkan/kernels/reduce.rs:74-139,
+ * with the merge on the device too), larger k on the host over read-back logits */
 int gh_read_topk(gh_backend* b, const gh_buf* logits, uint64_t vocab, uint64_t k,
                  uint32_t* idx, float* val, uint64_t* count);
 
@@ -254,6 +256,44 @@ int gh_model_read_argmax(gh_model* m, uint32_t* out);
  * position resident on the device; tokens_out[i] receives the argmax of step i. */
 int gh_model_decode_greedy(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps,
                            uint32_t* tokens_out);
+/* read_topk over the model's logits (min(k, vocab) pairs, the order of gh_read_topk) */
+int gh_model_read_topk(gh_model* m, uint64_t k, uint32_t* idx, float* val, uint64_t* count);
+
+/* ---- host sampling (sampling.rs:1-203, restated for the driver's generation loop) ----
+ * The engine samples on the host after the device reduction; these mirror its filters
+ * (repeat penalty -> temperature -> top-k -> top-p -> min-p -> inverse-CDF draw, FP32,
+ * sequential sums) and its xorshift64* generator, so a seed reproduces the same draws. */
+typedef struct gh_sampling { /* api/request.rs:13-20 */
+    float temperature;    /* <= 0: greedy argmax */
+    float top_p;          /* 1: off */
+    uint32_t top_k;       /* 0: off */
+    float min_p;          /* 0: off */
+    float repeat_penalty; /* 1: off */
+    uint64_t seed;
+} gh_sampling;
+/* sampling::plan (sampling.rs:165-192) */
+#define GH_SAMPLE_GREEDY 0
+#define GH_SAMPLE_TOPK 1
+#define GH_SAMPLE_FALLBACK 2
+#define GH_SAMPLE_MAX_DEVICE_K 128u /* sampling::MAX_DEVICE_K */
+int gh_sampling_plan(const gh_sampling* p, uint32_t* k);
+/* Rng::new / Rng::next_f32 (sampling.rs:15-36): the state after seeding; a uniform in [0, 1) */
+uint64_t gh_rng_seed(uint64_t seed);
+float gh_rng_next_f32(uint64_t* state);
+/* sampling::sample over host logits (mutated in place by the penalty) */
+int gh_sample(float* logits, uint64_t vocab, const gh_sampling* p, const uint32_t* recent,
+              uint64_t n_recent, uint64_t* rng, uint32_t* token);
+/* sampling::sample_from_candidates: candidates sorted by (scaled logit desc, index asc) */
+int gh_sample_from_candidates(const uint32_t* idx, const float* logit, uint64_t n,
+                              const gh_sampling* p, uint64_t* rng, uint32_t* token);
+/* generation::drive (family/mistral/generation/mod.rs:75-148): prefill `prompt` at
+ * positions 0.., then up to max_tokens tokens, each from the plan's path — device argmax
+ * (greedy), device top-k + host tail (temperature and 0 < top_k <= 128, no penalty), or
+ * full read-back + gh_sample (otherwise); stops at `eos` (UINT32_MAX: none) or the
+ * context. Each decode step replays the captured decode graph. out receives *n_out tokens. */
+int gh_model_generate(gh_model* m, const uint32_t* prompt, uint32_t n_prompt, const gh_sampling* p,
+                      uint32_t max_tokens, uint32_t eos, uint32_t* out, uint32_t* n_out);
+
 /* KV cache handle of the model's request (for parity checks of the cache contents) */
 int gh_model_kv(gh_model* m, gh_kv* out);
 /* the FP32 residual x of the last token processed (embedding_length floats) */

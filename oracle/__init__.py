@@ -211,7 +211,7 @@ def topk(l, k):
     idx = np.zeros(max(k, 1), dtype=np.uint32)
     val = np.zeros(max(k, 1), dtype=np.float32)
     n = lib().gho_topk(_p(l), l.size, k, _p(idx), _p(val))
-    return [(int(i), float(v)) for i, v in zip(idx[:n], val[:n])]
+    return [(int(i), v) for i, v in zip(idx[:n], val[:n])]  # np.float32: raw bits kept
 
 
 class Model:

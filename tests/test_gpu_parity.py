@@ -337,9 +337,42 @@ def test_argmax_and_topk(hip):
     for l in cases:
         lb = up(hip, l)
         assert hip.read_argmax(lb, vocab) == O.argmax(l)
-        if np.isfinite(l).all():
-            assert hip.read_topk(lb, vocab, 40) == O.topk(l, 40)
+        assert _topk_bits(hip.read_topk(lb, vocab, 40)) == _topk_bits(O.topk(l, 40))
         hip.free_buffer(lb)
+
+
+def _topk_bits(pairs):
+    return [(i, int(np.asarray(v, dtype=np.float32).view(np.uint32))) for i, v in pairs]
+
+
+@pytest.mark.parametrize("vocab,ks", [
+    (5, [1, 3, 99]),                 # the reference's readback test vector sizes; k > vocab
+    (3000, [1, 64, 128, 129]),       # two chunks of 2048; k = 129 takes the host path
+    (131072, [1, 40, 100, 128]),     # the vocabulary of the 8B/14B shapes: 64 stripes
+    (700001, [128, 2]),              # stripes of several 2048-logit chunks (114 stripes)
+])
+def test_topk_device_bit_exact(hip, vocab, ks):
+    """Device top-k vs the oracle (cpu/readback.rs:59-69 order): indices and raw logit bits
+    identical, with exact ties, ±0, ±inf, denormals and NaNs of both signs and two payloads."""
+    rng = np.random.default_rng(vocab)
+    if vocab == 5:
+        bits = np.array([0.1, 2.5, 2.5, -1.0, 2.4], dtype=np.float32).view(np.uint32)
+    else:
+        bits = rng.standard_normal(vocab).astype(np.float32).view(np.uint32).copy()
+        bits[rng.integers(0, vocab, vocab // 5)] = bits[rng.integers(0, vocab, vocab // 5)]
+        specials = np.array([0x7FC00000, 0xFFC00000, 0x7F800001, 0xFF800001, 0x7F800000,
+                             0xFF800000, 0, 0x80000000, 1, 0x80000001], dtype=np.uint32)
+        bits[rng.integers(0, vocab, 3 * specials.size)] = np.repeat(specials, 3)
+        fin = bits.view(np.float32)[np.isfinite(bits.view(np.float32))]
+        bits[rng.integers(0, vocab, 50)] = np.float32(fin.max()).view(np.uint32)  # ties at the top
+    l = bits.view(np.float32)
+    lb = up(hip, l)
+    for k in ks:
+        got = _topk_bits(hip.read_topk(lb, vocab, k))
+        want = _topk_bits(O.topk(l, k))
+        assert len(got) == min(k, vocab)
+        assert got == want, f"vocab {vocab} k {k}"
+    hip.free_buffer(lb)
 
 
 # ---------------------------------------------------------------- graph driver (whole model)
@@ -460,4 +493,61 @@ def test_fused_decode_is_bit_identical_to_op_by_op(hip, shape_name):
         a = hip.download(getattr(kv, role), np.uint16, n).reshape(shape.block_count, 64, -1)
         b = hip.download(getattr(ref.kv, role), np.uint16, n).reshape(shape.block_count, 64, -1)
         assert np.array_equal(a[:, :5], b[:, :5]), role
+    gm.close()
+
+
+# ---------------------------------------------------------------- generation loop (§ sampling)
+def _manual_generate(gm, prompt, p, max_tokens, context):
+    """generation::drive restated over the driver's primitives with the oracle's sampling:
+    the same decode kernels (one replayed graph step per token) and the same device reductions."""
+    from oracle import sampling as S
+    path, k = S.plan(p)
+    st = S.rng_seed(p["seed"])
+    recent = list(prompt)
+    gm.prefill(prompt, 0)
+    out = []
+    while len(out) < max_tokens and len(prompt) + len(out) < context:
+        if path == S.GREEDY:
+            tok = gm.read_argmax()
+        elif path == S.TOPK:
+            inv = np.float32(1.0) / np.float32(p["temperature"])
+            cand = [(i, np.float32(v * inv)) for i, v in gm.read_topk(k)]
+            tok, st = S.sample_from_candidates(cand, p, st)
+        else:
+            tok, st = S.sample(gm.read_logits(), p, recent, st)
+        out.append(tok)
+        recent.append(tok)
+        if len(out) < max_tokens and len(prompt) + len(out) < context:
+            gm.decode_greedy(tok, len(prompt) + len(out) - 1, 1)
+    return out
+
+
+@pytest.mark.parametrize("p", [
+    dict(temperature=0.0, top_p=1.0, top_k=0, min_p=0.0, repeat_penalty=1.0, seed=0),
+    dict(temperature=0.9, top_p=0.95, top_k=40, min_p=0.02, repeat_penalty=1.0, seed=11),
+    dict(temperature=1.2, top_p=1.0, top_k=128, min_p=0.0, repeat_penalty=1.0, seed=12),
+    dict(temperature=0.8, top_p=0.9, top_k=0, min_p=0.05, repeat_penalty=1.15, seed=13),
+], ids=["greedy", "device-topk40", "device-topk128", "fallback-penalty"])
+def test_generate_matches_driver_loop(hip, p):
+    """gh_model_generate (C++ loop, C++ sampling) == the same loop driven from Python with the
+    oracle's sampling, token for token (the device reductions and logits are shared, so any
+    difference is in the loop or the sampling restatement)."""
+    gm, om = _models(hip, "tiny", 34, 96)
+    om.close()
+    prompt = [5, 77, 1024, 3, 650]
+    got = gm.generate(prompt, F.GhSampling(**p), 24)
+    want = _manual_generate(gm, prompt, p, 24, 96)
+    assert [int(t) for t in got] == want
+    # greedy generate == the graph-replayed greedy decode from the prefill's argmax
+    if p["temperature"] == 0.0:
+        gm.prefill(prompt, 0)
+        first = gm.read_argmax()
+        assert int(got[0]) == first
+        assert [int(t) for t in gm.decode_greedy(first, len(prompt), 23)] == want[1:]
+    # stops at the context and at eos
+    short = gm.generate(prompt, F.GhSampling(**p), 500)
+    assert len(short) == 96 - len(prompt)
+    eos = int(got[3])
+    stop = gm.generate(prompt, F.GhSampling(**p), 24, eos=eos)
+    assert [int(t) for t in stop] == want[:want.index(eos)]
     gm.close()
