@@ -132,6 +132,7 @@ SIGNATURES = {
     "gh_model_read_x": (I32, [P, P]),
     "gh_model_weight": (I32, [P, U32, U32, BUFP]),
     "gh_model_read_topk": (I32, [P, U64, P, P, C.POINTER(U64)]),
+    "gh_prefill_rows": (U32, [P, U32, U32]),
     "gh_model_generate": (I32, [P, P, U32, C.POINTER(GhSampling), U32, U32, P, C.POINTER(U32)]),
     "gh_sampling_plan": (I32, [C.POINTER(GhSampling), C.POINTER(U32)]),
     "gh_rng_seed": (U64, [U64]),

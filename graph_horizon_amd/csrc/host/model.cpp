@@ -263,10 +263,22 @@ int run_steps(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps) {
 
 extern "C" {
 
+uint32_t gh_prefill_rows(const gh_backend* b, uint32_t block_count, uint32_t context) {
+    (void)b;
+    (void)block_count;
+    // One policy for every depth: 2048-row chunks. Measured on the 8B shape (34 blocks):
+    // 2048-token prompts 38.7K tok/s in one chunk vs 29.3K in 512-row chunks; 8192-token
+    // prompts 35.6K tok/s vs 36.4K with 4096-row chunks and 24.2K with 512 (each chunk
+    // streams every weight once, and the MFMA GEMM's efficiency grows with the rows). The
+    // scratch for 2048 rows is ~245 MB on the 8B shape. Capped by the context.
+    return std::max<uint32_t>(1, std::min<uint32_t>(2048, context));
+}
+
 int gh_model_create(gh_backend* b, const gh_model_config* cfg, gh_model** out) {
     if (!b || !cfg || !out) return GH_E_INVALID;
     *out = nullptr;
-    const gh_model_config& c = *cfg;
+    gh_model_config c = *cfg;
+    if (c.prefill_rows == 0) c.prefill_rows = gh_prefill_rows(b, c.block_count, c.kv_context);
     if (c.block_count == 0 || c.embedding_length % 256 || c.feed_forward_length % 256 ||
         c.head_count == 0 || c.kv_head_count == 0 || c.head_count % c.kv_head_count ||
         c.key_length != 128 || c.value_length != 128 || c.vocab_size == 0 || c.kv_context == 0 ||

@@ -101,7 +101,7 @@ class GgufFile:
         _check(self.lib.gh_gguf_meta_array_len(self.h, key.encode(), C.byref(v)))
         return v.value
 
-    def model_config(self, kv_context: int, prefill_rows: int = 512, flags: int = 0) -> F.GhModelConfig:
+    def model_config(self, kv_context: int, prefill_rows: int = 0, flags: int = 0) -> F.GhModelConfig:
         cfg = F.GhModelConfig()
         _check(self.lib.gh_gguf_model_config(self.h, kv_context, prefill_rows, C.byref(cfg)))
         cfg.flags = flags
@@ -236,7 +236,7 @@ def write_synthetic_model(path: str, shape: synth.Shape, seed: int, tied: bool =
     write_gguf(path, mistral3_metadata(shape, context_length), tensors)
 
 
-def load_model(backend, path: str, kv_context: int, prefill_rows: int = 512, flags: int = 0):
+def load_model(backend, path: str, kv_context: int, prefill_rows: int = 0, flags: int = 0):
     """A HipModel built from a GGUF file: configuration from its mistral3 metadata, every
     tensor uploaded by gh_gguf_load_model (checked before the first upload)."""
     from .backend import HipModel

@@ -102,7 +102,7 @@ def yarn_params(shape: Shape):
                 q_temperature_scale=0.1)
 
 
-def model_config(shape: Shape, kv_context: int, prefill_rows: int = 512,
+def model_config(shape: Shape, kv_context: int, prefill_rows: int = 0,
                  flags: int = 0) -> F.GhModelConfig:
     y = yarn_params(shape)
     return F.GhModelConfig(

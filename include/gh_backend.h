@@ -212,7 +212,8 @@ typedef struct gh_model_config {
     float rms_epsilon;
     gh_yarn yarn;
     uint32_t kv_context;   /* request KV capacity in tokens (kv_cache::alloc_shape) */
-    uint32_t prefill_rows; /* prefill chunk row capacity (graph/prefill/mod.rs:20-22) */
+    uint32_t prefill_rows; /* prefill chunk row capacity (graph/prefill/mod.rs:20-22);
+                              0: gh_prefill_rows(backend, block_count, kv_context) */
     uint32_t flags;        /* GH_MODEL_* bits */
 } gh_model_config;
 
@@ -237,6 +238,11 @@ enum gh_tensor_id {
     GH_T_OUTPUT_NORM = 17,
     GH_T_OUTPUT = 18
 };
+
+/* The backend's prefill chunk policy (VulkanBackend::prefill_rows, vulkan/mod.rs:65-75 with
+ * profile.rs:42-58; selection.rs:95,124 sizes the request's prefill scratch with it): rows per
+ * prefill batch for a model of block_count blocks and a request context. Host-only. */
+uint32_t gh_prefill_rows(const gh_backend* b, uint32_t block_count, uint32_t context);
 
 typedef struct gh_model gh_model;
 int gh_model_create(gh_backend* b, const gh_model_config* cfg, gh_model** out);

@@ -58,3 +58,13 @@ def test_no_device_is_a_bounded_error():
     r = subprocess.run(["python", "-c", code], capture_output=True, text=True, timeout=120, env=env)
     assert r.returncode == 0, r.stderr
     assert int(r.stdout.strip().splitlines()[-1]) == -2
+
+
+def test_prefill_rows_policy():
+    """gh_prefill_rows (host-only): 2048-row chunks, capped by the context."""
+    lib = C.CDLL(_ffi.LIB_PATH)
+    lib.gh_prefill_rows.restype = C.c_uint32
+    lib.gh_prefill_rows.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32]
+    assert lib.gh_prefill_rows(None, 34, 8192) == 2048
+    assert lib.gh_prefill_rows(None, 40, 600) == 600
+    assert lib.gh_prefill_rows(None, 1, 131072) == 2048

@@ -413,6 +413,26 @@ def test_model_prefill_matches_oracle(hip):
     om.close()
 
 
+def test_model_prefill_policy_chunks(hip):
+    """prefill_rows = 0 takes gh_prefill_rows (2048-row chunks): a 2500-token prompt in two
+    chunks (2048 + 452 rows, the second attending across the first) gives the logits and KV
+    of 512-row chunking within the model tolerance."""
+    from graph_horizon_amd import HipModel
+    shape = synth.SHAPES["tiny"]
+    ctx = 2600
+    assert hip.lib.gh_prefill_rows(hip.h, shape.block_count, ctx) == 2048
+    toks = list(np.random.default_rng(4).integers(0, shape.vocab_size, 2500))
+    logits = []
+    for rows in (0, 512):
+        gm = HipModel(hip, synth.model_config(shape, ctx, rows))
+        for layer, tid, fmt, data in synth.model_tensors(shape, 35):
+            gm.load_tensor(layer, tid, fmt, data)
+        gm.prefill(toks, 0)
+        logits.append(gm.read_logits())
+        gm.close()
+    assert np.allclose(logits[0], logits[1], rtol=2e-2, atol=2e-2)
+
+
 def test_greedy_decode_graph_replay_teacher_forced(hip):
     """64-step greedy decode through the replayed HIP graph; each step's argmax is checked
     against the oracle fed the same (teacher-forced) token history (parity.rs protocol)."""
