@@ -538,7 +538,8 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     const uint32_t cap = max_wg ? max_wg : resident_wgs(b, k, 256, shmem);
     // split-K: one task per workgroup (four waves share it); otherwise one per wave
     const uint32_t want = splitk ? task : ceil_div(task, 4);
-    return launch(b, k, std::max<uint32_t>(1, std::min<uint32_t>(want, cap)), 1, 1, 256, &a, shmem);
+    a.groups = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
+    return launch(b, k, a.groups, 1, 1, 256, &a, shmem);
 }
 
 int op_step_advance(gh_backend* b, void* scalars, void* history) {

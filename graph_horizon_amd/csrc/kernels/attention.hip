@@ -165,7 +165,7 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
     }
     __syncthreads();
     const size_t pbase = ((size_t)row * a.q_heads + h0) * a.splits;
-    for (uint32_t i = tid; i < (uint32_t)G * 128; i += blockDim.x) {
+    for (uint32_t i = tid; i < (uint32_t)G * 128; i += 256) {
         const uint32_t h = i >> 7, d = i & 127u;
         float M = -__builtin_inff();
 #pragma unroll

@@ -142,7 +142,7 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t r0 = blockIdx.x * BR, t0 = blockIdx.y * (4 * WT) + wave * WT;
     const uint32_t units = a.in_dim / 64;
-    const uint32_t per = (units + gridDim.z - 1) / gridDim.z;
+    const uint32_t per = (units + a.splits - 1) / a.splits;
     const uint32_t u0 = blockIdx.z * per, u1 = min(units, u0 + per);
     const uint32_t fm = lane & 31u, fg = lane >> 5;  // fragment row, k half
     const bool wload = threadIdx.x < 2 * BR;
@@ -216,7 +216,7 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
             for (int j = 0; j < TJ; ++j) {
                 const uint32_t row = r0 + 32 * j + fm;
                 if (row >= a.rows) continue;
-                if (gridDim.z == 1)
+                if (a.splits == 1)
                     gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] = gh_f2h(acc[i][j][r]);
                 else
                     gh_gpw<float>(a.part)[((uint64_t)blockIdx.z * a.n + t) * a.rows + row] = acc[i][j][r];
@@ -241,7 +241,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t r0 = blockIdx.x * BR;
     const uint32_t units = a.in_dim / 64;
-    const uint32_t per = (units + gridDim.z - 1) / gridDim.z;
+    const uint32_t per = (units + a.splits - 1) / a.splits;
     const uint32_t u0 = blockIdx.z * per, u1 = min(units, u0 + per);
     if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
     auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };
@@ -342,7 +342,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
             for (int j = 0; j < TJ; ++j) {
                 const uint32_t row = r0 + 32 * j + fm;
                 if (row >= a.rows) continue;
-                if (gridDim.z == 1)
+                if (a.splits == 1)
                     gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] = gh_f2h(acc[i][j][r]);
                 else
                     gh_gpw<float>(a.part)[((uint64_t)blockIdx.z * a.n + t) * a.rows + row] = acc[i][j][r];
@@ -370,8 +370,9 @@ GH_KERNEL __launch_bounds__(512) void gh_gemm3_q6k_r96(GhGemmArgs a) { gemm3_bod
 // Sum split-K partials in split order, round to FP16: out[i] = f16(Σ_s part[s][i]).
 GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce(GhGemmArgs a) {
     const uint64_t total = (uint64_t)a.n * a.rows;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (uint64_t)gridDim.x * blockDim.x) {
+    // launched with min(ceil(total / 256), 4096) workgroups of 256
+    const uint64_t groups = min((total + 255) / 256, (uint64_t)4096);
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += groups * 256) {
         float s = 0.0f;
         for (uint32_t k = 0; k < a.splits; ++k) s += gh_gp<float>(a.part)[k * total + i];
         gh_gpw<uint16_t>(a.out)[i] = gh_f2h(s);

@@ -108,7 +108,7 @@ __device__ __forceinline__ void pair_unit(const X8& x8, uint32_t u, uint4 (&xv)[
 }
 template <uint32_t FMT, class X8>
 __device__ __forceinline__ void stage_x(const X8& x8, uint32_t units, uint4* xs, float4* sums) {
-    for (uint32_t item = threadIdx.x; item < units * 4; item += blockDim.x) {
+    for (uint32_t item = threadIdx.x; item < units * 4; item += 256) {
         const uint32_t u = item >> 2, q = item & 3u;
         uint4 p02, p13;
         float sq;
@@ -449,8 +449,8 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
     float4* xsum4 = (float4*)(lds + 8 * units);
     uint4* xs6 = lds + 9 * units;
     float4* xsum6 = (float4*)(lds + 17 * units);
-    const uint32_t waves = gridDim.x * (blockDim.x >> 6);
-    const uint32_t gw = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t waves = a.groups * 4;  // 256-thread workgroups
+    const uint32_t gw = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     // segment of this wave and its position among the segment's waves
     uint32_t si = 0, w0 = 0, nw = waves;
     if (a.nseg > 1) {
@@ -552,30 +552,42 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
     }
 }
 
-// Single-token launch of one Q4_K or Q6_K matrix with in_dim <= 4096 (one unit per lane):
-// each wave loads and pairs its own lane's slice of x in registers, together with the first
-// task's weights — no LDS, no workgroup barrier; waves run independently from the first load.
+// Single-token launch of one Q4_K or Q6_K matrix with in_dim <= 4096 (one unit per lane).
+// The workgroup stages x once in LDS (two 16-byte pieces per thread, requested before the
+// first task's weights; only an LDS fence and s_barrier separate the staging from its reads,
+// so the weight loads stay in flight across it); each wave then pairs its lanes' x slices in
+// registers and runs its tasks without further barriers. x fetched per wave instead (8 KiB
+// each, 16 waves per CU) measured ~1.5 us of a 10 us 12288x4096 launch.
 template <int R, uint32_t FMT>
 __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
+    __shared__ uint4 xs[512];  // x: in_dim <= 4096 FP16
     const uint32_t lane = threadIdx.x & 63u, nb = a.in_dim >> 8, units = nb * 4;
-    const uint32_t waves = gridDim.x * (blockDim.x >> 6);
-    const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t waves = a.groups * 4;  // 256-thread workgroups
+    const uint32_t gw = blockIdx.x * 4 + (threadIdx.x >> 6);
     const GhGemvSeg sg = a.seg[0];
-    if (gw >= a.tasks) return;  // wave-uniform; this kernel has no barrier
     const uint32_t u = min(lane, units - 1);
     const uint8_t* w[1] = {(const uint8_t*)sg.w};
-    // x first, then the weights: the pairing below waits only for the x loads (in-order
-    // counters) while the weight stream is in flight
     const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x);
-    uint4 xraw[8];
-    load_unit_x<FMT>([&](uint32_t e) { return xh[e >> 3]; }, u, xraw);
+    const uint32_t nx = a.in_dim >> 3, t = threadIdx.x;
+    const uint4 x0 = xh[min(t, nx - 1)], x1 = xh[min(t + 256, nx - 1)];
     __builtin_amdgcn_sched_barrier(0);
+    // waves past the last task (the grid has at most three, all in the last workgroup) load
+    // the last task's rows, take part in the barrier, and leave
+    const uint32_t t0 = min(gw, a.tasks - 1);
     WRow<FMT> wr[1][R];
-    load_step<FMT, R, 1>(w, sg.rows, nb, gw * R, u, wr);
+    load_step<FMT, R, 1>(w, sg.rows, nb, t0 * R, u, wr);
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t pos = epi_needs_pos(sg.epi) ? position(a) : 0u;
     EpiIn<R> ei;
-    epi_load<R, false>(a, sg, 0, gw * R, pos, ei);
+    epi_load<R, false>(a, sg, 0, t0 * R, pos, ei);
+    if (t < nx) xs[t] = x0;
+    if (t + 256 < nx) xs[t + 256] = x1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (gw >= a.tasks) return;  // wave-uniform
+    uint4 xraw[8];
+    load_unit_x<FMT>([&](uint32_t e) { return xs[e >> 3]; }, u, xraw);
     uint4 xv[8];
     float4 xsum;
     pair_raw<FMT>(xraw, xv, xsum);
@@ -626,7 +638,7 @@ __device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a) {
     float4 xsum;
     pair_raw<FMT>(xraw, xv, xsum);
     const Masks mk = make_masks();
-    for (uint32_t k = blockIdx.x; k < a.tasks; k += gridDim.x) {
+    for (uint32_t k = blockIdx.x; k < a.tasks; k += a.groups) {
         if (k != blockIdx.x) {
             load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
             epi_load<R, false>(a, sg, 0, k * R, pos, ei);

@@ -76,7 +76,8 @@ struct GhGemvArgs {
     uint32_t pairs;    // rope pairs per head (rope_dim / 2)
     uint32_t head_dim;
     uint32_t tasks;    // total tasks of the launch
-    uint32_t pad;
+    uint32_t groups;   // workgroups launched (256 threads each): read from here rather than
+                       // from the dispatch packet, whose fields cost a memory round trip
 };
 
 // Prefill GEMM (gemm.hip): out f16 [n][rows] (or FP32 split partials [splits][n][rows]).

@@ -13,7 +13,7 @@ GH_KERNEL __launch_bounds__(256) void gh_rmsnorm_x(GhRmsnormArgs a) {
     GH_GLOBAL uint2* out = gh_gpw<uint2>(a.out + (uint64_t)row * a.dim * 2);
     __shared__ float red[4];
     const float inverse = gh_rms_inverse_256(x, a.dim, a.eps, red);
-    for (uint32_t i = threadIdx.x; i < (a.dim >> 2); i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < (a.dim >> 2); i += 256) {
         const float4 v = x[i];
         const uint2 wv = w[i];
         const uint32_t o0 = gh_f2h(v.x * inverse * gh_h2f(wv.x & 0xFFFFu));
@@ -29,7 +29,7 @@ GH_KERNEL __launch_bounds__(256) void gh_rmsnorm_x(GhRmsnormArgs a) {
 // One thread per (row, head, pair).
 GH_KERNEL __launch_bounds__(256) void gh_rope(GhRopeArgs a) {
 #pragma clang fp contract(off)
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t total = (size_t)a.rows * a.heads * a.pairs;
     if (t >= total) return;
     const uint32_t pair = (uint32_t)(t % a.pairs);
@@ -50,7 +50,7 @@ GH_KERNEL __launch_bounds__(256) void gh_rope(GhRopeArgs a) {
 // silu_mul (cpu/kernels/elementwise/activation.rs:16-29): out = f16(f16(g/(1+exp(-g))) * u).
 GH_KERNEL __launch_bounds__(256) void gh_silu_mul(GhEltArgs a) {
 #pragma clang fp contract(off)
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= a.n) return;
     const float g = gh_h2f(((const uint16_t*)a.a)[i]);
     const float u = gh_h2f(((const uint16_t*)a.b)[i]);
@@ -61,7 +61,7 @@ GH_KERNEL __launch_bounds__(256) void gh_silu_mul(GhEltArgs a) {
 
 // residual_add (cpu/kernels/elementwise/residual.rs:12-22): x(f32) += f16 y.
 GH_KERNEL __launch_bounds__(256) void gh_residual_add(GhEltArgs a) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= a.n) return;
     float* x = (float*)a.out;
     x[i] = x[i] + gh_h2f(((const uint16_t*)a.b)[i]);
@@ -70,7 +70,7 @@ GH_KERNEL __launch_bounds__(256) void gh_residual_add(GhEltArgs a) {
 // kv_write f16 (cpu/kernels/attention/write.rs:50-63): raw FP16 copy of K and V into the
 // caches at element offsets; with pos_ptr the offsets advance by stride * (*pos_ptr).
 GH_KERNEL __launch_bounds__(256) void gh_kv_write(GhKvWriteArgs a) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t pos = a.pos_ptr ? *(const uint32_t*)a.pos_ptr : 0u;
     if (i < a.k_count)
         ((uint16_t*)a.kc)[a.k_off + pos * a.k_stride + i] = ((const uint16_t*)a.k)[i];
@@ -103,15 +103,15 @@ __device__ __forceinline__ void argmax_block(float& v, uint32_t& i) {
     __syncthreads();
     v = sv[0];
     i = si[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) argmax_merge(v, i, sv[w], si[w]);
+    for (int w = 1; w < 4; ++w) argmax_merge(v, i, sv[w], si[w]);
 }
 
 GH_KERNEL __launch_bounds__(256) void gh_argmax_partial(GhArgmaxArgs a) {
     const float* l = (const float*)a.logits;
     float v = -__builtin_inff();
     uint32_t idx = 0xFFFFFFFFu;
-    const uint32_t stride = gridDim.x * blockDim.x;
-    for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < a.n; j += stride) {
+    const uint32_t stride = a.blocks * 256;
+    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < a.n; j += stride) {
         const float x = l[j];
         if (x > v) {  // strict: the first (lowest) index of this thread's subset wins
             v = x;
@@ -128,7 +128,7 @@ GH_KERNEL __launch_bounds__(256) void gh_argmax_partial(GhArgmaxArgs a) {
 GH_KERNEL __launch_bounds__(256) void gh_argmax_final(GhArgmaxArgs a) {
     float v = -__builtin_inff();
     uint32_t idx = 0xFFFFFFFFu;
-    for (uint32_t j = threadIdx.x; j < a.blocks; j += blockDim.x)
+    for (uint32_t j = threadIdx.x; j < a.blocks; j += 256)
         argmax_merge(v, idx, ((const float*)a.part_v)[j], ((const uint32_t*)a.part_i)[j]);
     argmax_block(v, idx);
     if (threadIdx.x == 0) {
@@ -165,11 +165,12 @@ __device__ __forceinline__ uint64_t topk_key(uint32_t bits, uint32_t idx) {
 }
 
 // Ascending bitonic sort of s[0, n), n a power of 2, by the whole workgroup.
+template <uint32_t NT>
 __device__ void topk_sort(uint64_t* s, uint32_t n) {
     for (uint32_t size = 2; size <= n; size <<= 1) {
         for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
             __syncthreads();
-            for (uint32_t t = threadIdx.x; t < n / 2; t += blockDim.x) {
+            for (uint32_t t = threadIdx.x; t < n / 2; t += NT) {
                 const uint32_t i = 2 * t - (t & (stride - 1)), j = i + stride;
                 const uint64_t x = s[i], y = s[j];
                 if ((x > y) == ((i & size) == 0)) {
@@ -184,10 +185,11 @@ __device__ void topk_sort(uint64_t* s, uint32_t n) {
 
 // `lists` independent sorted lists of width w at s + l * w: sorts each bitonic list ascending
 // (compare-exchanges at strides w/2 .. 1, all ascending).
+template <uint32_t NT>
 __device__ void topk_bitonic_merge(uint64_t* s, uint32_t lists, uint32_t w) {
     for (uint32_t stride = w >> 1; stride > 0; stride >>= 1) {
         __syncthreads();
-        for (uint32_t t = threadIdx.x; t < lists * (w / 2); t += blockDim.x) {
+        for (uint32_t t = threadIdx.x; t < lists * (w / 2); t += NT) {
             const uint32_t l = t / (w / 2), u = t % (w / 2);
             const uint32_t i = l * w + 2 * u - (u & (stride - 1)), j = i + stride;
             const uint64_t x = s[i], y = s[j];
@@ -206,17 +208,17 @@ GH_KERNEL __launch_bounds__(512) void gh_topk_partial(GhTopkArgs a) {
     const uint32_t w = a.width;
     const uint64_t b0 = (uint64_t)blockIdx.x * a.per, e = min((uint64_t)a.n, b0 + a.per);
     const uint32_t* bits = (const uint32_t*)a.logits;
-    for (uint32_t t = threadIdx.x; t < w; t += blockDim.x) r[t] = ~0ull;
+    for (uint32_t t = threadIdx.x; t < w; t += 512) r[t] = ~0ull;
     for (uint64_t c = b0; c < e; c += kTopkChunk) {
         __syncthreads();
-        for (uint32_t t = threadIdx.x; t < kTopkChunk; t += blockDim.x)
+        for (uint32_t t = threadIdx.x; t < kTopkChunk; t += 512)
             s[t] = c + t < e ? topk_key(bits[c + t], (uint32_t)(c + t)) : ~0ull;
-        topk_sort(s, kTopkChunk);
+        topk_sort<512>(s, kTopkChunk);
         // the w smallest of (r, s[0, w)): r[i] = min(r[i], s[w - 1 - i]) is bitonic; sort it
-        for (uint32_t t = threadIdx.x; t < w; t += blockDim.x) r[t] = min(r[t], s[w - 1 - t]);
-        topk_bitonic_merge(r, 1, w);
+        for (uint32_t t = threadIdx.x; t < w; t += 512) r[t] = min(r[t], s[w - 1 - t]);
+        topk_bitonic_merge<512>(r, 1, w);
     }
-    for (uint32_t t = threadIdx.x; t < w; t += blockDim.x)
+    for (uint32_t t = threadIdx.x; t < w; t += 512)
         ((uint64_t*)a.part)[(size_t)blockIdx.x * w + t] = r[t];
 }
 
@@ -227,18 +229,18 @@ GH_KERNEL __launch_bounds__(1024) void gh_topk_final(GhTopkArgs a) {
     const uint32_t w = a.width;
     uint32_t lists = 1;
     while (lists < a.stripes) lists <<= 1;
-    for (uint32_t t = threadIdx.x; t < lists * w; t += blockDim.x)
+    for (uint32_t t = threadIdx.x; t < lists * w; t += 1024)
         s[t] = t < a.stripes * w ? ((const uint64_t*)a.part)[t] : ~0ull;
     for (uint32_t half = lists >> 1; half > 0; half >>= 1) {
         __syncthreads();
         // list l (< half) takes the w smallest of itself and list l + half
-        for (uint32_t t = threadIdx.x; t < half * w; t += blockDim.x) {
+        for (uint32_t t = threadIdx.x; t < half * w; t += 1024) {
             const uint32_t l = t / w, i = t % w;
             s[t] = min(s[t], s[(l + half) * w + (w - 1 - i)]);
         }
-        topk_bitonic_merge(s, half, w);
+        topk_bitonic_merge<1024>(s, half, w);
     }
-    for (uint32_t t = threadIdx.x; t < a.k; t += blockDim.x) {
+    for (uint32_t t = threadIdx.x; t < a.k; t += 1024) {
         const uint64_t key = s[t];
         const uint32_t ord = ~(uint32_t)(key >> 32);
         ((uint32_t*)a.out)[t] = (uint32_t)key;

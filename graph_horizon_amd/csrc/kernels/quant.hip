@@ -5,9 +5,9 @@
 #include "gh_common.h"
 
 // One thread per 16-byte chunk of a 144-byte Q4_K block (9 chunks: header, then 8 of qs).
-GH_KERNEL void gh_repack_q4k(GhRepackArgs a) {
+GH_KERNEL __launch_bounds__(256) void gh_repack_q4k(GhRepackArgs a) {
     const size_t total = (size_t)a.rows * a.nb * 9;
-    const size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t c = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (c >= total) return;
     const size_t blk = c / 9;  // row * nb + b
     const uint32_t k = (uint32_t)(c % 9);
@@ -27,9 +27,9 @@ GH_KERNEL void gh_repack_q4k(GhRepackArgs a) {
 }
 
 // One thread per byte of a 210-byte Q6_K block (blocks are not 16-byte aligned in GGUF).
-GH_KERNEL void gh_repack_q6k(GhRepackArgs a) {
+GH_KERNEL __launch_bounds__(256) void gh_repack_q6k(GhRepackArgs a) {
     const size_t total = (size_t)a.rows * a.nb * 210;
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= total) return;
     const size_t blk = i / 210;
     const uint32_t j = (uint32_t)(i % 210);
@@ -57,11 +57,11 @@ GH_KERNEL void gh_repack_q6k(GhRepackArgs a) {
 
 // dequant_row_q4_k (backend/cpu/dequant.rs:93-123): w = (d*sc)*q - dmin*mn with two
 // roundings (mul, mul, sub; contraction off), one thread per output value.
-GH_KERNEL void gh_dequant_q4k(GhDequantArgs a) {
+GH_KERNEL __launch_bounds__(256) void gh_dequant_q4k(GhDequantArgs a) {
 #pragma clang fp contract(off)
     const uint32_t in_dim = a.nb * 256;
     const size_t total = (size_t)a.rows * in_dim;
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= total) return;
     const uint32_t r = (uint32_t)(t / in_dim);
     const uint32_t i = (uint32_t)(t % in_dim);
@@ -86,11 +86,11 @@ GH_KERNEL void gh_dequant_q4k(GhDequantArgs a) {
 }
 
 // dequant_row_q6_k (backend/cpu/dequant.rs:274-308): w = (d*scale)*(q6 - 32).
-GH_KERNEL void gh_dequant_q6k(GhDequantArgs a) {
+GH_KERNEL __launch_bounds__(256) void gh_dequant_q6k(GhDequantArgs a) {
 #pragma clang fp contract(off)
     const uint32_t in_dim = a.nb * 256;
     const size_t total = (size_t)a.rows * in_dim;
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= total) return;
     const uint32_t r = (uint32_t)(t / in_dim);
     const uint32_t i = (uint32_t)(t % in_dim);
