@@ -539,7 +539,10 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     // split-K: one task per workgroup (four waves share it); otherwise one per wave
     const uint32_t want = splitk ? task : ceil_div(task, 4);
     a.groups = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
-    return launch(b, k, a.groups, 1, 1, 256, &a, shmem);
+    // the kernels' leading scalar parameters (preloaded into SGPRs), then the full arguments
+    void* params[] = {&a.x, &a.seg[0].w, &a.norm_w, &a.in_dim, &a.seg[0].rows, &a.tasks, &a.groups, &a};
+    return hip_check(b, hipModuleLaunchKernel(b->fn[k], a.groups, 1, 1, 256, 1, 1, shmem, b->stream, params, nullptr),
+                     "hipModuleLaunchKernel");
 }
 
 int op_step_advance(gh_backend* b, void* scalars, void* history) {

@@ -386,8 +386,16 @@ __device__ __forceinline__ void epilogue(const GhGemvArgs& a, const GhGemvSeg& s
 // MODE: which row kernels a launch may need (specialized to keep register use low).
 enum : int { kModeQ4 = 0, kModeQ6 = 1, kModeMixed = 2, kModeSwiglu = 3 };
 
-__device__ __forceinline__ uint32_t i_end(const GhGemvArgs& a, uint32_t si) {
-    return si + 1 < a.nseg ? a.seg[si + 1].task0 : a.tasks;
+// The launch's first-needed arguments, passed as leading scalar kernel parameters that the
+// dispatch preloads into SGPRs (-amdgpu-kernarg-preload-count): x and the first weight
+// addresses are known without waiting for a kernarg load (~0.3 us per launch measured).
+struct GhHot {
+    uint64_t x, w0, nw;  // a.x, a.seg[0].w, a.norm_w
+    uint32_t in_dim, rows0, tasks, groups;
+};
+
+__device__ __forceinline__ uint32_t i_end(const GhGemvArgs& a, const GhHot& h, uint32_t si) {
+    return si + 1 < a.nseg ? a.seg[si + 1].task0 : h.tasks;
 }
 
 // A wave's work: tasks first, first + stride, ... < ntask of one segment; a task is nch chunks
@@ -441,24 +449,24 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // staging). Off for the RMSNorm variants: their staging is short (x and the norm weights are
 // cache-resident) and the held registers cost more than the overlap gains (measured on decode).
 template <int R, int MODE, bool NORM, bool PRIME = !NORM>
-__device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
+__device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     extern __shared__ uint4 lds[];
     constexpr int M = MODE == kModeSwiglu ? 2 : 1;
-    const uint32_t nb = a.in_dim >> 8, units = nb * 4;
+    const uint32_t nb = h.in_dim >> 8, units = nb * 4;
     uint4* xs4 = lds;
     float4* xsum4 = (float4*)(lds + 8 * units);
     uint4* xs6 = lds + 9 * units;
     float4* xsum6 = (float4*)(lds + 17 * units);
-    const uint32_t waves = a.groups * 4;  // 256-thread workgroups
+    const uint32_t waves = h.groups * 4;  // 256-thread workgroups
     const uint32_t gw = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     // segment of this wave and its position among the segment's waves
     uint32_t si = 0, w0 = 0, nw = waves;
     if (a.nseg > 1) {
         uint32_t acc_w = 0;
         for (uint32_t i = 0; i < a.nseg; ++i) {
-            const uint32_t t_end = i + 1 < a.nseg ? a.seg[i + 1].task0 : a.tasks;
+            const uint32_t t_end = i + 1 < a.nseg ? a.seg[i + 1].task0 : h.tasks;
             const uint32_t t_n = t_end - a.seg[i].task0;
-            uint32_t n_w = i + 1 < a.nseg ? (uint32_t)(((uint64_t)t_n * waves + a.tasks - 1) / a.tasks)
+            uint32_t n_w = i + 1 < a.nseg ? (uint32_t)(((uint64_t)t_n * waves + h.tasks - 1) / h.tasks)
                                           : waves - acc_w;
             n_w = max(1u, min(n_w, waves - acc_w - (a.nseg - 1 - i)));
             if (gw >= acc_w && gw < acc_w + n_w) {
@@ -470,7 +478,7 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
         }
     }
     const GhGemvSeg sg = a.seg[si];
-    const uint32_t ntask = i_end(a, si) - sg.task0, first = gw - w0;
+    const uint32_t ntask = i_end(a, h, si) - sg.task0, first = gw - w0;
     const Masks mk = make_masks();
     // The first step's weights of the kernel's primary format are requested before x is
     // staged, so their latency overlaps the staging.
@@ -499,9 +507,9 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
             // of gh_rms_inverse_256, and the normalized FP16 row f16((x · inverse) · f16 w) —
             // the bits gh_rmsnorm_x stores — goes to LDS, from which x is staged.
             constexpr uint32_t kMaxChunks = 5;  // in_dim <= 5120
-            const uint32_t n4 = a.in_dim >> 2;
-            const GH_GLOBAL float4* xr = gh_gp<float4>(a.x + (uint64_t)t * a.in_dim * 4);
-            const GH_GLOBAL uint2* wn = gh_gp<uint2>(a.norm_w);
+            const uint32_t n4 = h.in_dim >> 2;
+            const GH_GLOBAL float4* xr = gh_gp<float4>(h.x + (uint64_t)t * h.in_dim * 4);
+            const GH_GLOBAL uint2* wn = gh_gp<uint2>(h.nw);
             uint2* xn = (uint2*)(lds + (MODE == kModeMixed ? 18 : 9) * units);
             float* red = (float*)(xn + n4);
             float4 v[kMaxChunks];
@@ -516,7 +524,7 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
 #pragma unroll
             for (uint32_t k = 0; k < kMaxChunks; ++k)
                 if (threadIdx.x + 256 * k < n4) ss = gh_rms_add(ss, v[k]);
-            const float inv = gh_rms_finish_256(ss, a.in_dim, a.eps, red);
+            const float inv = gh_rms_finish_256(ss, h.in_dim, a.eps, red);
 #pragma unroll
             for (uint32_t k = 0; k < kMaxChunks; ++k) {
 #pragma clang fp contract(off)
@@ -533,7 +541,7 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
             const uint4* xn4 = (const uint4*)xn;
             stage([&](uint32_t e) { return xn4[e >> 3]; });
         } else {
-            const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x + (uint64_t)t * a.in_dim * 2);
+            const GH_GLOBAL uint4* xh = gh_gp<uint4>(h.x + (uint64_t)t * h.in_dim * 2);
             stage([&](uint32_t e) { return xh[e >> 3]; });
         }
         __syncthreads();
@@ -559,21 +567,23 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a) {
 // registers and runs its tasks without further barriers. x fetched per wave instead (8 KiB
 // each, 16 waves per CU) measured ~1.5 us of a 10 us 12288x4096 launch.
 template <int R, uint32_t FMT>
-__device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
+__device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h) {
     __shared__ uint4 xs[512];  // x: in_dim <= 4096 FP16
-    const uint32_t lane = threadIdx.x & 63u, nb = a.in_dim >> 8, units = nb * 4;
-    const uint32_t waves = a.groups * 4;  // 256-thread workgroups
+    const uint32_t lane = threadIdx.x & 63u, nb = h.in_dim >> 8, units = nb * 4;
+    const uint32_t waves = h.groups * 4;  // 256-thread workgroups
     const uint32_t gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const GhGemvSeg sg = a.seg[0];
+    GhGemvSeg sg = a.seg[0];
+    sg.w = h.w0;
+    sg.rows = h.rows0;
     const uint32_t u = min(lane, units - 1);
     const uint8_t* w[1] = {(const uint8_t*)sg.w};
-    const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x);
-    const uint32_t nx = a.in_dim >> 3, t = threadIdx.x;
+    const GH_GLOBAL uint4* xh = gh_gp<uint4>(h.x);
+    const uint32_t nx = h.in_dim >> 3, t = threadIdx.x;
     const uint4 x0 = xh[min(t, nx - 1)], x1 = xh[min(t + 256, nx - 1)];
     __builtin_amdgcn_sched_barrier(0);
     // waves past the last task (the grid has at most three, all in the last workgroup) load
     // the last task's rows, take part in the barrier, and leave
-    const uint32_t t0 = min(gw, a.tasks - 1);
+    const uint32_t t0 = min(gw, h.tasks - 1);
     WRow<FMT> wr[1][R];
     load_step<FMT, R, 1>(w, sg.rows, nb, t0 * R, u, wr);
     __builtin_amdgcn_sched_barrier(0);
@@ -585,14 +595,14 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-    if (gw >= a.tasks) return;  // wave-uniform
+    if (gw >= h.tasks) return;  // wave-uniform
     uint4 xraw[8];
     load_unit_x<FMT>([&](uint32_t e) { return xs[e >> 3]; }, u, xraw);
     uint4 xv[8];
     float4 xsum;
     pair_raw<FMT>(xraw, xv, xsum);
     const Masks mk = make_masks();
-    for (uint32_t k = gw; k < a.tasks; k += waves) {
+    for (uint32_t k = gw; k < h.tasks; k += waves) {
         if (k != gw) {
             load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
             epi_load<R, false>(a, sg, 0, k * R, pos, ei);
@@ -614,31 +624,33 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a) {
 // loads go out from all four waves at once — one memory round trip per task instead of one
 // per 64-unit chunk. The four partial sums of a row are added in wave order through LDS.
 template <int R, uint32_t FMT>
-__device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a) {
+__device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a, const GhHot& h) {
     __shared__ float part[4][R];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nb = a.in_dim >> 8;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nb = h.in_dim >> 8;
     const uint32_t units = nb * 4, q = (units + 3) / 4;
     const uint32_t uw = wave * q + lane;                    // this lane's unit
     const bool active = lane < q && uw < units;
     const uint32_t u = min(uw, units - 1);
-    const GhGemvSeg sg = a.seg[0];
+    GhGemvSeg sg = a.seg[0];
+    sg.w = h.w0;
+    sg.rows = h.rows0;
     const uint8_t* w[1] = {(const uint8_t*)sg.w};
-    const GH_GLOBAL uint4* xh = gh_gp<uint4>(a.x);
+    const GH_GLOBAL uint4* xh = gh_gp<uint4>(h.x);
     uint4 xraw[8];
     load_unit_x<FMT>([&](uint32_t e) { return xh[e >> 3]; }, u, xraw);
     __builtin_amdgcn_sched_barrier(0);
     WRow<FMT> wr[1][R];
     // unconditional (clamped task): loads outside branches keep the wait counts exact
-    load_step<FMT, R, 1>(w, sg.rows, nb, min(blockIdx.x, a.tasks - 1) * R, u, wr);
+    load_step<FMT, R, 1>(w, sg.rows, nb, min(blockIdx.x, h.tasks - 1) * R, u, wr);
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t pos = epi_needs_pos(sg.epi) ? position(a) : 0u;
     EpiIn<R> ei;
-    if (blockIdx.x < a.tasks) epi_load<R, false>(a, sg, 0, blockIdx.x * R, pos, ei);
+    if (blockIdx.x < h.tasks) epi_load<R, false>(a, sg, 0, blockIdx.x * R, pos, ei);
     uint4 xv[8];
     float4 xsum;
     pair_raw<FMT>(xraw, xv, xsum);
     const Masks mk = make_masks();
-    for (uint32_t k = blockIdx.x; k < a.tasks; k += a.groups) {
+    for (uint32_t k = blockIdx.x; k < h.tasks; k += h.groups) {
         if (k != blockIdx.x) {
             load_step<FMT, R, 1>(w, sg.rows, nb, k * R, u, wr);
             epi_load<R, false>(a, sg, 0, k * R, pos, ei);
@@ -665,34 +677,40 @@ __device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a) {
 
 }  // namespace
 
+// Kernel parameters: the hot scalars (GhHot), preloaded into SGPRs, then the full arguments.
+#define GH_HOT_PARAMS                                                                            \
+    uint64_t x, uint64_t w0, uint64_t nw, uint32_t in_dim, uint32_t rows0, uint32_t tasks,        \
+        uint32_t groups, GhGemvArgs a
+#define GH_HOT GhHot{x, w0, nw, in_dim, rows0, tasks, groups}
+
 // NORM kernels (suffix _n) stage the RMSNorm of an FP32 x (norm_w set); the others read FP16 x.
-#define GH_GEMV(NAME, R, MODE)                                                                 \
-    GH_KERNEL __launch_bounds__(256) void NAME(GhGemvArgs a) { gemv_body<R, MODE, false>(a); } \
-    GH_KERNEL __launch_bounds__(256) void NAME##_n(GhGemvArgs a) { gemv_body<R, MODE, true>(a); }
+#define GH_GEMV(NAME, R, MODE)                                                                   \
+    GH_KERNEL __launch_bounds__(256) void NAME(GH_HOT_PARAMS) { gemv_body<R, MODE, false>(a, GH_HOT); } \
+    GH_KERNEL __launch_bounds__(256) void NAME##_n(GH_HOT_PARAMS) { gemv_body<R, MODE, true>(a, GH_HOT); }
 GH_GEMV(gh_gemv_q4k_r1, 1, kModeQ4)
 GH_GEMV(gh_gemv_q4k_r2, 2, kModeQ4)
 GH_GEMV(gh_gemv_q6k_r1, 1, kModeQ6)
 GH_GEMV(gh_gemv_q6k_r2, 2, kModeQ6)
-GH_KERNEL __launch_bounds__(256) void gh_gemv_mixed_r2(GhGemvArgs a) { gemv_body<2, kModeMixed, false>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_mixed_r2(GH_HOT_PARAMS) { gemv_body<2, kModeMixed, false>(a, GH_HOT); }
 // The RMSNorm mixed (Q/K/V) kernel is held to 168 VGPRs, three waves per SIMD: with 3 x 256
 // CUs x 4 waves resident, an 8B-shaped QKV launch (4096 + 1024 + 1024 rows, R = 2) is one task
 // per wave instead of two rounds.
-GH_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gh_gemv_mixed_r2_n(GhGemvArgs a) {
-    gemv_body<2, kModeMixed, true>(a);
+GH_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gh_gemv_mixed_r2_n(GH_HOT_PARAMS) {
+    gemv_body<2, kModeMixed, true>(a, GH_HOT);
 }
 GH_GEMV(gh_gemv_swiglu_r1, 1, kModeSwiglu)
 GH_GEMV(gh_gemv_swiglu_r2, 2, kModeSwiglu)
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4(GhGemvArgs a) { gemv_body<4, kModeQ4, false>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4(GH_HOT_PARAMS) { gemv_body<4, kModeQ4, false>(a, GH_HOT); }
 // direct-x variants (suffix _d): single token, one matrix, in_dim <= 4096, no RMSNorm
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_d(GhGemvArgs a) { gemv_direct<1, kQ4K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_d(GhGemvArgs a) { gemv_direct<2, kQ4K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_d(GhGemvArgs a) { gemv_direct<1, kQ6K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_d(GhGemvArgs a) { gemv_direct<2, kQ6K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4_d(GhGemvArgs a) { gemv_direct<4, kQ4K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4_d(GhGemvArgs a) { gemv_direct<4, kQ6K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ4K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ4K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ6K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ6K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4_d(GH_HOT_PARAMS) { gemv_direct<4, kQ4K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4_d(GH_HOT_PARAMS) { gemv_direct<4, kQ6K>(a, GH_HOT); }
 // split-K variants (suffix _k): single token, one matrix, 4096 < in_dim <= 16384, no RMSNorm
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_k(GhGemvArgs a) { gemv_splitk<1, kQ4K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_k(GhGemvArgs a) { gemv_splitk<2, kQ4K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_k(GhGemvArgs a) { gemv_splitk<1, kQ6K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_k(GhGemvArgs a) { gemv_splitk<2, kQ6K>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4(GhGemvArgs a) { gemv_body<4, kModeQ6, false>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_k(GH_HOT_PARAMS) { gemv_splitk<1, kQ4K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_k(GH_HOT_PARAMS) { gemv_splitk<2, kQ4K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_k(GH_HOT_PARAMS) { gemv_splitk<1, kQ6K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_k(GH_HOT_PARAMS) { gemv_splitk<2, kQ6K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4(GH_HOT_PARAMS) { gemv_body<4, kModeQ6, false>(a, GH_HOT); }
