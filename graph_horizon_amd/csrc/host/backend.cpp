@@ -364,7 +364,11 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.rows = nr;
         a.splits = splits;
         a.scale = 1.0f / std::sqrt((float)kv->head_dim);
-        rc = launch(b, k, splits, kv->kv_heads, nr, 256, &a);
+        // leading scalar parameters (preloaded into SGPRs), then the full arguments
+        void* params[] = {&a.q, &a.kc, &a.vc, &a.pos_ptr, &a.layer, &a.context, &a.q_heads, &a.kv_heads, &a};
+        rc = hip_check(b, hipModuleLaunchKernel(b->fn[k], splits, kv->kv_heads, nr, 256, 1, 1, 0, b->stream, params,
+                                                nullptr),
+                       "hipModuleLaunchKernel");
         if (rc) return rc;
     }
     return GH_OK;

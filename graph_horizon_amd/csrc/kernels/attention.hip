@@ -101,8 +101,15 @@ __device__ __forceinline__ void chunk_step(const ChunkRegs<G>& r, const uint4 (&
     }
 }
 
+// The decode kernels' first-needed arguments, passed as leading scalar kernel parameters that
+// the dispatch preloads into SGPRs: the query, cache and position loads need no kernarg load.
+struct AttnHot {
+    uint64_t q, kc, vc, pos_ptr;
+    uint32_t layer, context, q_heads, kv_heads;
+};
+
 template <int G>
-__device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
+__device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& hot) {
     __shared__ float wm[kWaves][G], wl[kWaves][G];
     __shared__ float wacc[kWaves][G][128];
     __shared__ float wsplit[G][kMaxSplits];
@@ -116,18 +123,18 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         const GH_GLOBAL uint4* qp =
-            gh_gp<uint4>(a.q + (((uint64_t)row * a.q_heads + h0 + h) * 128 + (lane & 3u) * 32) * 2);
+            gh_gp<uint4>(hot.q + (((uint64_t)row * hot.q_heads + h0 + h) * 128 + (lane & 3u) * 32) * 2);
 #pragma unroll
         for (int i = 0; i < 4; ++i) qv[h][i] = qp[i];
     }
-    const size_t kv_row = (size_t)a.kv_heads * 128;
-    const size_t cache0 = (size_t)a.layer * a.context * kv_row + (size_t)kvh * 128;
-    const uint16_t* kc = (const uint16_t*)a.kc + cache0;
-    const uint16_t* vc = (const uint16_t*)a.vc + cache0;
+    const size_t kv_row = (size_t)hot.kv_heads * 128;
+    const size_t cache0 = (size_t)hot.layer * hot.context * kv_row + (size_t)kvh * 128;
+    const uint16_t* kc = (const uint16_t*)hot.kc + cache0;
+    const uint16_t* vc = (const uint16_t*)hot.vc + cache0;
     // this split's first chunk (chunk `split`) is requested before the position arrives
     ChunkRegs<G> ra, rb;
-    load_chunk<G>(kc, vc, kv_row, split, a.context, ra);
-    const uint32_t pos = (a.pos_ptr ? *gh_gp<uint32_t>(a.pos_ptr) : 0u) + a.base + row;
+    load_chunk<G>(kc, vc, kv_row, split, hot.context, ra);
+    const uint32_t pos = (hot.pos_ptr ? *gh_gp<uint32_t>(hot.pos_ptr) : 0u) + a.base + row;
     const uint32_t len = pos + 1;
     const uint32_t nchunk = (len + kChunk - 1) / kChunk;
     const uint32_t nsplit = min(nchunk, a.splits);
@@ -164,7 +171,7 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
         wacc[wave][h][2 * lane + 1] = acc[h][1];
     }
     __syncthreads();
-    const size_t pbase = ((size_t)row * a.q_heads + h0) * a.splits;
+    const size_t pbase = ((size_t)row * hot.q_heads + h0) * a.splits;
     for (uint32_t i = tid; i < (uint32_t)G * 128; i += 256) {
         const uint32_t h = i >> 7, d = i & 127u;
         float M = -__builtin_inff();
@@ -178,7 +185,7 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
             v += e * wacc[w][h][d];
         }
         if (nsplit == 1) {
-            gh_gpw<uint16_t>(a.out)[((size_t)row * a.q_heads + h0 + h) * 128 + d] = gh_f2h(v / L);
+            gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0 + h) * 128 + d] = gh_f2h(v / L);
         } else {
             const size_t pi = pbase + (size_t)h * a.splits + split;
             gh_gpw<float>(a.part_acc)[pi * 128 + d] = v;
@@ -193,7 +200,7 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
     // the last workgroup of this (row, kv head) merges the splits
     __syncthreads();
     if (tid == 0) {
-        uint32_t* ctr = (uint32_t*)a.counters + (size_t)row * a.kv_heads + kvh;
+        uint32_t* ctr = (uint32_t*)a.counters + (size_t)row * hot.kv_heads + kvh;
         const uint32_t done =
             __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         last = (done + 1 == nsplit) ? 1u : 0u;
@@ -232,7 +239,7 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
             float acc_o = 0.0f;
 #pragma unroll
             for (uint32_t j = 0; j < kMaxSplits; ++j) acc_o += wsplit[h][j] * pv[o][j];
-            gh_gpw<uint16_t>(a.out)[((size_t)row * a.q_heads + h0 + h) * 128 + d] = gh_f2h(acc_o);
+            gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0 + h) * 128 + d] = gh_f2h(acc_o);
         }
     } else {
         // G = 1: 128 outputs, threads 0..127
@@ -242,17 +249,21 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a) {
 #pragma unroll
             for (uint32_t j = 0; j < kMaxSplits; ++j)
                 acc_o += wsplit[0][j] * pa[(size_t)min(j, nsplit - 1) * 128];
-            gh_gpw<uint16_t>(a.out)[((size_t)row * a.q_heads + h0) * 128 + tid] = gh_f2h(acc_o);
+            gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0) * 128 + tid] = gh_f2h(acc_o);
         }
     }
 }
 
 }  // namespace
 
-GH_KERNEL __launch_bounds__(256) void gh_attn_g1(GhAttnArgs a) { attn_body<1>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_g2(GhAttnArgs a) { attn_body<2>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_g4(GhAttnArgs a) { attn_body<4>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_g8(GhAttnArgs a) { attn_body<8>(a); }
+#define GH_ATTN_PARAMS                                                                          \
+    uint64_t q, uint64_t kc, uint64_t vc, uint64_t pos_ptr, uint32_t layer, uint32_t context,     \
+        uint32_t q_heads, uint32_t kv_heads, GhAttnArgs a
+#define GH_ATTN_HOT AttnHot{q, kc, vc, pos_ptr, layer, context, q_heads, kv_heads}
+GH_KERNEL __launch_bounds__(256) void gh_attn_g1(GH_ATTN_PARAMS) { attn_body<1>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_g2(GH_ATTN_PARAMS) { attn_body<2>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_g4(GH_ATTN_PARAMS) { attn_body<4>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_g8(GH_ATTN_PARAMS) { attn_body<8>(a, GH_ATTN_HOT); }
 
 // ---------------------------------------------------------------------------------------------
 // Causal GQA prefill attention on the matrix cores (flash attention, G = 4 query heads per kv
