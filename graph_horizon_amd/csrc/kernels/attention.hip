@@ -101,6 +101,14 @@ __device__ __forceinline__ void chunk_step(const ChunkRegs<G>& r, const uint4 (&
     }
 }
 
+// Agent-scope relaxed atomic accesses for the split partials (see the merge in attn_body).
+__device__ __forceinline__ void st_agent(GH_GLOBAL float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const GH_GLOBAL float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The decode kernels' first-needed arguments, passed as leading scalar kernel parameters that
 // the dispatch preloads into SGPRs: the query, cache and position loads need no kernarg load.
 struct AttnHot {
@@ -188,29 +196,36 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
             gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0 + h) * 128 + d] = gh_f2h(v / L);
         } else {
             const size_t pi = pbase + (size_t)h * a.splits + split;
-            gh_gpw<float>(a.part_acc)[pi * 128 + d] = v;
+            st_agent(gh_gpw<float>(a.part_acc) + pi * 128 + d, v);
             if (d == 0) {
-                gh_gpw<float>(a.part_m)[pi] = M;
-                gh_gpw<float>(a.part_l)[pi] = L;
+                st_agent(gh_gpw<float>(a.part_m) + pi, M);
+                st_agent(gh_gpw<float>(a.part_l) + pi, L);
             }
         }
     }
     if (nsplit == 1) return;
 
-    // the last workgroup of this (row, kv head) merges the splits
+    // The last workgroup of this (row, kv head) merges the splits. Every partial crosses
+    // workgroups only through agent-scope atomic accesses — stores written through to the
+    // device coherence point, loads that do not hit a stale L2 line of another XCD — so the
+    // exchange needs no L2 writeback or invalidation (an agent-scope release/acquire pair
+    // would do both to the whole L2: ~3 us per launch measured). Each thread waits for its
+    // own stores to complete before the barrier, so the counter increment follows all of the
+    // workgroup's partials; the last workgroup issues its loads only after it has seen the
+    // count (the barrier that publishes `last` orders them after the atomic's return).
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
         uint32_t* ctr = (uint32_t*)a.counters + (size_t)row * hot.kv_heads + kvh;
-        const uint32_t done =
-            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t done = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = (done + 1 == nsplit) ? 1u : 0u;
         if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // every partial this workgroup needs is requested before any is used (indexes past
-    // nsplit re-read split nsplit - 1 and get weight 0)
+    // nsplit re-read split nsplit - 1 and get weight 0; unconditional loads measured faster
+    // than skipping them)
     constexpr uint32_t kOut = (uint32_t)G * 128 / 256;  // outputs per thread (G >= 2)
     float pv[kOut > 0 ? kOut : 1][kMaxSplits];
 #pragma unroll
@@ -218,14 +233,14 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
         const uint32_t i = tid + 256 * o, h = i >> 7, d = i & 127u;
         const GH_GLOBAL float* pa = gh_gp<float>(a.part_acc) + (pbase + (size_t)h * a.splits) * 128 + d;
 #pragma unroll
-        for (uint32_t j = 0; j < kMaxSplits; ++j) pv[o][j] = pa[(size_t)min(j, nsplit - 1) * 128];
+        for (uint32_t j = 0; j < kMaxSplits; ++j) pv[o][j] = ld_agent(pa + (size_t)min(j, nsplit - 1) * 128);
     }
     // weights e^{m_s - M} / L per (head, split): lanes are splits, wave h handles head h
     for (uint32_t h = wave; h < (uint32_t)G; h += kWaves) {
         const size_t base = pbase + (size_t)h * a.splits;
         const uint32_t s2 = min(lane, nsplit - 1);
-        const float ms = gh_gp<float>(a.part_m)[base + s2];
-        const float ls = gh_gp<float>(a.part_l)[base + s2];
+        const float ms = ld_agent(gh_gp<float>(a.part_m) + base + s2);
+        const float ls = ld_agent(gh_gp<float>(a.part_l) + base + s2);
         const float M = gh_wave_max(lane < nsplit ? ms : -__builtin_inff());
         const float w = lane < nsplit ? expf(ms - M) : 0.0f;
         const float L = gh_wave_sum(w * ls);
@@ -248,7 +263,7 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
             float acc_o = 0.0f;
 #pragma unroll
             for (uint32_t j = 0; j < kMaxSplits; ++j)
-                acc_o += wsplit[0][j] * pa[(size_t)min(j, nsplit - 1) * 128];
+                acc_o += wsplit[0][j] * ld_agent(pa + (size_t)min(j, nsplit - 1) * 128);
             gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0) * 128 + tid] = gh_f2h(acc_o);
         }
     }

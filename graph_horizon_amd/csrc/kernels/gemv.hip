@@ -446,9 +446,12 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // Waves are split between the segments in proportion to their tasks (args: seg.task0 is the
 // first task index, the wave split is recomputed here), so a wave only ever runs one format.
 // PRIME: request the first step's weights before x is staged (their latency overlaps the
-// staging). Off for the RMSNorm variants: their staging is short (x and the norm weights are
-// cache-resident) and the held registers cost more than the overlap gains (measured on decode).
-template <int R, int MODE, bool NORM, bool PRIME = !NORM>
+// staging). With RMSNorm (NORM) the first token's x row is requested before them: the memory
+// counter is in order, so the staging waits only for its own loads. Off for the RMSNorm
+// two-matrix (SwiGLU) and mixed kernels: holding their primed rows next to the staging raises the
+// SwiGLU kernel to 193 VGPRs (two waves per SIMD instead of three; measured 546 vs 560 tok/s
+// on the 8B decode) and spills in the mixed kernel.
+template <int R, int MODE, bool NORM, bool PRIME = (!NORM || (MODE != kModeSwiglu && MODE != kModeMixed))>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     extern __shared__ uint4 lds[];
     constexpr int M = MODE == kModeSwiglu ? 2 : 1;
@@ -483,6 +486,27 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     // The first step's weights of the kernel's primary format are requested before x is
     // staged, so their latency overlaps the staging.
     constexpr uint32_t F0 = MODE == kModeQ6 ? kQ6K : kQ4K;
+    // NORM: the first token's FP32 x row and the norm weights (each thread: chunks tid + 256 k)
+    constexpr uint32_t kMaxChunks = 5;  // in_dim <= 5120
+    const uint32_t n4 = h.in_dim >> 2;
+    float4 v[kMaxChunks];
+    uint2 wv[kMaxChunks];
+    auto load_norm_row = [&](uint32_t t) __attribute__((always_inline)) {
+        const GH_GLOBAL float4* xr = gh_gp<float4>(h.x + (uint64_t)t * h.in_dim * 4);
+#pragma unroll
+        for (uint32_t k = 0; k < kMaxChunks; ++k) v[k] = xr[min(threadIdx.x + 256 * k, n4 - 1)];
+    };
+    // the norm weights are requested after Σx²'s partial (they are first used after the
+    // reduction), so they are not held in registers next to the primed weights
+    auto load_norm_w = [&]() __attribute__((always_inline)) {
+        const GH_GLOBAL uint2* wn = gh_gp<uint2>(h.nw);
+#pragma unroll
+        for (uint32_t k = 0; k < kMaxChunks; ++k) wv[k] = wn[min(threadIdx.x + 256 * k, n4 - 1)];
+    };
+    if constexpr (NORM && PRIME) {
+        load_norm_row(0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     WRow<F0> w0r[M][R];
     const bool primed = PRIME && sg.fmt == F0 && first < ntask;
     if (primed) {
@@ -503,27 +527,18 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
         };
         if constexpr (NORM) {
             // rmsnorm_x fused: x is the FP32 residual row. Each thread loads its float4 chunks
-            // (tid + 256 k) and their norm weights once, the row's Σx² is reduced in the order
-            // of gh_rms_inverse_256, and the normalized FP16 row f16((x · inverse) · f16 w) —
-            // the bits gh_rmsnorm_x stores — goes to LDS, from which x is staged.
-            constexpr uint32_t kMaxChunks = 5;  // in_dim <= 5120
-            const uint32_t n4 = h.in_dim >> 2;
-            const GH_GLOBAL float4* xr = gh_gp<float4>(h.x + (uint64_t)t * h.in_dim * 4);
-            const GH_GLOBAL uint2* wn = gh_gp<uint2>(h.nw);
+            // (tid + 256 k) and their norm weights once (token 0's before the primed weights),
+            // the row's Σx² is reduced in the order of gh_rms_inverse_256, and the normalized
+            // FP16 row f16((x · inverse) · f16 w) — the bits gh_rmsnorm_x stores — goes to LDS,
+            // from which x is staged.
             uint2* xn = (uint2*)(lds + (MODE == kModeMixed ? 18 : 9) * units);
             float* red = (float*)(xn + n4);
-            float4 v[kMaxChunks];
-            uint2 wv[kMaxChunks];
-#pragma unroll
-            for (uint32_t k = 0; k < kMaxChunks; ++k) {
-                const uint32_t i = min(threadIdx.x + 256 * k, n4 - 1);
-                v[k] = xr[i];
-                wv[k] = wn[i];
-            }
+            if (t || !PRIME) load_norm_row(t);
             float ss = 0.0f;
 #pragma unroll
             for (uint32_t k = 0; k < kMaxChunks; ++k)
                 if (threadIdx.x + 256 * k < n4) ss = gh_rms_add(ss, v[k]);
+            load_norm_w();
             const float inv = gh_rms_finish_256(ss, h.in_dim, a.eps, red);
 #pragma unroll
             for (uint32_t k = 0; k < kMaxChunks; ++k) {
