@@ -34,10 +34,6 @@ constexpr uint32_t kQ4K = 12, kQ6K = 14;
 constexpr int BK = 64;        // k per stage: one 64-weight unit
 constexpr int LDK = BK + 8;   // LDS row pitch in FP16 (144 B: conflict-free 16-byte reads)
 
-__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
-    return (uint32_t)gh_f2h(a) | ((uint32_t)gh_f2h(b) << 16);
-}
-
 // k of FP16 chunk c (8 consecutive weights) of unit u, in LDS order.
 template <uint32_t FMT>
 __device__ __forceinline__ uint32_t chunk_k(uint32_t u, uint32_t c) {
@@ -91,39 +87,52 @@ __device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* 
         const float d = gh_h2f(ws.hd.x & 0xFFFFu), dmin = gh_h2f(ws.hd.x >> 16);
         const float d1 = d * (float)sc0, m1 = dmin * (float)mn0;
         const float d2 = d * (float)sc1, m2 = dmin * (float)mn1;
+        // nibbles four at a time: byte e of lo4 / hi4 is the low / high nibble of byte e
+        auto w2 = [](uint32_t q4, int e, float sc, float mn) __attribute__((always_inline)) {
+            typedef _Float16 hv2 __attribute__((ext_vector_type(2)));
+            const float f0 = (float)((q4 >> (8 * e)) & 0xFFu), f1 = (float)((q4 >> (8 * e + 8)) & 0xFFu);
+            const hv2 r = {(_Float16)(sc * f0 - mn), (_Float16)(sc * f1 - mn)};  // mul, then sub
+            return __builtin_bit_cast(uint32_t, r);
+        };
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; e += 2) {
-                const uint32_t b0 = (qw[j] >> (8 * e)) & 0xFFu, b1 = (qw[j] >> (8 * e + 8)) & 0xFFu;
-                lo[2 * j + e / 2] = pack_h2(d1 * (float)(b0 & 0xFu) - m1, d1 * (float)(b1 & 0xFu) - m1);
-                hi[2 * j + e / 2] = pack_h2(d2 * (float)(b0 >> 4) - m2, d2 * (float)(b1 >> 4) - m2);
-            }
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t lo4 = qw[j] & 0x0F0F0F0Fu, hi4 = (qw[j] >> 4) & 0x0F0F0F0Fu;
+            lo[2 * j] = w2(lo4, 0, d1, m1);
+            lo[2 * j + 1] = w2(lo4, 2, d1, m1);
+            hi[2 * j] = w2(hi4, 0, d2, m2);
+            hi[2 * j + 1] = w2(hi4, 2, d2, m2);
+        }
     } else {
         // part 0: ql plane a -> quarters 0 (low nibble, qh bits 0-1) and 2 (high, bits 4-5);
         // part 1: plane b -> quarters 1 (bits 2-3) and 3 (bits 6-7). Scale of quarter q:
-        // int8 scales[8s + h + 2q].
+        // int8 scales[8s + h + 2q]. Four quants per dword: the nibble and the two high bits
+        // are combined byte-parallel into unsigned 6-bit values u, and each weight is
+        // (u - 32)·da = u·da + (-32·da) (the bias exact: a power-of-two multiple), one fused
+        // multiply-add rounded once to FP16.
         const uint32_t s = (u >> 1) & 1u, h = u & 1u;
         const uint32_t scw[4] = {ws.hd.x, ws.hd.y, ws.hd.z, ws.hd.w};
         const uint32_t ia = 8 * s + h + 2 * part, ib = ia + 4;
         const float d = gh_h2f(ws.d);
         const float da = d * (float)(int8_t)(scw[ia >> 2] >> (8 * (ia & 3u)));
         const float db = d * (float)(int8_t)(scw[ib >> 2] >> (8 * (ib & 3u)));
+        const float na = -32.0f * da, nb = -32.0f * db;
         const uint32_t qh[4] = {ws.qh.x, ws.qh.y, ws.qh.z, ws.qh.w};
         const uint32_t sl = 2 * part, sh = 4 + 2 * part;
+        auto w2 = [](uint32_t q4, int e, float sc, float bias) __attribute__((always_inline)) {
+            typedef _Float16 hv2 __attribute__((ext_vector_type(2)));
+            const float f0 = (float)((q4 >> (8 * e)) & 0xFFu), f1 = (float)((q4 >> (8 * e + 8)) & 0xFFu);
+            const hv2 r = {(_Float16)__builtin_fmaf(f0, sc, bias), (_Float16)__builtin_fmaf(f1, sc, bias)};
+            return __builtin_bit_cast(uint32_t, r);
+        };
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; e += 2) {
-                const uint32_t b0 = (qw[j] >> (8 * e)) & 0xFFu, b1 = (qw[j] >> (8 * e + 8)) & 0xFFu;
-                const uint32_t h0 = (qh[j] >> (8 * e)) & 0xFFu, h1 = (qh[j] >> (8 * e + 8)) & 0xFFu;
-                const int32_t qa0 = (int32_t)((b0 & 0xFu) | (((h0 >> sl) & 3u) << 4)) - 32;
-                const int32_t qa1 = (int32_t)((b1 & 0xFu) | (((h1 >> sl) & 3u) << 4)) - 32;
-                const int32_t qb0 = (int32_t)((b0 >> 4) | (((h0 >> sh) & 3u) << 4)) - 32;
-                const int32_t qb1 = (int32_t)((b1 >> 4) | (((h1 >> sh) & 3u) << 4)) - 32;
-                lo[2 * j + e / 2] = pack_h2(da * (float)qa0, da * (float)qa1);
-                hi[2 * j + e / 2] = pack_h2(db * (float)qb0, db * (float)qb1);
-            }
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t qa4 = (qw[j] & 0x0F0F0F0Fu) | (((qh[j] >> sl) & 0x03030303u) << 4);
+            const uint32_t qb4 = ((qw[j] >> 4) & 0x0F0F0F0Fu) | (((qh[j] >> sh) & 0x03030303u) << 4);
+            lo[2 * j] = w2(qa4, 0, da, na);
+            lo[2 * j + 1] = w2(qa4, 2, da, na);
+            hi[2 * j] = w2(qb4, 0, db, nb);
+            hi[2 * j + 1] = w2(qb4, 2, db, nb);
+        }
     }
     // low nibbles (quarter 2·part for Q6_K): positions 16·part + i; high: 32 + 16·part + i
     *(uint4*)(dst + 16 * part) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
