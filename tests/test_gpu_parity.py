@@ -138,7 +138,8 @@ def test_c2_block_projection_matmul_f16(hip, name, fmt, rows, in_dim):
                                               (F.FMT_Q6_K, 3, 14336),
                                               # direct kernel, several tasks per wave (2-4,
                                               # unequal): the next task is prefetched
-                                              (F.FMT_Q4_K, 20000, 4096), (F.FMT_Q6_K, 9001, 2048)])
+                                              (F.FMT_Q4_K, 20000, 4096), (F.FMT_Q6_K, 9001, 2048),
+                                              (F.FMT_Q4_K, 12287, 4096)])  # ragged last task
 def test_gemv_logits_shapes(hip, fmt, rows, in_dim):
     got, want, scale = _gemv(hip, fmt, rows, in_dim, 3 + rows, True)
     assert_close_terms(got, want, scale, what=f"{fmt} {rows}x{in_dim}")
