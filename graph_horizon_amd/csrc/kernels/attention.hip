@@ -419,7 +419,13 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
     __shared__ __attribute__((aligned(16))) _Float16 vt[2][128 * kVP];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t nqb = (a.rows + kPQ - 1) / kPQ;
-    const uint32_t qb = nqb - 1 - blockIdx.x, kvh = blockIdx.y, h = kvh * 4 + wave;
+    // Work order: L = 0 is the heaviest (latest) query block. Workgroup k of the first half of
+    // the grid takes L = k, workgroup k + T/2 takes L = T - 1 - k: with the grid dispatched
+    // round-robin over the CUs and two workgroups resident per CU, the pair that shares a CU
+    // carries one heavy and one light causal block instead of two equal ones.
+    const uint32_t T = nqb * a.kv_heads, k = blockIdx.x + nqb * blockIdx.y, half = (T + 1) / 2;
+    const uint32_t L = k < half ? k : T - 1 - (k - half);  // grid: (nqb, kv_heads)
+    const uint32_t qb = nqb - 1 - L / a.kv_heads, kvh = L % a.kv_heads, h = kvh * 4 + wave;
     const uint32_t q0 = qb * kPQ;
     const uint32_t kv_end = a.base + min(q0 + kPQ, a.rows);  // keys 0 .. kv_end-1 are visible
     const uint32_t ntiles = (kv_end + kPK - 1) / kPK;
