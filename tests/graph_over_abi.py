@@ -1,4 +1,4 @@
-"""forward::token restated in Python over the C ABI, op by op (test helper).
+"""forward::token and prefill::prefill restated in Python over the C ABI, op by op (test helper).
 
 This is the engine's own structure — the graph recorders generic over `Backend`
 (family/mistral/graph/forward.rs:68-83, block.rs:17-107, mlp.rs:12-61, tail.rs:22-59) —
@@ -66,6 +66,49 @@ class AbiGraph:
         h.rmsnorm_x(self.normed, self.x, self.w[(F.NO_LAYER, F.T_OUTPUT_NORM)], d, eps, 1)
         h.logits(self.logits, self.normed, self.w[(F.NO_LAYER, F.T_OUTPUT)], d, s.vocab_size)
         h.submit()
+        return h.read_logits(self.logits, s.vocab_size)
+
+    def prefill(self, toks, base):
+        """prefill::record_batch (graph/prefill/encode.rs:43-106, layer.rs:18-122) for one batch
+        of rows at positions base..: every trait op batched over the rows, the tail on the
+        last row. Returns the last row's logits."""
+        h, s = self.hip, self.shape
+        n = len(toks)
+        d, ffn = s.embedding_length, s.feed_forward_length
+        qw, kw = s.head_count * s.head_dim, s.kv_head_count * s.head_dim
+        eps = 1e-5
+        a = h.alloc_buffer
+        x, normed = a(n * d * 4), a(n * d * 2)
+        q, k, v, attn = a(n * qw * 2), a(n * kw * 2), a(n * kw * 2), a(n * qw * 2)
+        proj, gate, up, act, ffn_out = a(n * d * 2), a(n * ffn * 2), a(n * ffn * 2), a(n * ffn * 2), a(n * d * 2)
+        h.begin()
+        for r, tok in enumerate(toks):
+            h.embed(h.view(x, r * d * 4, d * 4), self.w[(F.NO_LAYER, F.T_TOKEN_EMBD)], int(tok), d)
+        for li in range(s.block_count):
+            w = lambda t: self.w[(li, t)]  # noqa: E731
+            h.rmsnorm_x(normed, x, w(F.T_ATTN_NORM), d, eps, n)
+            h.matmul_batched(q, normed, w(F.T_ATTN_Q), d, qw, n)
+            h.matmul_batched(k, normed, w(F.T_ATTN_K), d, kw, n)
+            h.matmul_batched(v, normed, w(F.T_ATTN_V), d, kw, n)
+            h.rope_yarn_batched(q, k, s.head_count, s.kv_head_count, s.head_dim, base, n, self.yarn)
+            off = ((li * self.kv_context + base) * kw) * 2
+            h.kv_write(self.kv, k, v, off, off, n * s.kv_head_count)
+            h.attention_prefill(attn, q, self.kv, s.head_count, base, n, li)
+            h.matmul_batched(proj, attn, w(F.T_ATTN_OUTPUT), qw, d, n)
+            h.residual_add(x, proj, n * d)
+            h.rmsnorm_x(normed, x, w(F.T_FFN_NORM), d, eps, n)
+            h.matmul_batched(gate, normed, w(F.T_FFN_GATE), d, ffn, n)
+            h.matmul_batched(up, normed, w(F.T_FFN_UP), d, ffn, n)
+            h.silu_mul(act, gate, up, n * ffn)
+            h.matmul_batched(ffn_out, act, w(F.T_FFN_DOWN), ffn, d, n)
+            h.residual_add(x, ffn_out, n * d)
+        last = h.view(x, (n - 1) * d * 4, d * 4)
+        h.rmsnorm_x(self.normed, last, self.w[(F.NO_LAYER, F.T_OUTPUT_NORM)], d, eps, 1)
+        h.logits(self.logits, self.normed, self.w[(F.NO_LAYER, F.T_OUTPUT)], d, s.vocab_size)
+        h.submit()
+        self.prefill_x = h.download(x, np.float32, n * d)
+        for b in (x, normed, q, k, v, attn, proj, gate, up, act, ffn_out):
+            h.free_buffer(b)
         return h.read_logits(self.logits, s.vocab_size)
 
     def read_x(self):

@@ -520,6 +520,36 @@ def test_fused_decode_is_bit_identical_to_op_by_op(hip, shape_name):
     gm.close()
 
 
+@pytest.mark.parametrize("n", [37, 300])
+def test_prefill_driver_is_bit_identical_to_op_by_op(hip, n):
+    """The driver's prefill (one batch: GEMV for n < 8 rows, the MFMA GEMMs above, the
+    warp-specialized ones from 256 rows) leaves the same logits and KV bits as recording every
+    trait op separately (prefill::record_batch over the C ABI)."""
+    from graph_horizon_amd import HipModel
+    from graph_over_abi import AbiGraph
+
+    shape = synth.SHAPES["tiny"]
+    ctx = 320
+    ref = AbiGraph(hip, shape, 43, ctx)
+    gm = HipModel(hip, synth.model_config(shape, ctx, 512))
+    for layer, tid, fmt, data in synth.model_tensors(shape, 43):
+        gm.load_tensor(layer, tid, fmt, data)
+    toks = [int(t) for t in np.random.default_rng(n).integers(0, shape.vocab_size, n)]
+    want = ref.prefill(toks, 0)
+    gm.prefill(toks, 0)
+    got = gm.read_logits()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    last_x = ref.prefill_x[(n - 1) * shape.embedding_length:]
+    assert np.array_equal(gm.read_x().view(np.uint32), last_x.view(np.uint32))
+    kv = gm.kv()
+    m = shape.block_count * ctx * shape.kv_head_count * shape.head_dim
+    for role in ("k", "v"):
+        a = hip.download(getattr(kv, role), np.uint16, m).reshape(shape.block_count, ctx, -1)
+        b = hip.download(getattr(ref.kv, role), np.uint16, m).reshape(shape.block_count, ctx, -1)
+        assert np.array_equal(a[:, :n], b[:, :n]), role
+    gm.close()
+
+
 # ---------------------------------------------------------------- generation loop (§ sampling)
 def _manual_generate(gm, prompt, p, max_tokens, context):
     """generation::drive restated over the driver's primitives with the oracle's sampling:
