@@ -513,6 +513,7 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     }
     a.x = x->addr;
     if (norm) {
+        if (n != 1) return fail(b, GH_E_INVALID, "gemv: fused norm is single-token");
         if (norm->format != GH_FMT_F16 || norm->bytes < (uint64_t)in_dim * 2 || in_dim % 8 || in_dim > kFusedNormMaxDim)
             return fail(b, GH_E_INVALID, "gemv: fused norm needs an F16[in_dim] weight and in_dim <= 5120");
         a.norm_w = norm->addr;

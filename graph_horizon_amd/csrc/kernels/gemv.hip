@@ -252,6 +252,54 @@ __device__ __forceinline__ void compute_regs(const uint4 (&xv)[8], const float4&
         }
 }
 
+// The Q4_K dot products of R rows against x paired in LDS (stage_x's layout), in two halves
+// of a unit's 32 quant bytes so only half the pairs (16 VGPRs) are live at once; the same
+// accumulation order as dot_q4.
+template <int R>
+__device__ __forceinline__ void compute_q4_halves(const uint4* xs, const float4* sums, uint32_t units,
+                                                  uint32_t u, const Masks& m, const WQ4 (&wr)[R],
+                                                  float (&acc)[R]) {
+    const float4 xq = sums[u];
+    const float s0 = xq.x + xq.y, s1 = xq.z + xq.w;
+    float slo[R], shi[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        slo[r] = -1024.0f * s0;
+        shi[r] = -1024.0f * s1;
+    }
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        __builtin_amdgcn_sched_barrier(0);  // one half's pairs live at a time
+        const uint4 l02 = xs[hf * units + u], l13 = xs[(2 + hf) * units + u];
+        const uint4 h02 = xs[(4 + hf) * units + u], h13 = xs[(6 + hf) * units + u];
+        const uint32_t L02[4] = {l02.x, l02.y, l02.z, l02.w}, L13[4] = {l13.x, l13.y, l13.z, l13.w};
+        const uint32_t H02[4] = {h02.x, h02.y, h02.z, h02.w}, H13[4] = {h13.x, h13.y, h13.z, h13.w};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint4 q = hf ? wr[r].q1 : wr[r].q0;
+            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t v = qw[k], v8 = v >> 8;
+                slo[r] = gh_dot2(L02[k], (v & m.lo4) | m.bias, slo[r]);
+                slo[r] = gh_dot2(L13[k], (v8 & m.lo4) | m.bias, slo[r]);
+                shi[r] = gh_dot2(H02[k], (v & m.hi4) | m.bias, shi[r]);
+                shi[r] = gh_dot2(H13[k], (v8 & m.hi4) | m.bias, shi[r]);
+            }
+        }
+    }
+    const uint32_t g = u & 3u;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float d = gh_h2f(wr[r].hd.x & 0xFFFFu), dmin = gh_h2f(wr[r].hd.x >> 16);
+        uint32_t sc0, mn0, sc1, mn1;
+        gh_q4k_scale_min(wr[r].hd, 2 * g, sc0, mn0);
+        gh_q4k_scale_min(wr[r].hd, 2 * g + 1, sc1, mn1);
+        acc[r] += (d * (float)sc0) * slo[r] - (dmin * (float)mn0) * s0 +
+                  (d * (float)sc1 * 0.0625f) * shi[r] - (dmin * (float)mn1) * s1;
+    }
+}
+
 template <uint32_t FMT, int R, int M>
 __device__ __forceinline__ void compute_step(const uint4* xs, const float4* sums, uint32_t units,
                                              uint32_t u, const Masks& mk,
@@ -448,9 +496,10 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // PRIME: request the first step's weights before x is staged (their latency overlaps the
 // staging). With RMSNorm (NORM) the first token's x row is requested before them: the memory
 // counter is in order, so the staging waits only for its own loads. Off for the RMSNorm
-// two-matrix (SwiGLU) and mixed kernels: holding their primed rows next to the staging raises the
-// SwiGLU kernel to 193 VGPRs (two waves per SIMD instead of three; measured 546 vs 560 tok/s
-// on the 8B decode) and spills in the mixed kernel.
+// two-matrix (SwiGLU) and mixed kernels: holding their primed rows next to the staging takes
+// them from 127 / 114 to 134 / 130 VGPRs (three waves per SIMD instead of four; measured 555 vs
+// 580 tok/s on the 8B decode). A one-dword-per-load L2 warm-up of the first task before the
+// norm, in place of priming, measured 539 tok/s.
 template <int R, int MODE, bool NORM, bool PRIME = (!NORM || (MODE != kModeSwiglu && MODE != kModeMixed))>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     extern __shared__ uint4 lds[];
@@ -515,7 +564,10 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
         if constexpr (M == 2) w[1] = (const uint8_t*)a.aux;
         load_step<F0, R, M>(w, sg.rows, nb, first * R, min(threadIdx.x & 63u, units - 1), w0r);
     }
-    for (uint32_t t = 0; t < a.n; ++t) {
+    // the RMSNorm kernels are single-token (the host rejects n > 1): a constant trip count
+    // keeps the first token's x row from being carried across the loop into the dot products
+    const uint32_t n_tok = NORM ? 1u : a.n;
+    for (uint32_t t = 0; t < n_tok; ++t) {
         if (t) __syncthreads();
         auto stage = [&](const auto& x8) {
             if constexpr (MODE == kModeQ6) {
@@ -576,14 +628,18 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
 }
 
 // Single-token launch of one Q4_K or Q6_K matrix with in_dim <= 4096 (one unit per lane).
-// The workgroup stages x once in LDS (two 16-byte pieces per thread, requested before the
-// first task's weights; only an LDS fence and s_barrier separate the staging from its reads,
-// so the weight loads stay in flight across it); each wave then pairs its lanes' x slices in
-// registers and runs its tasks without further barriers. x fetched per wave instead (8 KiB
-// each, 16 waves per CU) measured ~1.5 us of a 10 us 12288x4096 launch.
+// The workgroup stages x once in LDS as FP16 pairs (each thread pairs 16 values it requested
+// before the first task's weights; only an LDS fence and s_barrier separate the staging from
+// its reads, so the weight loads stay in flight across it); each task reads its pairs from LDS
+// again, half a unit at a time, so no x is held in registers between tasks. That keeps the
+// two-row Q4_K kernel at 69 VGPRs: seven waves per SIMD, 7,168 resident waves, so the 6,144
+// tasks of a 12288x4096 launch run in one round (pairs held per wave: 104 VGPRs, four waves
+// per SIMD, one and a half rounds; 7.7 -> 7.3 us). x fetched per wave instead of staged
+// (8 KiB each, 16 waves per CU) measured ~1.5 us of a 10 us 12288x4096 launch.
 template <int R, uint32_t FMT>
 __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h) {
-    __shared__ uint4 xs[512];  // x: in_dim <= 4096 FP16
+    __shared__ uint4 xs[512];     // x as FP16 pairs, stage_x's layout (in_dim <= 4096)
+    __shared__ float4 sums[64];
     const uint32_t lane = threadIdx.x & 63u, nb = h.in_dim >> 8, units = nb * 4;
     const uint32_t waves = h.groups * 4;  // 256-thread workgroups
     const uint32_t gw = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -593,8 +649,11 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h)
     const uint32_t u = min(lane, units - 1);
     const uint8_t* w[1] = {(const uint8_t*)sg.w};
     const GH_GLOBAL uint4* xh = gh_gp<uint4>(h.x);
-    const uint32_t nx = h.in_dim >> 3, t = threadIdx.x;
-    const uint4 x0 = xh[min(t, nx - 1)], x1 = xh[min(t + 256, nx - 1)];
+    // thread t pairs item t = (unit t/4, quarter t%4): 16 FP16 values, two 16-byte loads
+    const uint32_t t = threadIdx.x, it = min(t, units * 4 - 1), iu = it >> 2, iq = it & 3u;
+    const uint32_t e = FMT == kQ4K ? 16 * it
+                                   : (iu >> 2) * 256 + ((iu >> 1) & 1u) * 128 + iq * 32 + (iu & 1u) * 16;
+    const uint4 x0 = xh[e >> 3], x1 = xh[(e >> 3) + 1];
     __builtin_amdgcn_sched_barrier(0);
     // waves past the last task (the grid has at most three, all in the last workgroup) load
     // the last task's rows, take part in the barrier, and leave
@@ -605,17 +664,24 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h)
     const uint32_t pos = epi_needs_pos(sg.epi) ? position(a) : 0u;
     EpiIn<R> ei;
     epi_load<R, false>(a, sg, 0, t0 * R, pos, ei);
-    if (t < nx) xs[t] = x0;
-    if (t + 256 < nx) xs[t + 256] = x1;
+    if (t < units * 4) {
+        uint4 p02, p13;
+        float sq;
+        pair16(x0, x1, p02, p13, sq);
+        if constexpr (FMT == kQ4K) {
+            const uint32_t k0 = (iq & 1u) + 4 * (iq >> 1);
+            xs[k0 * units + iu] = p02;
+            xs[(k0 + 2) * units + iu] = p13;
+        } else {
+            xs[iq * units + iu] = p02;
+            xs[(4 + iq) * units + iu] = p13;
+        }
+        ((float*)&sums[iu])[iq] = sq;
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     if (gw >= h.tasks) return;  // wave-uniform
-    uint4 xraw[8];
-    load_unit_x<FMT>([&](uint32_t e) { return xs[e >> 3]; }, u, xraw);
-    uint4 xv[8];
-    float4 xsum;
-    pair_raw<FMT>(xraw, xv, xsum);
     const Masks mk = make_masks();
     for (uint32_t k = gw; k < h.tasks; k += waves) {
         if (k != gw) {
@@ -625,7 +691,15 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h)
         float acc[1][R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[0][r] = 0.0f;
-        if (lane < units) compute_regs<FMT, R, 1>(xv, xsum, u, mk, wr, acc);
+        if (lane < units) {
+            // opaque per task: keeps the pair reads inside the loop (not hoisted and held)
+            uint32_t ut = u;
+            asm volatile("" : "+v"(ut));
+            if constexpr (FMT == kQ4K)
+                compute_q4_halves<R>(xs, sums, units, ut, mk, wr[0], acc[0]);
+            else
+                compute_step<FMT, R, 1>(xs, sums, units, u, mk, wr, acc);
+        }
         float v[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) v[r] = gh_wave_sum63(acc[0][r]);

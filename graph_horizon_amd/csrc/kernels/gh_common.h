@@ -100,17 +100,16 @@ __device__ __forceinline__ uint32_t gh_byte(const uint4& v, uint32_t i) {
 
 // get_scale_min_k4 on the 12 scale bytes held in bytes 4..15 of the Q4_K header chunk
 // (backend/cpu/dequant.rs:78-89): 6-bit (sc, mn) of sub-block j.
+// Branch-free (j differs across the lanes of a wave): the scale bytes sit in hd.y (scales[0..3]),
+// hd.z ([4..7]) and hd.w ([8..11]); sub-block j and j + 4 use byte j & 3 of each word, so three
+// shifts by 8·(j & 3) serve both forms and a mask selects one.
 __device__ __forceinline__ void gh_q4k_scale_min(const uint4& hd, uint32_t j, uint32_t& sc,
                                                  uint32_t& mn) {
-    if (j < 4) {
-        sc = gh_byte(hd, 4 + j) & 63u;
-        mn = gh_byte(hd, 8 + j) & 63u;
-    } else {
-        uint32_t hi = gh_byte(hd, 8 + j);
-        uint32_t lo = gh_byte(hd, j);
-        sc = (hi & 0xFu) | ((lo >> 6) << 4);
-        mn = (hi >> 4) | ((gh_byte(hd, 4 + j) >> 6) << 4);
-    }
+    const uint32_t sh = (j & 3u) * 8u;
+    const uint32_t ys = hd.y >> sh, zs = hd.z >> sh, ws = hd.w >> sh;
+    const uint32_t hi = 0u - ((j >> 2) & 1u);  // all ones for j >= 4
+    sc = ((ys & 63u) & ~hi) | (((ws & 15u) | ((ys >> 2) & 48u)) & hi);
+    mn = ((zs & 63u) & ~hi) | ((((ws >> 4) & 15u) | ((zs >> 2) & 48u)) & hi);
 }
 
 #endif
