@@ -37,6 +37,8 @@ const KernelName kKernels[] = {
     {K_GEMV_Q4K_R4_D, "gh_gemv_q4k_r4_d"}, {K_GEMV_Q6K_R4_D, "gh_gemv_q6k_r4_d"},
     {K_GEMV_Q4K_R1_K, "gh_gemv_q4k_r1_k"}, {K_GEMV_Q4K_R2_K, "gh_gemv_q4k_r2_k"},
     {K_GEMV_Q6K_R1_K, "gh_gemv_q6k_r1_k"}, {K_GEMV_Q6K_R2_K, "gh_gemv_q6k_r2_k"},
+    {K_GEMV_Q4K_R2_K3, "gh_gemv_q4k_r2_k3"}, {K_GEMV_Q6K_R2_K3, "gh_gemv_q6k_r2_k3"},
+    {K_GEMV_Q4K_R4_K3, "gh_gemv_q4k_r4_k3"}, {K_GEMV_Q6K_R4_K3, "gh_gemv_q6k_r4_k3"},
     {K_RMSNORM, "gh_rmsnorm_x"},           {K_ROPE, "gh_rope"},
     {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
     {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
@@ -480,7 +482,22 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     static const bool no_splitk = std::getenv("GH_GEMV_NO_SPLITK") != nullptr;
     const bool splitk = !no_splitk && !norm && n == 1 && nseg == 1 && !swiglu && in_dim > 4096 &&
                         in_dim <= 16384;
-    if (splitk) {
+    // in_dim 12288 (192 units) splits over three waves, one unit per lane, four rows per task
+    // (the 8B FFN down: 1,024 tasks, one round at three waves per SIMD). Measured on the 8B
+    // decode: 607 tok/s, against 599 with two-row tasks and 596 with the four-wave kernels.
+    // GH_SPLITK_ROWS = 2 or 0 selects those for comparison.
+    static const uint32_t splitk_rows = [] {
+        const char* e = std::getenv("GH_SPLITK_ROWS");
+        const int v = e ? std::atoi(e) : 4;
+        return v == 4 ? 4u : v == 0 ? 0u : 2u;
+    }();
+    uint32_t block = 256;
+    if (splitk && splitk_rows && in_dim / 64 == 192 && r >= 2) {
+        const bool q4 = segs[0].w->format == GH_FMT_Q4_K;
+        r = splitk_rows;
+        k = r == 4 ? (q4 ? K_GEMV_Q4K_R4_K3 : K_GEMV_Q6K_R4_K3) : (q4 ? K_GEMV_Q4K_R2_K3 : K_GEMV_Q6K_R2_K3);
+        block = 192;
+    } else if (splitk) {
         switch (k) {
             case K_GEMV_Q4K_R1: k = K_GEMV_Q4K_R1_K; break;
             case K_GEMV_Q4K_R2: case K_GEMV_Q4K_R4: k = K_GEMV_Q4K_R2_K; r = 2; break;
@@ -540,13 +557,13 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
         return e ? (uint32_t)std::atoi(e) : 0u;
     }();
     if (direct || splitk) shmem = 0;
-    const uint32_t cap = max_wg ? max_wg : resident_wgs(b, k, 256, shmem);
+    const uint32_t cap = max_wg ? max_wg : resident_wgs(b, k, block, shmem);
     // split-K: one task per workgroup (four waves share it); otherwise one per wave
     const uint32_t want = splitk ? task : ceil_div(task, 4);
     a.groups = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
     // the kernels' leading scalar parameters (preloaded into SGPRs), then the full arguments
     void* params[] = {&a.x, &a.seg[0].w, &a.norm_w, &a.in_dim, &a.seg[0].rows, &a.tasks, &a.groups, &a};
-    return hip_check(b, hipModuleLaunchKernel(b->fn[k], a.groups, 1, 1, 256, 1, 1, shmem, b->stream, params, nullptr),
+    return hip_check(b, hipModuleLaunchKernel(b->fn[k], a.groups, 1, 1, block, 1, 1, shmem, b->stream, params, nullptr),
                      "hipModuleLaunchKernel");
 }
 

@@ -45,6 +45,11 @@ enum GhKernel : int {
     K_GEMV_Q4K_R2_K,
     K_GEMV_Q6K_R1_K,
     K_GEMV_Q6K_R2_K,
+    // three-wave split-K (in_dim 12288 = 192 units: one unit per lane)
+    K_GEMV_Q4K_R2_K3,
+    K_GEMV_Q6K_R2_K3,
+    K_GEMV_Q4K_R4_K3,
+    K_GEMV_Q6K_R4_K3,
     K_RMSNORM,
     K_ROPE,
     K_SILU_MUL,

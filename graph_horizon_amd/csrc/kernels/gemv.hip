@@ -496,10 +496,10 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // PRIME: request the first step's weights before x is staged (their latency overlaps the
 // staging). With RMSNorm (NORM) the first token's x row is requested before them: the memory
 // counter is in order, so the staging waits only for its own loads. Off for the RMSNorm
-// two-matrix (SwiGLU) and mixed kernels: holding their primed rows next to the staging takes
-// them from 127 / 114 to 134 / 130 VGPRs (three waves per SIMD instead of four; measured 555 vs
-// 580 tok/s on the 8B decode). A one-dword-per-load L2 warm-up of the first task before the
-// norm, in place of priming, measured 539 tok/s.
+// two-matrix (SwiGLU) and mixed kernels, where it measured slower on the 8B decode: primed,
+// they take 118 / 126 VGPRs (still four waves per SIMD) and the decode ran 567-576 tok/s
+// against 589-592 unprimed. A one-dword-per-load L2 warm-up of the first task before the norm,
+// in place of priming, was slower still.
 template <int R, int MODE, bool NORM, bool PRIME = (!NORM || (MODE != kModeSwiglu && MODE != kModeMixed))>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     extern __shared__ uint4 lds[];
@@ -707,16 +707,17 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h)
     }
 }
 
-// Single-token launch of one matrix with 4096 < in_dim <= 16384: the four waves of a
-// workgroup split the in-dimension into quarters (wave w: units w·q .. w·q + q, one per lane,
-// q = ceil(units / 4)), each pairs its lanes' x slices in registers once, and every task's
-// loads go out from all four waves at once — one memory round trip per task instead of one
-// per 64-unit chunk. The four partial sums of a row are added in wave order through LDS.
-template <int R, uint32_t FMT>
+// Single-token launch of one matrix with 4096 < in_dim <= 16384: the NW waves of a
+// workgroup (64·NW threads) split the in-dimension (wave w: units w·q .. w·q + q, one per lane,
+// q = ceil(units / NW)), each pairs its lanes' x slices in registers once, and every task's
+// loads go out from all NW waves at once — one memory round trip per task instead of one
+// per 64-unit chunk. The NW partial sums of a row are added in wave order through LDS.
+// NW = 3 for in_dim 12288 (192 units: every lane busy), 4 otherwise.
+template <int R, uint32_t FMT, int NW = 4>
 __device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a, const GhHot& h) {
-    __shared__ float part[4][R];
+    __shared__ float part[NW][R];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nb = h.in_dim >> 8;
-    const uint32_t units = nb * 4, q = (units + 3) / 4;
+    const uint32_t units = nb * 4, q = (units + NW - 1) / NW;
     const uint32_t uw = wave * q + lane;                    // this lane's unit
     const bool active = lane < q && uw < units;
     const uint32_t u = min(uw, units - 1);
@@ -757,7 +758,11 @@ __device__ __forceinline__ void gemv_splitk(const GhGemvArgs& a, const GhHot& h)
         if (threadIdx.x == 0) {
             float v[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) v[r] = ((part[0][r] + part[1][r]) + part[2][r]) + part[3][r];
+            for (int r = 0; r < R; ++r) {
+                v[r] = part[0][r];
+#pragma unroll
+                for (int i = 1; i < NW; ++i) v[r] += part[i][r];
+            }
             epilogue<R, false>(a, sg, 0, k * R, v, nullptr, pos, ei);
         }
         __syncthreads();
@@ -802,4 +807,8 @@ GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_k(GH_HOT_PARAMS) { gemv_spl
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_k(GH_HOT_PARAMS) { gemv_splitk<2, kQ4K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_k(GH_HOT_PARAMS) { gemv_splitk<1, kQ6K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_k(GH_HOT_PARAMS) { gemv_splitk<2, kQ6K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(192) void gh_gemv_q4k_r2_k3(GH_HOT_PARAMS) { gemv_splitk<2, kQ4K, 3>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(192) void gh_gemv_q6k_r2_k3(GH_HOT_PARAMS) { gemv_splitk<2, kQ6K, 3>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(192) void gh_gemv_q4k_r4_k3(GH_HOT_PARAMS) { gemv_splitk<4, kQ4K, 3>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(192) void gh_gemv_q6k_r4_k3(GH_HOT_PARAMS) { gemv_splitk<4, kQ6K, 3>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4(GH_HOT_PARAMS) { gemv_body<4, kModeQ6, false>(a, GH_HOT); }
