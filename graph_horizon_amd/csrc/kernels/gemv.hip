@@ -786,9 +786,9 @@ GH_GEMV(gh_gemv_q4k_r2, 2, kModeQ4)
 GH_GEMV(gh_gemv_q6k_r1, 1, kModeQ6)
 GH_GEMV(gh_gemv_q6k_r2, 2, kModeQ6)
 GH_KERNEL __launch_bounds__(256) void gh_gemv_mixed_r2(GH_HOT_PARAMS) { gemv_body<2, kModeMixed, false>(a, GH_HOT); }
-// The RMSNorm mixed (Q/K/V) kernel is held to 168 VGPRs, three waves per SIMD: with 3 x 256
-// CUs x 4 waves resident, an 8B-shaped QKV launch (4096 + 1024 + 1024 rows, R = 2) is one task
-// per wave instead of two rounds.
+// The RMSNorm mixed (Q/K/V) kernel runs at least three waves per SIMD (it needs 106 VGPRs, so
+// four): with 3 x 256 CUs x 4 waves resident, an 8B-shaped QKV launch (4096 + 1024 + 1024 rows,
+// R = 2) is one task per wave instead of two rounds.
 GH_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gh_gemv_mixed_r2_n(GH_HOT_PARAMS) {
     gemv_body<2, kModeMixed, true>(a, GH_HOT);
 }
