@@ -129,6 +129,16 @@ __device__ __forceinline__ void stage_x(const X8& x8, uint32_t units, uint4* xs,
     }
 }
 
+// Weights are streamed once per token: nontemporal loads (the `nt` bit: streaming, not kept
+// in the caches) measured 606 -> 629 tok/s on the 8B decode, 7.31 -> 7.2 us at 12288x4096.
+// (The same hint on the prefill GEMM's weights, which two token tiles share, and on the decode
+// attention's K/V measured slower: 83 -> 105 us on the 512-token gate, 12.9 -> 14.3 us at ctx 4096.)
+__device__ __forceinline__ uint4 gh_ld_nt(uint64_t a) {
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    const u4v v = __builtin_nontemporal_load((const GH_GLOBAL u4v*)a);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 struct WQ4 {
     uint4 q0, q1, hd;
 };
@@ -136,10 +146,9 @@ struct WQ4 {
 __device__ __forceinline__ void load_w_q4(const uint8_t* w, uint32_t rows, uint32_t nb,
                                           uint32_t row, uint32_t u, WQ4& o) {
     const uint8_t* rq = w + (size_t)row * GH_Q4K_QS_BYTES * nb + (size_t)u * 16;
-    o.q0 = *gh_gp<uint4>((uint64_t)rq);
-    o.q1 = *gh_gp<uint4>((uint64_t)(rq + (size_t)nb * 64));
-    o.hd = *gh_gp<uint4>((uint64_t)(w + (size_t)rows * GH_Q4K_QS_BYTES * nb +
-                                    ((size_t)row * nb + (u >> 2)) * 16));
+    o.q0 = gh_ld_nt((uint64_t)rq);
+    o.q1 = gh_ld_nt((uint64_t)(rq + (size_t)nb * 64));
+    o.hd = gh_ld_nt((uint64_t)(w + (size_t)rows * GH_Q4K_QS_BYTES * nb + ((size_t)row * nb + (u >> 2)) * 16));
 }
 
 // One Q4_K unit: the 32 qs bytes of group g (sub-blocks 2g, 2g+1) against staged x.
@@ -177,12 +186,12 @@ __device__ __forceinline__ void load_w_q6(const uint8_t* w, uint32_t rows, uint3
                                           uint32_t row, uint32_t u, WQ6& o) {
     const uint8_t* rq = w + (size_t)row * GH_Q6K_QLH_BYTES * nb + (size_t)u * 16;
     const size_t plane = (size_t)nb * 64;
-    o.qa = *gh_gp<uint4>((uint64_t)rq);
-    o.qb = *gh_gp<uint4>((uint64_t)(rq + plane));
-    o.qh = *gh_gp<uint4>((uint64_t)(rq + 2 * plane));
+    o.qa = gh_ld_nt((uint64_t)rq);
+    o.qb = gh_ld_nt((uint64_t)(rq + plane));
+    o.qh = gh_ld_nt((uint64_t)(rq + 2 * plane));
     const size_t blk = (size_t)row * nb + (u >> 2);
-    o.sc = *gh_gp<uint4>((uint64_t)(w + (size_t)rows * GH_Q6K_QLH_BYTES * nb + blk * 16));
-    o.d = *gh_gp<uint16_t>((uint64_t)(w + (size_t)rows * 208 * nb + blk * 2));
+    o.sc = gh_ld_nt((uint64_t)(w + (size_t)rows * GH_Q6K_QLH_BYTES * nb + blk * 16));
+    o.d = __builtin_nontemporal_load(gh_gp<uint16_t>((uint64_t)(w + (size_t)rows * 208 * nb + blk * 2)));
 }
 
 // One Q6_K unit (segment s, half h of block b): 16 weights of each quarter.
