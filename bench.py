@@ -233,7 +233,7 @@ def main():
 # rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --traffic-probe`, each scaled by
 # the same counter's reading for a 256 MiB device-to-device copy (FETCH_SIZE x 2.0, WRITE_SIZE
 # x 1.0): profiles/q4k_gemv_12288x4096.txt. Re-measure whenever the kernel changes.
-ROOFLINE_TRAFFIC_BYTES = 28512277
+ROOFLINE_TRAFFIC_BYTES = 28512941
 
 
 def traffic_probe(shape):
