@@ -256,9 +256,10 @@ int op_kv_write(gh_backend* b, const gh_kv* kv, const gh_buf* k, const gh_buf* v
     return launch(b, K_KV_WRITE, ceil_div(std::max(a.k_count, a.v_count), 256), 1, 1, 256, &a);
 }
 
-// Workgroups per (row, kv head): one per 64-position chunk up to 32; longer contexts loop.
 // Workgroups per (row, kv head): enough that rows x kv heads x splits covers about two
-// workgroups per CU, at most one per 64-position chunk and at most 32 (the merge's limit).
+// workgroups per CU, at most one per 64-position chunk and at most 32 (the merge's limit);
+// longer contexts loop over chunks. (Eight-wave workgroups over 128-position chunks measured
+// 35.5 vs 37.1 us at ctx 32768 but 613 vs 625 tok/s on the 8B decode: not kept.)
 uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows) {
     static const uint32_t forced = [] {
         const char* e = std::getenv("GH_ATTN_SPLITS");
