@@ -213,7 +213,7 @@ def main():
             "unit": "GB/s",
             "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
             "traffic": ROOFLINE_TRAFFIC_BYTES if (d, ffn) == (4096, 12288) else None,
-            "kernel": f"gh_gemv_q4k_r2_d (Q4_K GEMV {ffn}x{d}, {gemv_bytes} B/launch)",
+            "kernel": f"{gemv_kernel_name(d, ffn)} (Q4_K GEMV {ffn}x{d}, {gemv_bytes} B/launch)",
             "avg_us": round(gemv_ms * 1e3, 3),
         },
     }
@@ -229,11 +229,18 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-# HBM bytes per launch of the roofline kernel (gh_gemv_q4k_r2_d at 12288x4096), from the two
+def gemv_kernel_name(in_dim, rows):
+    """The kernel gh_matmul launches for one token (the host's selection in op_gemv)."""
+    if in_dim <= 4096:
+        return "gh_gemv_q4k_r1_d" if rows >= 8192 else "gh_gemv_q4k_r2_d"
+    return "gh_gemv_q4k_r2_k"
+
+
+# HBM bytes per launch of the roofline kernel (gh_gemv_q4k_r1_d at 12288x4096), from the two
 # rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --traffic-probe`, each scaled by
 # the same counter's reading for a 256 MiB device-to-device copy (FETCH_SIZE x 2.0, WRITE_SIZE
 # x 1.0): profiles/q4k_gemv_12288x4096.txt. Re-measure whenever the kernel changes.
-ROOFLINE_TRAFFIC_BYTES = 28512941
+ROOFLINE_TRAFFIC_BYTES = 28531416
 
 
 def traffic_probe(shape):

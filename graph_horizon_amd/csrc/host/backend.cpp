@@ -469,6 +469,14 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     }
     static const bool no_direct = std::getenv("GH_GEMV_NO_DIRECT") != nullptr;
     const bool direct = !no_direct && !norm && n == 1 && nseg == 1 && !swiglu && in_dim <= 4096;
+    // direct launches of 8192 rows or more take one-row tasks (more waves in flight: 12288x4096
+    // Q4_K measured 6.84 us against 7.21 us with two-row tasks; 4096x4096 stays at two rows,
+    // 3.94 us against 4.06 us)
+    static const bool direct_r2 = std::getenv("GH_DIRECT_R2") != nullptr;  // for comparison
+    if (direct && !direct_r2 && total_rows >= 8192 && (k == K_GEMV_Q4K_R2 || k == K_GEMV_Q6K_R2)) {
+        k = k == K_GEMV_Q4K_R2 ? K_GEMV_Q4K_R1 : K_GEMV_Q6K_R1;
+        r = 1;
+    }
     if (direct) {
         switch (k) {
             case K_GEMV_Q4K_R1: k = K_GEMV_Q4K_R1_D; break;
