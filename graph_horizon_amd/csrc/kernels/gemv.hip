@@ -507,8 +507,9 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // counter is in order, so the staging waits only for its own loads. Off for the RMSNorm
 // two-matrix (SwiGLU) and mixed kernels, where it measured slower on the 8B decode: primed,
 // they take 118 / 126 VGPRs (still four waves per SIMD) and the decode ran 567-576 tok/s
-// against 589-592 unprimed. A one-dword-per-load L2 warm-up of the first task before the norm,
-// in place of priming, was slower still.
+// against 589-592 unprimed (with the norm weights also requested up front: 605 against 628).
+// A one-dword-per-load L2 warm-up of the first task before the norm, in place of priming, was
+// slower still. For the output GEMV (Q6_K, primed) priming measured neutral.
 template <int R, int MODE, bool NORM, bool PRIME = (!NORM || (MODE != kModeSwiglu && MODE != kModeMixed))>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     extern __shared__ uint4 lds[];
