@@ -503,14 +503,12 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // Waves are split between the segments in proportion to their tasks (args: seg.task0 is the
 // first task index, the wave split is recomputed here), so a wave only ever runs one format.
 // PRIME: request the first step's weights before x is staged (their latency overlaps the
-// staging). With RMSNorm (NORM) the first token's x row is requested before them: the memory
-// counter is in order, so the staging waits only for its own loads. Off for the RMSNorm
-// two-matrix (SwiGLU) and mixed kernels, where it measured slower on the 8B decode: primed,
-// they take 118 / 126 VGPRs (still four waves per SIMD) and the decode ran 567-576 tok/s
-// against 589-592 unprimed (with the norm weights also requested up front: 605 against 628).
-// A one-dword-per-load L2 warm-up of the first task before the norm, in place of priming, was
-// slower still. For the output GEMV (Q6_K, primed) priming measured neutral.
-template <int R, int MODE, bool NORM, bool PRIME = (!NORM || (MODE != kModeSwiglu && MODE != kModeMixed))>
+// staging); the kernels without RMSNorm do. Off for the RMSNorm kernels, where requesting the
+// weights ahead of the norm's loads measured slower: primed, the SwiGLU and QKV kernels ran the
+// 8B decode at 567-576 tok/s against 589-592 (605 against 628 with the norm weights also
+// requested up front), and an L2 warm-up of the first task (one dword per load) in place of
+// priming was slower still; for the output GEMV priming measured neutral.
+template <int R, int MODE, bool NORM, bool PRIME = !NORM>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     extern __shared__ uint4 lds[];
     constexpr int M = MODE == kModeSwiglu ? 2 : 1;
@@ -546,21 +544,28 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     // staged, so their latency overlaps the staging.
     constexpr uint32_t F0 = MODE == kModeQ6 ? kQ6K : kQ4K;
     // NORM: the first token's FP32 x row and the norm weights (each thread: chunks tid + 256 k)
-    constexpr uint32_t kMaxChunks = 5;  // in_dim <= 5120
-    const uint32_t n4 = h.in_dim >> 2;
-    float4 v[kMaxChunks];
-    uint2 wv[kMaxChunks];
+    // NORM: each thread owns the 16-value items j = tid, tid + 256 of the FP32 x row (item j:
+    // float4 chunks 4j .. 4j + 3), the order gh_rms_inverse_256 reduces them in; in_dim <= 5120
+    // is at most 320 items
+    constexpr uint32_t kItems = 2;
+    const uint32_t n4 = h.in_dim >> 2, n16 = h.in_dim >> 4;
+    float4 v[kItems][4];
+    uint4 wv[kItems][2];
     auto load_norm_row = [&](uint32_t t) __attribute__((always_inline)) {
         const GH_GLOBAL float4* xr = gh_gp<float4>(h.x + (uint64_t)t * h.in_dim * 4);
 #pragma unroll
-        for (uint32_t k = 0; k < kMaxChunks; ++k) v[k] = xr[min(threadIdx.x + 256 * k, n4 - 1)];
+        for (uint32_t it = 0; it < kItems; ++it)
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) v[it][q] = xr[min(4 * (threadIdx.x + 256 * it) + q, n4 - 1)];
     };
     // the norm weights are requested after Σx²'s partial (they are first used after the
     // reduction), so they are not held in registers next to the primed weights
     auto load_norm_w = [&]() __attribute__((always_inline)) {
-        const GH_GLOBAL uint2* wn = gh_gp<uint2>(h.nw);
+        const GH_GLOBAL uint4* wn = gh_gp<uint4>(h.nw);
 #pragma unroll
-        for (uint32_t k = 0; k < kMaxChunks; ++k) wv[k] = wn[min(threadIdx.x + 256 * k, n4 - 1)];
+        for (uint32_t it = 0; it < kItems; ++it)
+#pragma unroll
+            for (uint32_t q = 0; q < 2; ++q) wv[it][q] = wn[min(2 * (threadIdx.x + 256 * it) + q, n4 / 2 - 1)];
     };
     if constexpr (NORM && PRIME) {
         load_norm_row(0);
@@ -588,35 +593,55 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
             }
         };
         if constexpr (NORM) {
-            // rmsnorm_x fused: x is the FP32 residual row. Each thread loads its float4 chunks
-            // (tid + 256 k) and their norm weights once (token 0's before the primed weights),
-            // the row's Σx² is reduced in the order of gh_rms_inverse_256, and the normalized
-            // FP16 row f16((x · inverse) · f16 w) — the bits gh_rmsnorm_x stores — goes to LDS,
-            // from which x is staged.
-            uint2* xn = (uint2*)(lds + (MODE == kModeMixed ? 18 : 9) * units);
-            float* red = (float*)(xn + n4);
+            // rmsnorm_x fused: x is the FP32 residual row. Each thread loads its items (16
+            // consecutive values) and their norm weights once, the row's Σx² is reduced in the
+            // order of gh_rms_inverse_256 (one barrier), and each
+            // item's normalized FP16 values f16((x · inverse) · f16 w) — the bits gh_rmsnorm_x
+            // stores — are paired in registers and staged straight into the unit layouts.
+            float* red = (float*)(lds + (MODE == kModeMixed ? 18 : 9) * units);
             if (t || !PRIME) load_norm_row(t);
             float ss = 0.0f;
 #pragma unroll
-            for (uint32_t k = 0; k < kMaxChunks; ++k)
-                if (threadIdx.x + 256 * k < n4) ss = gh_rms_add(ss, v[k]);
+            for (uint32_t it = 0; it < kItems; ++it)
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q)
+                    if (4 * (threadIdx.x + 256 * it) + q < n4) ss = gh_rms_add(ss, v[it][q]);
             load_norm_w();
             const float inv = gh_rms_finish_256(ss, h.in_dim, a.eps, red);
 #pragma unroll
-            for (uint32_t k = 0; k < kMaxChunks; ++k) {
+            for (uint32_t it = 0; it < kItems; ++it) {
 #pragma clang fp contract(off)
-                const uint32_t i = threadIdx.x + 256 * k;
-                if (i < n4) {
+                const uint32_t j = threadIdx.x + 256 * it;
+                if (j < n16) {
                     auto n2 = [&](float a0, float a1, uint32_t wp) {
                         return (uint32_t)gh_f2h(a0 * inv * gh_h2f(wp & 0xFFFFu)) |
                                ((uint32_t)gh_f2h(a1 * inv * gh_h2f(wp >> 16)) << 16);
                     };
-                    xn[i] = make_uint2(n2(v[k].x, v[k].y, wv[k].x), n2(v[k].z, v[k].w, wv[k].y));
+                    const float4* c = v[it];
+                    const uint4 lo = make_uint4(n2(c[0].x, c[0].y, wv[it][0].x), n2(c[0].z, c[0].w, wv[it][0].y),
+                                                n2(c[1].x, c[1].y, wv[it][0].z), n2(c[1].z, c[1].w, wv[it][0].w));
+                    const uint4 hi = make_uint4(n2(c[2].x, c[2].y, wv[it][1].x), n2(c[2].z, c[2].w, wv[it][1].y),
+                                                n2(c[3].x, c[3].y, wv[it][1].z), n2(c[3].z, c[3].w, wv[it][1].w));
+                    uint4 p02, p13;
+                    float sq;
+                    pair16(lo, hi, p02, p13, sq);
+                    if constexpr (MODE != kModeQ6) {  // Q4_K unit j / 4, quarter j % 4
+                        const uint32_t u = j >> 2, q = j & 3u, k0 = (q & 1u) + 4 * (q >> 1);
+                        xs4[k0 * units + u] = p02;
+                        xs4[(k0 + 2) * units + u] = p13;
+                        ((float*)&xsum4[u])[q] = sq;
+                    }
+                    if constexpr (MODE == kModeQ6 || MODE == kModeMixed) {
+                        // Q6_K unit (block j / 16, segment, half) and quarter of the same values
+                        const uint32_t u = (j >> 4) * 4 + ((j >> 3) & 1u) * 2 + (j & 1u), q = (j >> 1) & 3u;
+                        uint4* x6 = MODE == kModeQ6 ? xs4 : xs6;
+                        float4* s6 = MODE == kModeQ6 ? xsum4 : xsum6;
+                        x6[q * units + u] = p02;
+                        x6[(4 + q) * units + u] = p13;
+                        ((float*)&s6[u])[q] = sq;
+                    }
                 }
             }
-            __syncthreads();
-            const uint4* xn4 = (const uint4*)xn;
-            stage([&](uint32_t e) { return xn4[e >> 3]; });
         } else {
             const GH_GLOBAL uint4* xh = gh_gp<uint4>(h.x + (uint64_t)t * h.in_dim * 2);
             stage([&](uint32_t e) { return xh[e >> 3]; });

@@ -85,10 +85,15 @@ __device__ __forceinline__ float gh_rms_finish_256(float s, uint32_t dim, float 
     return 1.0f / __builtin_sqrtf(sum / (float)dim + eps);
 }
 
+// Σx² order: thread t adds the float4 chunks of the 16-value items j = t, t + 256, ... (chunks
+// 4j .. 4j + 3 in turn), then the wave sums and the four waves' sums in order — the order the
+// fused RMSNorm GEMVs use, so both produce the same inverse.
 __device__ __forceinline__ float gh_rms_inverse_256(const __attribute__((address_space(1))) float4* x,
                                                    uint32_t dim, float eps, float* red) {
     float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < (dim >> 2); i += 256) s = gh_rms_add(s, x[i]);
+    const uint32_t n4 = dim >> 2;
+    for (uint32_t j = threadIdx.x; 4 * j < n4; j += 256)
+        for (uint32_t q = 0; q < 4 && 4 * j + q < n4; ++q) s = gh_rms_add(s, x[4 * j + q]);
     return gh_rms_finish_256(s, dim, eps, red);
 }
 
