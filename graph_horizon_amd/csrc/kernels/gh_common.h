@@ -97,12 +97,6 @@ __device__ __forceinline__ float gh_rms_inverse_256(const __attribute__((address
     return gh_rms_finish_256(s, dim, eps, red);
 }
 
-// Byte `i` (runtime, 0..15) of a 16-byte register block.
-__device__ __forceinline__ uint32_t gh_byte(const uint4& v, uint32_t i) {
-    uint32_t w = (i < 4) ? v.x : (i < 8) ? v.y : (i < 12) ? v.z : v.w;
-    return (w >> ((i & 3) * 8)) & 0xFFu;
-}
-
 // get_scale_min_k4 on the 12 scale bytes held in bytes 4..15 of the Q4_K header chunk
 // (backend/cpu/dequant.rs:78-89): 6-bit (sc, mn) of sub-block j.
 // Branch-free (j differs across the lanes of a wave): the scale bytes sit in hd.y (scales[0..3]),
