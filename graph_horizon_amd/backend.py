@@ -214,6 +214,10 @@ class HipBackend:
     def synchronize(self):
         self._ok(self.lib.gh_synchronize(self.h), "synchronize")
 
+    def set_attention_splits(self, splits: int):
+        """Decode attention workgroups per (row, kv head); 0 = the backend's policy."""
+        self._ok(self.lib.gh_set_attention_splits(self.h, splits), "set_attention_splits")
+
 
 class HipModel:
     """The C++ graph driver (gh_model_*): MistralGraph's decode and prefill over the backend."""

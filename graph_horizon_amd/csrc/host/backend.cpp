@@ -24,8 +24,7 @@ const KernelName kKernels[] = {
     {K_REPACK_Q4K, "gh_repack_q4k"},       {K_REPACK_Q6K, "gh_repack_q6k"},
     {K_DEQUANT_Q4K, "gh_dequant_q4k"},     {K_DEQUANT_Q6K, "gh_dequant_q6k"},
     {K_GEMV_Q4K_R1, "gh_gemv_q4k_r1"},     {K_GEMV_Q4K_R2, "gh_gemv_q4k_r2"},
-    {K_GEMV_Q4K_R4, "gh_gemv_q4k_r4"},     {K_GEMV_Q6K_R1, "gh_gemv_q6k_r1"},
-    {K_GEMV_Q6K_R2, "gh_gemv_q6k_r2"},     {K_GEMV_Q6K_R4, "gh_gemv_q6k_r4"},
+    {K_GEMV_Q6K_R1, "gh_gemv_q6k_r1"},     {K_GEMV_Q6K_R2, "gh_gemv_q6k_r2"},
     {K_GEMV_MIXED_R2, "gh_gemv_mixed_r2"}, {K_GEMV_SWIGLU_R1, "gh_gemv_swiglu_r1"},
     {K_GEMV_SWIGLU_R2, "gh_gemv_swiglu_r2"},
     {K_GEMV_Q4K_R1_N, "gh_gemv_q4k_r1_n"}, {K_GEMV_Q4K_R2_N, "gh_gemv_q4k_r2_n"},
@@ -34,10 +33,8 @@ const KernelName kKernels[] = {
     {K_GEMV_SWIGLU_R1_N, "gh_gemv_swiglu_r1_n"}, {K_GEMV_SWIGLU_R2_N, "gh_gemv_swiglu_r2_n"},
     {K_GEMV_Q4K_R1_D, "gh_gemv_q4k_r1_d"}, {K_GEMV_Q4K_R2_D, "gh_gemv_q4k_r2_d"},
     {K_GEMV_Q6K_R1_D, "gh_gemv_q6k_r1_d"}, {K_GEMV_Q6K_R2_D, "gh_gemv_q6k_r2_d"},
-    {K_GEMV_Q4K_R4_D, "gh_gemv_q4k_r4_d"}, {K_GEMV_Q6K_R4_D, "gh_gemv_q6k_r4_d"},
     {K_GEMV_Q4K_R1_K, "gh_gemv_q4k_r1_k"}, {K_GEMV_Q4K_R2_K, "gh_gemv_q4k_r2_k"},
     {K_GEMV_Q6K_R1_K, "gh_gemv_q6k_r1_k"}, {K_GEMV_Q6K_R2_K, "gh_gemv_q6k_r2_k"},
-    {K_GEMV_Q4K_R2_K3, "gh_gemv_q4k_r2_k3"}, {K_GEMV_Q6K_R2_K3, "gh_gemv_q6k_r2_k3"},
     {K_GEMV_Q4K_R4_K3, "gh_gemv_q4k_r4_k3"}, {K_GEMV_Q6K_R4_K3, "gh_gemv_q6k_r4_k3"},
     {K_RMSNORM, "gh_rmsnorm_x"},           {K_ROPE, "gh_rope"},
     {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
@@ -47,12 +44,8 @@ const KernelName kKernels[] = {
     {K_ATTN_G8, "gh_attn_g8"},
     {K_STEP_ADVANCE, "gh_step_advance"},
     {K_GEMM_Q4K_T128_R64, "gh_gemm_q4k_t128_r64"},   {K_GEMM_Q4K_T128_R128, "gh_gemm_q4k_t128_r128"},
-    {K_GEMM_Q4K_T256_R64, "gh_gemm_q4k_t256_r64"},   {K_GEMM_Q4K_T256_R96, "gh_gemm_q4k_t256_r96"},
-    {K_GEMM_Q4K_T256_R128, "gh_gemm_q4k_t256_r128"}, {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},
-    {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"}, {K_GEMM_Q6K_T256_R64, "gh_gemm_q6k_t256_r64"},
-    {K_GEMM_Q6K_T256_R96, "gh_gemm_q6k_t256_r96"},   {K_GEMM_Q6K_T256_R128, "gh_gemm_q6k_t256_r128"},
+    {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},   {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"},
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
-    {K_ATTN_PREFILL_G4_Q16, "gh_attn_prefill_g4_q16"},
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
@@ -192,13 +185,21 @@ bool yarn_valid(const gh_yarn* y) {
     return true;
 }
 
-int ensure_rope(gh_backend* b, const gh_yarn* y, uint32_t positions) {
-    GhRopeTable& t = b->rope;
+void free_rope(GhRopeTable& t) {
+    if (t.table) (void)hipFree(t.table);
+    if (t.post) (void)hipFree(t.post);
+    t.table = t.post = nullptr;
+    t.positions = 0;
+}
+
+int ensure_rope(gh_backend* b, GhRopeTable& t, const gh_yarn* y, uint32_t positions) {
+    if (positions > kMaxRopePositions)
+        return fail(b, GH_E_RANGE, "rope: position beyond the table limit (262144 positions)");
     bool same = t.table && std::memcmp(&t.yarn, y, sizeof(gh_yarn)) == 0;
     if (same && t.positions >= positions) return GH_OK;
     if (b->capturing) return fail(b, GH_E_STATE, "rope table growth during graph capture");
-    uint32_t n = std::max<uint32_t>(positions, 4096);
-    if (same) n = std::max(n, t.positions * 2);
+    uint32_t n = std::min(std::max<uint32_t>(positions, 4096), kMaxRopePositions);
+    if (same) n = std::min(std::max(n, t.positions * 2), kMaxRopePositions);
     const uint32_t pairs = y->rope_dim / 2;
     std::vector<float> table((size_t)n * pairs * 2), post(n);
     for (uint32_t p = 0; p < n; ++p) {
@@ -208,31 +209,31 @@ int ensure_rope(gh_backend* b, const gh_yarn* y, uint32_t positions) {
     }
     int rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
     if (rc) return rc;
-    if (t.table) (void)hipFree(t.table);
-    if (t.post) (void)hipFree(t.post);
-    t.table = t.post = nullptr;
-    t.positions = 0;
+    free_rope(t);
     rc = hip_check(b, hipMalloc(&t.table, table.size() * 4), "hipMalloc(rope)");
     if (!rc) rc = hip_check(b, hipMalloc(&t.post, post.size() * 4), "hipMalloc(rope)");
     if (!rc) rc = hip_check(b, hipMemcpy(t.table, table.data(), table.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(rope)");
     if (!rc) rc = hip_check(b, hipMemcpy(t.post, post.data(), post.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(rope)");
-    if (rc) return rc;
+    if (rc) {
+        free_rope(t);
+        return rc;
+    }
     t.yarn = *y;
     t.positions = n;
-    ++b->gen;
     return GH_OK;
 }
 
-int op_rope(gh_backend* b, const gh_buf* x, uint32_t heads, uint32_t head_dim, uint32_t base,
-            uint32_t rows, uint32_t role, const void* pos_ptr) {
+int op_rope(gh_backend* b, const GhRopeTable& t, const gh_buf* x, uint32_t heads,
+            uint32_t head_dim, uint32_t base, uint32_t rows, uint32_t role, const void* pos_ptr) {
+    if (!t.table) return fail(b, GH_E_STATE, "rope: table not built");
     GhRopeArgs a{};
     a.x = x->addr;
-    a.table = (uint64_t)b->rope.table;
-    a.post = role == GH_ROPE_QUERY ? (uint64_t)b->rope.post : 0;
+    a.table = (uint64_t)t.table;
+    a.post = role == GH_ROPE_QUERY ? (uint64_t)t.post : 0;
     a.pos_ptr = (uint64_t)pos_ptr;
     a.heads = heads;
     a.head_dim = head_dim;
-    a.pairs = b->rope.yarn.rope_dim / 2;
+    a.pairs = t.yarn.rope_dim / 2;
     a.base = base;
     a.rows = rows;
     uint64_t total = (uint64_t)rows * heads * a.pairs;
@@ -260,13 +261,11 @@ int op_kv_write(gh_backend* b, const gh_kv* kv, const gh_buf* k, const gh_buf* v
 // workgroups per CU, at most one per 64-position chunk and at most 32 (the merge's limit);
 // longer contexts loop over chunks. (Eight-wave workgroups over 128-position chunks measured
 // 35.5 vs 37.1 us at ctx 32768 but 613 vs 625 tok/s on the 8B decode: not kept.)
+// gh_set_attention_splits replaces the policy's count (still capped by chunks and 32).
 uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows) {
-    static const uint32_t forced = [] {
-        const char* e = std::getenv("GH_ATTN_SPLITS");
-        return e ? (uint32_t)std::atoi(e) : 0u;
-    }();
     const uint32_t chunks = ceil_div(max_len, 64);
-    const uint32_t want = forced ? forced : ceil_div(2 * std::max(b->cus, 1u), std::max(kv_heads * rows, 1u));
+    const uint32_t want = b->attn_splits ? b->attn_splits
+                                         : ceil_div(2 * std::max(b->cus, 1u), std::max(kv_heads * rows, 1u));
     return std::max<uint32_t>(1, std::min<uint32_t>({want, chunks, 32u}));
 }
 
@@ -309,8 +308,7 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         default: return fail(b, GH_E_UNSUPPORTED, "attention: GQA group must be 1, 2, 4 or 8");
     }
     // Batched prefill on the matrix cores: 32-row query blocks x kv heads (G = 4, head 128).
-    static const bool no_mfma = std::getenv("GH_ATTN_PREFILL_SIMT") != nullptr;
-    if (!no_mfma && !pos_ptr && rows >= kAttnPrefillMinRows && group == 4 && kv->head_dim == 128 &&
+    if (!pos_ptr && rows >= kAttnPrefillMinRows && group == 4 && kv->head_dim == 128 &&
         kv->value_dim == 128) {
         GhAttnArgs a{};
         a.q = q->addr;
@@ -326,14 +324,9 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.base = base;
         a.rows = rows;
         a.scale = 1.0f / std::sqrt((float)kv->head_dim);
-        // 32 query rows per workgroup (K/V tiles shared by twice the rows; 248 VGPRs keep two
-        // workgroups resident per CU) or 16 (GH_ATTN_PREFILL_ROWS=16, for comparison)
-        static const uint32_t qrows = [] {
-            const char* e = std::getenv("GH_ATTN_PREFILL_ROWS");
-            return e && std::atoi(e) == 16 ? 16u : 32u;
-        }();
-        return launch(b, qrows == 16 ? K_ATTN_PREFILL_G4_Q16 : K_ATTN_PREFILL_G4, ceil_div(rows, qrows),
-                      kv->kv_heads, 1, 256, &a);
+        // 32 query rows per workgroup (K/V tiles shared by twice the rows of 16-row blocks;
+        // 248 VGPRs keep two workgroups resident per CU)
+        return launch(b, K_ATTN_PREFILL_G4, ceil_div(rows, 32), kv->kv_heads, 1, 256, &a);
     }
     const uint32_t splits = attention_splits(b, max_pos + 1, kv->kv_heads, rows);
     // bound the partials: rows in groups that fit a 256 MiB workspace
@@ -407,16 +400,8 @@ int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, vo
     return rc;
 }
 
-// Rows per wavefront task: enough tasks to fill the machine (>= ~2 per SIMD) with as many
-// rows per task as that allows; GH_GEMV_ROWS (1, 2, 4) overrides for tuning sweeps.
-static uint32_t gemv_rows(uint64_t total_rows) {
-    static const int forced = [] {
-        const char* e = std::getenv("GH_GEMV_ROWS");
-        return e ? std::atoi(e) : 0;
-    }();
-    if (forced == 1 || forced == 2 || forced == 4) return (uint32_t)forced;
-    return total_rows >= 4096 ? 2 : 1;
-}
+// Rows per wavefront task: two from 4096 rows, one below (more tasks to fill the machine).
+static uint32_t gemv_rows(uint64_t total_rows) { return total_rows >= 4096 ? 2 : 1; }
 
 uint32_t resident_wgs(gh_backend* b, GhKernel k, uint32_t block, uint32_t shmem) {
     int n = 0;
@@ -427,7 +412,7 @@ uint32_t resident_wgs(gh_backend* b, GhKernel k, uint32_t block, uint32_t shmem)
 
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
             uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up,
-            const gh_buf* norm, float eps) {
+            const gh_buf* norm, float eps, const GhRopeTable* rt) {
     if (nseg == 0 || nseg > 3) return fail(b, GH_E_INVALID, "gemv: 1..3 segments");
     GhGemvArgs a{};
     const uint32_t in_dim = segs[0].w->cols;
@@ -453,27 +438,20 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
         if (nseg != 1 || !up || up->format != GH_FMT_Q4_K || segs[0].w->format != GH_FMT_Q4_K ||
             up->rows != segs[0].w->rows || up->cols != in_dim)
             return fail(b, GH_E_INVALID, "gemv: SwiGLU needs Q4_K gate/up of one shape");
-        static const uint32_t swiglu_rows = [] {
-            const char* e = std::getenv("GH_SWIGLU_ROWS");
-            return e ? (uint32_t)std::atoi(e) : 0u;
-        }();
-        r = swiglu_rows == 1 || swiglu_rows == 2 ? swiglu_rows : std::min<uint32_t>(r, 2);
         k = r == 2 ? K_GEMV_SWIGLU_R2 : K_GEMV_SWIGLU_R1;
         a.aux = up->addr;
     } else if (mixed) {
         k = K_GEMV_MIXED_R2;
     } else if (segs[0].w->format == GH_FMT_Q4_K) {
-        k = r == 4 ? K_GEMV_Q4K_R4 : r == 2 ? K_GEMV_Q4K_R2 : K_GEMV_Q4K_R1;
+        k = r == 2 ? K_GEMV_Q4K_R2 : K_GEMV_Q4K_R1;
     } else {
-        k = r == 4 ? K_GEMV_Q6K_R4 : r == 2 ? K_GEMV_Q6K_R2 : K_GEMV_Q6K_R1;
+        k = r == 2 ? K_GEMV_Q6K_R2 : K_GEMV_Q6K_R1;
     }
-    static const bool no_direct = std::getenv("GH_GEMV_NO_DIRECT") != nullptr;
-    const bool direct = !no_direct && !norm && n == 1 && nseg == 1 && !swiglu && in_dim <= 4096;
+    const bool direct = !norm && n == 1 && nseg == 1 && !swiglu && in_dim <= 4096;
     // direct launches of 8192 rows or more take one-row tasks (more waves in flight: 12288x4096
     // Q4_K measured 6.84 us against 7.21 us with two-row tasks; 4096x4096 stays at two rows,
     // 3.94 us against 4.06 us)
-    static const bool direct_r2 = std::getenv("GH_DIRECT_R2") != nullptr;  // for comparison
-    if (direct && !direct_r2 && total_rows >= 8192 && (k == K_GEMV_Q4K_R2 || k == K_GEMV_Q6K_R2)) {
+    if (direct && total_rows >= 8192 && (k == K_GEMV_Q4K_R2 || k == K_GEMV_Q6K_R2)) {
         k = k == K_GEMV_Q4K_R2 ? K_GEMV_Q4K_R1 : K_GEMV_Q6K_R1;
         r = 1;
     }
@@ -481,38 +459,28 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
         switch (k) {
             case K_GEMV_Q4K_R1: k = K_GEMV_Q4K_R1_D; break;
             case K_GEMV_Q4K_R2: k = K_GEMV_Q4K_R2_D; break;
-            case K_GEMV_Q4K_R4: k = K_GEMV_Q4K_R4_D; break;
             case K_GEMV_Q6K_R1: k = K_GEMV_Q6K_R1_D; break;
             case K_GEMV_Q6K_R2: k = K_GEMV_Q6K_R2_D; break;
-            case K_GEMV_Q6K_R4: k = K_GEMV_Q6K_R4_D; break;
             default: break;
         }
     }
-    static const bool no_splitk = std::getenv("GH_GEMV_NO_SPLITK") != nullptr;
-    const bool splitk = !no_splitk && !norm && n == 1 && nseg == 1 && !swiglu && in_dim > 4096 &&
-                        in_dim <= 16384;
+    const bool splitk = !norm && n == 1 && nseg == 1 && !swiglu && in_dim > 4096 && in_dim <= 16384;
     // in_dim 12288 (192 units) splits over three waves, one unit per lane, four rows per task
     // (the 8B FFN down: 1,024 tasks, one round at three waves per SIMD). Measured on the 8B
     // decode: 607 tok/s, against 599 with two-row tasks and 596 with the four-wave kernels.
-    // GH_SPLITK_ROWS = 2 or 0 selects those for comparison. (Four-row tasks for in_dim 16384,
-    // four waves, measured neutral on the 14B decode: 374.2 vs 374.0 tok/s.)
-    static const uint32_t splitk_rows = [] {
-        const char* e = std::getenv("GH_SPLITK_ROWS");
-        const int v = e ? std::atoi(e) : 4;
-        return v == 4 ? 4u : v == 0 ? 0u : 2u;
-    }();
+    // (Four-row tasks for in_dim 16384, four waves, measured neutral on the 14B decode: 374.2
+    // vs 374.0 tok/s.)
     uint32_t block = 256;
-    if (splitk && splitk_rows && in_dim / 64 == 192 && r >= 2) {
-        const bool q4 = segs[0].w->format == GH_FMT_Q4_K;
-        r = splitk_rows;
-        k = r == 4 ? (q4 ? K_GEMV_Q4K_R4_K3 : K_GEMV_Q6K_R4_K3) : (q4 ? K_GEMV_Q4K_R2_K3 : K_GEMV_Q6K_R2_K3);
+    if (splitk && in_dim / 64 == 192 && r >= 2) {
+        r = 4;
+        k = segs[0].w->format == GH_FMT_Q4_K ? K_GEMV_Q4K_R4_K3 : K_GEMV_Q6K_R4_K3;
         block = 192;
     } else if (splitk) {
         switch (k) {
             case K_GEMV_Q4K_R1: k = K_GEMV_Q4K_R1_K; break;
-            case K_GEMV_Q4K_R2: case K_GEMV_Q4K_R4: k = K_GEMV_Q4K_R2_K; r = 2; break;
+            case K_GEMV_Q4K_R2: k = K_GEMV_Q4K_R2_K; break;
             case K_GEMV_Q6K_R1: k = K_GEMV_Q6K_R1_K; break;
-            case K_GEMV_Q6K_R2: case K_GEMV_Q6K_R4: k = K_GEMV_Q6K_R2_K; r = 2; break;
+            case K_GEMV_Q6K_R2: k = K_GEMV_Q6K_R2_K; break;
             default: break;
         }
     }
@@ -546,28 +514,24 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
         a.norm_w = norm->addr;
         a.eps = eps;
     }
-    a.table = (uint64_t)b->rope.table;
-    a.post = (uint64_t)b->rope.post;
+    if (rope && (!rt || !rt->table)) return fail(b, GH_E_STATE, "gemv: RoPE table not built");
+    a.table = rt ? (uint64_t)rt->table : 0;
+    a.post = rt ? (uint64_t)rt->post : 0;
     a.pos_ptr = (uint64_t)pos_ptr;
     a.in_dim = in_dim;
     a.nseg = nseg;
     a.n = n;
     a.base = base;
-    a.pairs = b->rope.yarn.rope_dim / 2;
+    a.pairs = rt ? rt->yarn.rope_dim / 2 : 0;
     a.head_dim = head_dim;
     a.tasks = task;
-    if (rope && !b->rope.table) return fail(b, GH_E_STATE, "gemv: RoPE table not built");
     if (in_dim / 64 > 256) return fail(b, GH_E_UNSUPPORTED, "gemv: in_dim above 16384");
     // x staged once per workgroup in LDS (144 B per 64-weight unit; both layouts if mixed);
     // the persistent grid (at most what is resident at once) loops its waves over the tasks.
     // + the normalized FP16 row and 16 bytes of reduction scratch when RMSNorm is fused
     uint32_t shmem = (in_dim / 64) * 144 * (mixed ? 2 : 1) + (norm ? in_dim * 2 + 16 : 0);
-    static const uint32_t max_wg = [] {
-        const char* e = std::getenv("GH_GEMV_MAX_WG");
-        return e ? (uint32_t)std::atoi(e) : 0u;
-    }();
     if (direct || splitk) shmem = 0;
-    const uint32_t cap = max_wg ? max_wg : resident_wgs(b, k, block, shmem);
+    const uint32_t cap = resident_wgs(b, k, block, shmem);
     // split-K: one task per workgroup (four waves share it); otherwise one per wave
     const uint32_t want = splitk ? task : ceil_div(task, 4);
     a.groups = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
@@ -638,8 +602,7 @@ void gh_destroy(gh_backend* b) {
     if (b->stream) (void)hipStreamSynchronize(b->stream);
     if (b->ws) (void)hipFree(b->ws);
     if (b->counters) (void)hipFree(b->counters);
-    if (b->rope.table) (void)hipFree(b->rope.table);
-    if (b->rope.post) (void)hipFree(b->rope.post);
+    free_rope(b->rope);
     for (hipModule_t m : b->modules) (void)hipModuleUnload(m);
     if (b->ev_start) (void)hipEventDestroy(b->ev_start);
     if (b->ev_stop) (void)hipEventDestroy(b->ev_stop);
@@ -816,14 +779,14 @@ int gh_embed(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* w, u
 
 // Matrix-core GEMM for n >= kGemmMinTokens. Batches of 256 tokens or more take the
 // warp-specialized kernels (256 tokens x 128 or 96 rows per 512-thread workgroup); shorter
-// batches take the 256-thread tiles (tokens x rows: 128 x 64, 128 x 128, 256 x 64, 256 x 96,
-// 256 x 128). Either splits K over the units when the tiles alone would leave CUs idle.
+// batches take the 256-thread tiles of 128 tokens x 64 rows (outputs below 4096 rows) or
+// x 128 rows. Either splits K over the units when the tiles alone would leave CUs idle.
 constexpr uint32_t kGemmMinTokens = 8;
 
 struct GemmTile {
     uint32_t tokens, rows, index;
 };
-constexpr GemmTile kGemmTiles[5] = {{128, 64, 0}, {128, 128, 1}, {256, 64, 2}, {256, 96, 3}, {256, 128, 4}};
+constexpr GemmTile kGemmTiles[2] = {{128, 64, 0}, {128, 128, 1}};
 
 // One GEMM launch over tr x tt tiles and `splits` K ranges; with splits > 1 the kernel writes
 // FP32 partials to the workspace and gh_gemm_reduce sums them in split order.
@@ -852,21 +815,12 @@ static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, u
 
 int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n) {
     const uint32_t in_dim = w->cols, rows = w->rows, units = in_dim / 64;
-    static const int forced_tile = [] {
-        const char* e = std::getenv("GH_GEMM_TILE");
-        return e ? std::atoi(e) : -1;
-    }();
-    static const uint32_t forced_splits = [] {
-        const char* e = std::getenv("GH_GEMM_SPLITS");
-        return e ? (uint32_t)std::atoi(e) : 0u;
-    }();
     // splits: at most 16 and at least 8 units of 64 k per split
     auto clamp_splits = [&](uint32_t s) {
-        return std::max<uint32_t>(1, std::min<uint32_t>({forced_splits ? forced_splits : s,
-                                                         std::max<uint32_t>(1, units / 8), 16u}));
+        return std::max<uint32_t>(1, std::min<uint32_t>({s, std::max<uint32_t>(1, units / 8), 16u}));
     };
     const bool q4 = w->format == GH_FMT_Q4_K;
-    if (n >= 256 && forced_tile < 0) {
+    if (n >= 256) {
         // Row height (measured at 512 tokens on the 8B and 14B shapes): one workgroup per CU,
         // s = CUs / tiles splits, and the height whose tiles x splits fill the CUs' last wave
         // better — 96 rows for 12288 x 4096 (256 tiles against 192 of 128 rows), 128 rows
@@ -886,12 +840,7 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
         return gemm_launch(b, k, 512, tr, tt, clamp_splits(std::max<uint32_t>(1, slots / tiles)), out, a, w, n);
     }
-    GemmTile tile;
-    if (forced_tile >= 0 && forced_tile < 5) {
-        tile = kGemmTiles[forced_tile];
-    } else {
-        tile = rows >= 4096 ? kGemmTiles[1] : kGemmTiles[0];
-    }
+    const GemmTile tile = rows >= 4096 ? kGemmTiles[1] : kGemmTiles[0];
     const GhKernel k = (GhKernel)((q4 ? K_GEMM_Q4K_T128_R64 : K_GEMM_Q6K_T128_R64) + tile.index);
     const uint32_t tr = ceil_div(rows, tile.rows), tt = ceil_div(n, tile.tokens), tiles = tr * tt;
     return gemm_launch(b, k, 256, tr, tt, clamp_splits(std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles)),
@@ -949,9 +898,10 @@ int gh_rope_yarn(gh_backend* b, gh_encoder* enc, const gh_buf* x, uint32_t heads
     if (!yarn_valid(yarn) || role > 1 || yarn->rope_dim > head_dim)
         return latch(enc, fail(b, GH_E_INVALID, "rope: invalid YaRN parameters"));
     if (!fits(x, (uint64_t)heads * head_dim * 2)) return latch(enc, fail(b, GH_E_RANGE, "rope: buffer too small"));
-    rc = ensure_rope(b, yarn, pos + 1);
+    if (pos >= kMaxRopePositions) return latch(enc, fail(b, GH_E_RANGE, "rope: position beyond the table limit"));
+    rc = ensure_rope(b, b->rope, yarn, pos + 1);
     if (rc) return latch(enc, rc);
-    return latch(enc, op_rope(b, x, heads, head_dim, pos, 1, role, nullptr));
+    return latch(enc, op_rope(b, b->rope, x, heads, head_dim, pos, 1, role, nullptr));
 }
 
 int gh_rope_yarn_batched(gh_backend* b, gh_encoder* enc, const gh_buf* q, const gh_buf* k,
@@ -964,9 +914,9 @@ int gh_rope_yarn_batched(gh_backend* b, gh_encoder* enc, const gh_buf* q, const 
     if ((uint64_t)base + rows > 0xFFFFFFFFull) return latch(enc, fail(b, GH_E_RANGE, "rope: position overflow"));
     if (!fits(q, (uint64_t)rows * q_heads * head_dim * 2) || !fits(k, (uint64_t)rows * kv_heads * head_dim * 2))
         return latch(enc, fail(b, GH_E_RANGE, "rope: buffer too small"));
-    rc = ensure_rope(b, yarn, base + rows);
-    if (!rc) rc = op_rope(b, q, q_heads, head_dim, base, rows, GH_ROPE_QUERY, nullptr);
-    if (!rc) rc = op_rope(b, k, kv_heads, head_dim, base, rows, GH_ROPE_KEY, nullptr);
+    rc = ensure_rope(b, b->rope, yarn, base + rows);
+    if (!rc) rc = op_rope(b, b->rope, q, q_heads, head_dim, base, rows, GH_ROPE_QUERY, nullptr);
+    if (!rc) rc = op_rope(b, b->rope, k, kv_heads, head_dim, base, rows, GH_ROPE_KEY, nullptr);
     return latch(enc, rc);
 }
 
@@ -1122,6 +1072,14 @@ int gh_timer_stop(gh_backend* b, float* ms) {
 int gh_synchronize(gh_backend* b) {
     if (!b) return GH_E_INVALID;
     return hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
+}
+
+int gh_set_attention_splits(gh_backend* b, uint32_t splits) {
+    if (!b) return GH_E_INVALID;
+    if (splits > 32) return fail(b, GH_E_INVALID, "attention splits: at most 32");
+    b->attn_splits = splits;
+    ++b->gen;  // recorded graphs hold the old grid
+    return GH_OK;
 }
 
 }  // extern "C"

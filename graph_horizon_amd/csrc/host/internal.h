@@ -18,10 +18,8 @@ enum GhKernel : int {
     K_DEQUANT_Q6K,
     K_GEMV_Q4K_R1,
     K_GEMV_Q4K_R2,
-    K_GEMV_Q4K_R4,
     K_GEMV_Q6K_R1,
     K_GEMV_Q6K_R2,
-    K_GEMV_Q6K_R4,
     K_GEMV_MIXED_R2,
     K_GEMV_SWIGLU_R1,
     K_GEMV_SWIGLU_R2,
@@ -38,16 +36,12 @@ enum GhKernel : int {
     K_GEMV_Q4K_R2_D,
     K_GEMV_Q6K_R1_D,
     K_GEMV_Q6K_R2_D,
-    K_GEMV_Q4K_R4_D,
-    K_GEMV_Q6K_R4_D,
     // split-K variants (single token, one matrix, 4096 < in_dim <= 16384, no RMSNorm)
     K_GEMV_Q4K_R1_K,
     K_GEMV_Q4K_R2_K,
     K_GEMV_Q6K_R1_K,
     K_GEMV_Q6K_R2_K,
-    // three-wave split-K (in_dim 12288 = 192 units: one unit per lane)
-    K_GEMV_Q4K_R2_K3,
-    K_GEMV_Q6K_R2_K3,
+    // three-wave split-K with four-row tasks (in_dim 12288 = 192 units: one unit per lane)
     K_GEMV_Q4K_R4_K3,
     K_GEMV_Q6K_R4_K3,
     K_RMSNORM,
@@ -65,17 +59,10 @@ enum GhKernel : int {
     // prefill GEMM tile variants (tokens x rows per workgroup), Q4_K then Q6_K
     K_GEMM_Q4K_T128_R64,
     K_GEMM_Q4K_T128_R128,
-    K_GEMM_Q4K_T256_R64,
-    K_GEMM_Q4K_T256_R96,
-    K_GEMM_Q4K_T256_R128,
     K_GEMM_Q6K_T128_R64,
     K_GEMM_Q6K_T128_R128,
-    K_GEMM_Q6K_T256_R64,
-    K_GEMM_Q6K_T256_R96,
-    K_GEMM_Q6K_T256_R128,
     K_GEMM_REDUCE,
     K_ATTN_PREFILL_G4,
-    K_ATTN_PREFILL_G4_Q16,
     K_GEMM3_Q4K_R128,
     K_GEMM3_Q6K_R128,
     K_GEMM3_Q4K_R96,
@@ -86,7 +73,10 @@ enum GhKernel : int {
 };
 
 // Device-resident YaRN rotation table: (cos, sin) per (position, pair) and the query
-// post-scale per position, computed on the host with Yarn::pair's formula.
+// post-scale per position, computed on the host with Yarn::pair's formula. The backend keeps
+// one for the trait's rope ops (rebuilt when their YaRN parameters change); every model owns
+// its own, built once at creation for its KV context, which its recorded graphs read.
+constexpr uint32_t kMaxRopePositions = 262144;  // family/mistral/version.rs:16 MAX_CONTEXT
 struct GhRopeTable {
     gh_yarn yarn{};
     uint32_t positions = 0;
@@ -115,7 +105,8 @@ struct gh_backend {
     size_t ws_bytes = 0;
     void* counters = nullptr;  // attention merge counters, zero between launches
     size_t counter_slots = 0;
-    GhRopeTable rope;
+    GhRopeTable rope;  // the trait ops' table (gh_rope_yarn, gh_rope_yarn_batched)
+    uint32_t attn_splits = 0;  // gh_set_attention_splits: 0 = attention_splits' policy
     uint64_t gen = 0;  // bumped whenever the workspace or rope table moves (captured graphs hold them)
 };
 
@@ -135,11 +126,14 @@ int launch(gh_backend* b, GhKernel k, uint32_t gx, uint32_t gy, uint32_t gz, uin
 int ensure_workspace(gh_backend* b, size_t bytes);
 // Workgroups of `block` threads and `shmem` bytes of LDS resident on the whole device at once.
 uint32_t resident_wgs(gh_backend* b, GhKernel k, uint32_t block, uint32_t shmem);
-int ensure_rope(gh_backend* b, const gh_yarn* y, uint32_t positions);
+// Builds (or rebuilds, for other parameters or more positions) table t for `positions`
+// positions (at most kMaxRopePositions).
+int ensure_rope(gh_backend* b, GhRopeTable& t, const gh_yarn* y, uint32_t positions);
+void free_rope(GhRopeTable& t);
 bool yarn_valid(const gh_yarn* y);
 // Graph-capturable op variants used by the model driver: positions/tokens read from device.
-int op_rope(gh_backend* b, const gh_buf* x, uint32_t heads, uint32_t head_dim, uint32_t base,
-            uint32_t rows, uint32_t role, const void* pos_ptr);
+int op_rope(gh_backend* b, const GhRopeTable& t, const gh_buf* x, uint32_t heads,
+            uint32_t head_dim, uint32_t base, uint32_t rows, uint32_t role, const void* pos_ptr);
 int op_kv_write(gh_backend* b, const gh_kv* kv, const gh_buf* k, const gh_buf* v,
                 uint64_t k_elem_off, uint64_t v_elem_off, uint32_t vectors, const void* pos_ptr);
 int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
@@ -158,9 +152,10 @@ struct GemvSeg {
 // norm: x is the FP32 residual and rmsnorm_x(norm, eps) is applied while staging it
 // (in_dim <= kFusedNormMaxDim).
 constexpr uint32_t kFusedNormMaxDim = 5120;
+// rope: the table the RoPE epilogues read (required when a segment has one).
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
             uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up,
-            const gh_buf* norm = nullptr, float eps = 0.0f);
+            const gh_buf* norm = nullptr, float eps = 0.0f, const GhRopeTable* rope = nullptr);
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
 uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows);
 int ensure_counters(gh_backend* b, size_t slots);

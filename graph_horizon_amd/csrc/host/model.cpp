@@ -34,6 +34,7 @@ struct gh_model {
     gh_buf scalars{};  // u32[4]: position, token, argmax, spare
     gh_buf history{};  // u32[kv_context]
     gh_kv kv{};
+    GhRopeTable rope;  // this model's YaRN table for positions 0 .. kv_context - 1
     std::vector<gh_buf> owned;
     hipGraphExec_t step = nullptr;
     hipGraph_t step_graph = nullptr;
@@ -105,7 +106,7 @@ int layer_decode_fused(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t 
                             {&w[GH_T_ATTN_V], vbase, GH_EPI_CACHE}};
     const gh_buf *xin = nullptr, *nw = nullptr;
     int rc = normed(&w[GH_T_ATTN_NORM], &xin, &nw);
-    if (!rc) rc = op_gemv(b, qkv, 3, xin, 1, base, pos_ptr, c.key_length, nullptr, nw, c.rms_epsilon);
+    if (!rc) rc = op_gemv(b, qkv, 3, xin, 1, base, pos_ptr, c.key_length, nullptr, nw, c.rms_epsilon, &m->rope);
     const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base;
     if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, 1, li, pos_ptr, max_pos);
     const GemvSeg o{&w[GH_T_ATTN_OUTPUT], s.x.addr, GH_EPI_RESID};
@@ -142,8 +143,8 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
     if (!rc) rc = gh_matmul_batched(b, enc, &s.k, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);
     if (!rc) rc = gh_matmul_batched(b, enc, &s.v, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
     // rope_yarn (block.rs:147-166) / rope_yarn_batched (prefill/layer.rs:79-89)
-    if (!rc) rc = op_rope(b, &s.q, c.head_count, c.key_length, base, rows, GH_ROPE_QUERY, pos_ptr);
-    if (!rc) rc = op_rope(b, &s.k, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, pos_ptr);
+    if (!rc) rc = op_rope(b, m->rope, &s.q, c.head_count, c.key_length, base, rows, GH_ROPE_QUERY, pos_ptr);
+    if (!rc) rc = op_rope(b, m->rope, &s.k, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, pos_ptr);
     // kv_cache::append_batch (kv_cache/mod.rs:133-177): payload offsets of (layer, base)
     const uint64_t per_pos_k = (uint64_t)c.kv_head_count * c.key_length;
     const uint64_t per_pos_v = (uint64_t)c.kv_head_count * c.value_length;
@@ -304,7 +305,7 @@ int gh_model_create(gh_backend* b, const gh_model_config* cfg, gh_model** out) {
     if (!rc) rc = alloc(m, (uint64_t)c.vocab_size * 4, &m->logits);
     if (!rc) rc = alloc(m, 16, &m->scalars);
     if (!rc) rc = alloc(m, (uint64_t)c.kv_context * 4, &m->history);
-    if (!rc) rc = ensure_rope(b, &c.yarn, c.kv_context);
+    if (!rc) rc = ensure_rope(b, m->rope, &c.yarn, c.kv_context);
     // partials for a decode step and for one prefill chunk
     const uint32_t dsplits = attention_splits(b, c.kv_context, c.kv_head_count, 1);
     if (!rc) rc = ensure_workspace(b, attention_workspace(1, c.head_count, dsplits));
@@ -327,6 +328,8 @@ void gh_model_destroy(gh_model* m) {
             if (w.addr) gh_free_buffer(m->b, &w);
     for (gh_buf* w : {&m->token_embd, &m->output_norm, &m->output})
         if (w->addr) gh_free_buffer(m->b, w);
+    (void)hipStreamSynchronize(m->b->stream);
+    free_rope(m->rope);
     delete m;
 }
 

@@ -210,10 +210,11 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
     // device coherence point, loads that do not hit a stale L2 line of another XCD — so the
     // exchange needs no L2 writeback or invalidation (an agent-scope release/acquire pair
     // would do both to the whole L2: ~3 us per launch measured). Each thread waits for its
-    // own stores to complete before the barrier, so the counter increment follows all of the
-    // workgroup's partials; the last workgroup issues its loads only after it has seen the
-    // count (the barrier that publishes `last` orders them after the atomic's return).
-    __builtin_amdgcn_s_waitcnt(0);
+    // own stores to complete before the barrier (the wait is an asm statement that clobbers
+    // memory, so the compiler keeps the stores ahead of it), so the counter increment follows
+    // all of the workgroup's partials; the last workgroup issues its loads only after it has
+    // seen the count (the barrier that publishes `last` orders them after the atomic's return).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
         uint32_t* ctr = (uint32_t*)a.counters + (size_t)row * hot.kv_heads + kvh;
@@ -571,4 +572,3 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
 }  // namespace
 
 GH_KERNEL __launch_bounds__(256) void gh_attn_prefill_g4(GhAttnArgs a) { attn_prefill_g4<2>(a); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_prefill_g4_q16(GhAttnArgs a) { attn_prefill_g4<1>(a); }

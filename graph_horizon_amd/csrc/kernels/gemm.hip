@@ -5,9 +5,12 @@
 // rows as tiles of v_mfma_f32_32x32x16_f16 (A = activations, M = tokens, loaded from global
 // memory straight into registers; B = weights, N = rows; FP32 accumulators). K advances one
 // 64-weight unit per stage. Each stage the workgroup dequantizes the w tile (BR rows x 64)
-// into LDS: w = FP16(RNE(the reference's FP32 dequantized weight)), computed per weight
-// exactly as dequant_row does (Q4_K: (d·sc)·q - dmin·mn; Q6_K: (d·sc)·(q - 32);
-// cpu/dequant.rs:93-123, 274-308). The LDS tile is double-buffered; the next unit's weight
+// into LDS as FP16. Q4_K: w = FP16(RNE(the reference's FP32 dequantized weight)), computed as
+// dequant_row does ((d·sc)·q - dmin·mn, cpu/dequant.rs:93-123). Q6_K: (q - 32)·(d·sc) as one
+// fused multiply-add u·da + (-32·da) rounded once to FP16 (the compiler forms v_fma_mix);
+// the reference rounds the same exact product to FP32 first (dequant.rs:274-308), and the two
+// roundings differ by one FP16 ulp when that FP32 value lands exactly on an FP16 tie. The
+// LDS tile is double-buffered; the next unit's weight
 // and activation loads are in flight while the matrix cores run on the current one, and one
 // barrier separates stages.
 //
@@ -16,7 +19,7 @@
 //
 // Numerics: the only departure from the reference CPU kernel (q4k.rs:218-325 / q6k.rs:157-235,
 // FP32 dequantized weights, FP32 accumulation) is the FP16 rounding of each dequantized
-// weight (relative 2^-12 at most) — the rounding the reference's own cooperative-matrix
+// weight (relative 2^-11 at most) — the rounding the reference's own cooperative-matrix
 // prefill shaders carry (vulkan/shaders/matmul/matmul_q4_k_coopmat_f16out.comp). Products of
 // FP16 values are exact in FP32; accumulation is FP32.
 //
@@ -361,15 +364,12 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
 
 }  // namespace
 
-// Tile variants: tokens per workgroup (4 waves x 32 or 64) x weight rows (64, 96, 128).
+// Tile variants: 128 tokens per workgroup (4 waves x 32) x 64 or 128 weight rows.
 #define GH_GEMM(SUF, WT, BR)                                                                       \
     GH_KERNEL __launch_bounds__(256) void gh_gemm_q4k_##SUF(GhGemmArgs a) { gemm_body<kQ4K, WT, BR>(a); } \
     GH_KERNEL __launch_bounds__(256) void gh_gemm_q6k_##SUF(GhGemmArgs a) { gemm_body<kQ6K, WT, BR>(a); }
 GH_GEMM(t128_r64, 32, 64)
 GH_GEMM(t128_r128, 32, 128)
-GH_GEMM(t256_r64, 64, 64)
-GH_GEMM(t256_r96, 64, 96)
-GH_GEMM(t256_r128, 64, 128)
 // warp-specialized 256-token tiles (512 threads)
 GH_KERNEL __launch_bounds__(512) void gh_gemm3_q4k_r128(GhGemmArgs a) { gemm3_body<kQ4K, 128>(a); }
 GH_KERNEL __launch_bounds__(512) void gh_gemm3_q6k_r128(GhGemmArgs a) { gemm3_body<kQ6K, 128>(a); }

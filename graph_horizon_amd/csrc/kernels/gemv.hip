@@ -829,21 +829,15 @@ GH_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gh
 }
 GH_GEMV(gh_gemv_swiglu_r1, 1, kModeSwiglu)
 GH_GEMV(gh_gemv_swiglu_r2, 2, kModeSwiglu)
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4(GH_HOT_PARAMS) { gemv_body<4, kModeQ4, false>(a, GH_HOT); }
 // direct-x variants (suffix _d): single token, one matrix, in_dim <= 4096, no RMSNorm
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ4K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ4K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ6K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ6K>(a, GH_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r4_d(GH_HOT_PARAMS) { gemv_direct<4, kQ4K>(a, GH_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4_d(GH_HOT_PARAMS) { gemv_direct<4, kQ6K>(a, GH_HOT); }
 // split-K variants (suffix _k): single token, one matrix, 4096 < in_dim <= 16384, no RMSNorm
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_k(GH_HOT_PARAMS) { gemv_splitk<1, kQ4K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_k(GH_HOT_PARAMS) { gemv_splitk<2, kQ4K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_k(GH_HOT_PARAMS) { gemv_splitk<1, kQ6K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_k(GH_HOT_PARAMS) { gemv_splitk<2, kQ6K>(a, GH_HOT); }
-GH_KERNEL __launch_bounds__(192) void gh_gemv_q4k_r2_k3(GH_HOT_PARAMS) { gemv_splitk<2, kQ4K, 3>(a, GH_HOT); }
-GH_KERNEL __launch_bounds__(192) void gh_gemv_q6k_r2_k3(GH_HOT_PARAMS) { gemv_splitk<2, kQ6K, 3>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(192) void gh_gemv_q4k_r4_k3(GH_HOT_PARAMS) { gemv_splitk<4, kQ4K, 3>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(192) void gh_gemv_q6k_r4_k3(GH_HOT_PARAMS) { gemv_splitk<4, kQ6K, 3>(a, GH_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r4(GH_HOT_PARAMS) { gemv_body<4, kModeQ6, false>(a, GH_HOT); }

@@ -16,6 +16,8 @@ __device__ __forceinline__ float gh_h2f(uint32_t bits16) {
 
 __device__ __forceinline__ uint16_t gh_f2h(float v) {
     // v_cvt_f16_f32 under the default round-to-nearest-even mode (f16 denormals preserved).
+    // A NaN keeps its sign and the top bits of its payload, quieted — as the reference's
+    // buffer writes narrow through F16C vcvtps2ph (backend/cpu/f16.rs:86-102).
     return __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 

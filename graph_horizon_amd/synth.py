@@ -6,7 +6,7 @@ Distributions (the benchmark configurations of the reference's hot path):
   Q6_K block (210 B): ql[128], qh[64] uniform bytes (quants uniform in -32..31);
       scales[16] = int8(clip(round(N(0, 16)), -128, 127)); d = f16(|N(0, d_std)|).
   Activations: f32 N(0, 1), rounded to FP16 at the boundary where the contract is FP16.
-Generator: numpy.random.default_rng(seed) (PCG64).
+Generator: numpy.random.default_rng(seed) (PCG64); uniform bytes are its raw 64-bit outputs.
 
 For whole-model runs `d_std = model_d_std(in_dim)` keeps every FP16 intermediate finite:
 a weight row then has std ≈ 1/sqrt(in_dim), so unit-RMS inputs give unit-scale outputs.
@@ -30,10 +30,15 @@ def f16_bits(x) -> np.ndarray:
     return to_f16(x).view(np.uint16)
 
 
+def uniform_bytes(rng: np.random.Generator, n: int) -> np.ndarray:
+    """n uniform bytes: the generator's raw 64-bit words, little-endian."""
+    return rng.bit_generator.random_raw((n + 7) // 8).view(np.uint8)[:n]
+
+
 def q4k_blocks(rng: np.random.Generator, rows: int, in_dim: int, d_std: float = 0.02) -> np.ndarray:
     assert in_dim % 256 == 0
     nblk = rows * (in_dim // 256)
-    blk = np.frombuffer(rng.bytes(nblk * Q4K_BLOCK), dtype=np.uint8).reshape(nblk, Q4K_BLOCK).copy()
+    blk = uniform_bytes(rng, nblk * Q4K_BLOCK).reshape(nblk, Q4K_BLOCK)
     dd = np.abs(rng.standard_normal((nblk, 2), dtype=np.float32) * np.float32(d_std))
     blk[:, 0:4] = dd.astype(np.float16).view(np.uint8).reshape(nblk, 4)
     return blk.reshape(-1)
@@ -43,7 +48,7 @@ def q6k_blocks(rng: np.random.Generator, rows: int, in_dim: int, d_std: float = 
                sc_std: float = 16.0) -> np.ndarray:
     assert in_dim % 256 == 0
     nblk = rows * (in_dim // 256)
-    blk = np.frombuffer(rng.bytes(nblk * Q6K_BLOCK), dtype=np.uint8).reshape(nblk, Q6K_BLOCK).copy()
+    blk = uniform_bytes(rng, nblk * Q6K_BLOCK).reshape(nblk, Q6K_BLOCK)
     sc = np.clip(np.rint(rng.standard_normal((nblk, 16), dtype=np.float32) * sc_std), -128, 127)
     blk[:, 192:208] = sc.astype(np.int8).view(np.uint8)
     d = np.abs(rng.standard_normal(nblk, dtype=np.float32) * np.float32(d_std))

@@ -153,7 +153,9 @@ int gh_logits(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* x
 /* rmsnorm_x, contract.rs:159-168: FP32 x rows -> FP16 out, FP16 weight */
 int gh_rmsnorm_x(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* x,
                  const gh_buf* w, uint32_t dim, float eps, uint32_t rows);
-/* rope_yarn, contract.rs:172-181: in place on FP16 x[heads][head_dim] at position pos */
+/* rope_yarn, contract.rs:172-181: in place on FP16 x[heads][head_dim] at position pos.
+ * Rotations come from a table built for the YaRN parameters (rebuilt when they change):
+ * positions at or beyond 262144 (MAX_CONTEXT, family/mistral/version.rs:16) are GH_E_RANGE. */
 int gh_rope_yarn(gh_backend* b, gh_encoder* enc, const gh_buf* x, uint32_t heads,
                  uint32_t head_dim, uint32_t pos, const gh_yarn* yarn, uint32_t role);
 /* rope_yarn_batched, contract.rs:187-246: rows packed Q then K rows at base..base+rows */
@@ -191,6 +193,11 @@ int gh_timer_start(gh_backend* b);
 /* milliseconds since gh_timer_start, after synchronizing the stream */
 int gh_timer_stop(gh_backend* b, float* ms);
 int gh_synchronize(gh_backend* b);
+/* Attention split count (no counterpart in the reference: a test and tuning hook). Decode
+ * attention splits each (row, kv head) over this many workgroups (at most one per 64-position
+ * chunk); 0 restores the backend's policy (about two workgroups per CU). At most 32. Graphs
+ * recorded before the call are re-recorded on their next use. */
+int gh_set_attention_splits(gh_backend* b, uint32_t splits);
 
 /* =====================================================================================
  * Graph driver: a C++ restatement of the caller side of the boundary — MistralGraph's pinned

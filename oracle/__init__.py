@@ -16,8 +16,11 @@ Every function here was checked against what pins it (tests/test_oracle.py):
   silu_mul / rmsnorm  sequential FP16 rounding rule; RMSNorm formula in fp64
   argmax / top-k      readback.rs:77-100 tie-break cases
   KV layout           layout.rs:105-205 hand-computed byte regions
-  graph               batched prefill == sequential decode within abs 0.05
-                      (generation/tests.rs:716-773)
+  graph               op trace == the reference's shape-recorder trace (graph/shape.rs:389-446),
+                      dedicated and tied; closed-form one-layer models (zeroed FFN or zeroed
+                      O projection) computed in fp64 from the pinned dequant; batched prefill
+                      == sequential decode within abs 0.05 (generation/tests.rs:716-773)
+  residual_add        closed form: numpy x + f32(y) bit for bit (±0, inf, NaN, prefix only)
 """
 from __future__ import annotations
 
@@ -96,6 +99,9 @@ _SIG = {
     "gho_model_logits": (C.POINTER(F32), [P]),
     "gho_model_kv": (C.POINTER(U16), [P, I32]),
     "gho_model_x": (C.POINTER(F32), [P]),
+    "gho_model_set_trace": (None, [P, I32]),
+    "gho_model_load_kv": (I32, [P, P, P, U32, U32]),
+    "gho_model_trace": (C.c_char_p, [P]),
 }
 
 _lib = None
@@ -257,6 +263,18 @@ class Model:
 
     def x(self) -> np.ndarray:
         return np.ctypeslib.as_array(lib().gho_model_x(self.h), (self.cfg.embedding_length,)).copy()
+
+    def load_kv(self, k16, v16, src_context: int, positions: int):
+        """Seed positions [0, positions) of every layer from caches of src_context positions."""
+        k16 = np.ascontiguousarray(k16, dtype=np.uint16)
+        v16 = np.ascontiguousarray(v16, dtype=np.uint16)
+        assert lib().gho_model_load_kv(self.h, _p(k16), _p(v16), src_context, positions) == 0
+
+    def set_trace(self, on: bool):
+        lib().gho_model_set_trace(self.h, 1 if on else 0)
+
+    def trace(self) -> list:
+        return lib().gho_model_trace(self.h).decode().split("\n")[:-1]
 
     def kv(self, role) -> np.ndarray:
         n = self.cfg.block_count * self.kv_context * self.cfg.kv_head_count * self.cfg.key_length

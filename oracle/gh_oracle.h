@@ -160,6 +160,15 @@ const float* gho_model_logits(const gho_model* m);
 const uint16_t* gho_model_kv(const gho_model* m, int role);
 /* last-layer hidden residual x (f32[embedding_length]) after the most recent call */
 const float* gho_model_x(const gho_model* m);
+/* Copies positions [0, positions) of every layer's K and V from caches laid out like this
+ * model's ([layer][src_context][kv_heads][dim]) into the model's cache: lets a test resume a
+ * sequence from another implementation's cache and recompute the following positions. */
+int gho_model_load_kv(gho_model* m, const uint16_t* k, const uint16_t* v, uint32_t src_context,
+                      uint32_t positions);
+/* op trace of the following token/prefill calls (on != 0 clears and starts it): one name per
+ * op, the tensor's name (l<i>.q, output_norm, logits:output, ...) when the op takes one */
+void gho_model_set_trace(gho_model* m, int on);
+const char* gho_model_trace(gho_model* m); /* newline-separated, valid until the next call */
 
 #ifdef __cplusplus
 }

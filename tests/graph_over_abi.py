@@ -12,18 +12,66 @@ import numpy as np
 from graph_horizon_amd import Yarn, synth
 from graph_horizon_amd import _ffi as F
 
+_LAYER_NAMES = {F.T_ATTN_NORM: "attn_norm", F.T_ATTN_Q: "q", F.T_ATTN_K: "k", F.T_ATTN_V: "v",
+                F.T_ATTN_OUTPUT: "attn_out", F.T_FFN_NORM: "ffn_norm", F.T_FFN_GATE: "gate",
+                F.T_FFN_UP: "up", F.T_FFN_DOWN: "down"}
+_GLOBAL_NAMES = {F.T_TOKEN_EMBD: "token_embd", F.T_OUTPUT_NORM: "output_norm", F.T_OUTPUT: "output"}
+
+
+class _Recorder:
+    """The backend seen through the reference's shape recorder (graph/shape.rs:120-360): every
+    op call is forwarded and logged under the name of the weight it was handed (looked up by
+    device address), or under its op name when it takes none."""
+
+    def __init__(self, hip, names):
+        self.hip, self.names, self.trace = hip, names, []
+
+    def _name(self, buf):
+        return self.names.get(buf.addr, "?")
+
+    def __getattr__(self, op):
+        fn = getattr(self.hip, op)
+
+        def call(*args):
+            if op in ("matmul", "matmul_batched", "rmsnorm_x"):
+                self.trace.append(self._name(args[2]))
+            elif op == "logits":
+                self.trace.append("logits:" + self._name(args[2]))
+            elif op == "rope_yarn":
+                self.trace.append("rope_q" if args[5] == F.ROPE_QUERY else "rope_k")
+            elif op in ("begin", "submit", "embed", "kv_write", "silu_mul"):
+                self.trace.append(op)
+            elif op == "residual_add":
+                self.trace.append("residual")
+            elif op == "attention_decode":
+                self.trace.append("attention")
+            elif op in ("attention_prefill", "rope_yarn_batched"):
+                self.trace.append(op)
+            return fn(*args)
+        return call
+
 
 class AbiGraph:
-    def __init__(self, hip, shape, seed, kv_context):
+    def __init__(self, hip, shape, seed, kv_context, tied=False, tensors=None):
+        """`tensors`: (layer, tensor id, format, data) tuples (synth.model_tensors(shape, seed)
+        when None); tied drops the output matrix, so the logits read token_embd
+        (tail.rs:43-58)."""
         self.hip, self.shape = hip, shape
         self.w = {}
-        for layer, tid, fmt, data in synth.model_tensors(shape, seed):
+        names = {}
+        for layer, tid, fmt, data in (tensors if tensors is not None else synth.model_tensors(shape, seed)):
+            if tied and layer == F.NO_LAYER and tid == F.T_OUTPUT:
+                continue
             if fmt == F.FMT_F32:
                 self.w[(layer, tid)] = hip.load_weight(F.FMT_F32, data, data.size, 1)
             else:
                 ind, outd = ((shape.embedding_length, shape.vocab_size) if layer == F.NO_LAYER
                              else synth.tensor_dims(shape, tid))
                 self.w[(layer, tid)] = hip.load_weight(fmt, data, ind, outd)
+            names[self.w[(layer, tid)].addr] = (_GLOBAL_NAMES[tid] if layer == F.NO_LAYER
+                                                else f"l{layer}.{_LAYER_NAMES[tid]}")
+        self.out_key = (F.NO_LAYER, F.T_OUTPUT if (F.NO_LAYER, F.T_OUTPUT) in self.w else F.T_TOKEN_EMBD)
+        self.rec = _Recorder(hip, names)
         d, ffn = shape.embedding_length, shape.feed_forward_length
         qw, kw = shape.head_count * shape.head_dim, shape.kv_head_count * shape.head_dim
         a = hip.alloc_buffer
@@ -37,8 +85,10 @@ class AbiGraph:
         self.kv_context = kv_context
         self.yarn = Yarn(**synth.yarn_params(shape))
 
-    def token(self, tok, pos):
-        h, s = self.hip, self.shape
+    def token(self, tok, pos, trace=None):
+        """One decode token op by op; `trace` (a list) receives the recorded op names."""
+        h, s = (self.rec, self.shape) if trace is not None else (self.hip, self.shape)
+        self.rec.trace = trace if trace is not None else []
         d, ffn = s.embedding_length, s.feed_forward_length
         qw, kw = s.head_count * s.head_dim, s.kv_head_count * s.head_dim
         eps = 1e-5
@@ -64,9 +114,9 @@ class AbiGraph:
             h.matmul(self.ffn_out, self.act, w(F.T_FFN_DOWN), ffn, d)
             h.residual_add(self.x, self.ffn_out, d)
         h.rmsnorm_x(self.normed, self.x, self.w[(F.NO_LAYER, F.T_OUTPUT_NORM)], d, eps, 1)
-        h.logits(self.logits, self.normed, self.w[(F.NO_LAYER, F.T_OUTPUT)], d, s.vocab_size)
+        h.logits(self.logits, self.normed, self.w[self.out_key], d, s.vocab_size)
         h.submit()
-        return h.read_logits(self.logits, s.vocab_size)
+        return self.hip.read_logits(self.logits, s.vocab_size)
 
     def prefill(self, toks, base):
         """prefill::record_batch (graph/prefill/encode.rs:43-106, layer.rs:18-122) for one batch
@@ -104,7 +154,7 @@ class AbiGraph:
             h.residual_add(x, ffn_out, n * d)
         last = h.view(x, (n - 1) * d * 4, d * 4)
         h.rmsnorm_x(self.normed, last, self.w[(F.NO_LAYER, F.T_OUTPUT_NORM)], d, eps, 1)
-        h.logits(self.logits, self.normed, self.w[(F.NO_LAYER, F.T_OUTPUT)], d, s.vocab_size)
+        h.logits(self.logits, self.normed, self.w[self.out_key], d, s.vocab_size)
         h.submit()
         self.prefill_x = h.download(x, np.float32, n * d)
         for b in (x, normed, q, k, v, attn, proj, gate, up, act, ffn_out):

@@ -126,3 +126,51 @@ def test_reference_prefill_attention_vectors(hip, context):
             _close(a, b, f"ctx {context} n {n} {what}", rel=1e-3, floor=1e-5)
         _free(hip, qb, pb, db)
     _free(hip, kv.k, kv.v)
+
+
+def test_decode_every_forced_split_count(hip):
+    """Decode attention with each split count 1..32 forced (gh_set_attention_splits): the split
+    partials cross workgroups through agent-scope atomics and the last workgroup of each
+    (row, kv head) merges them. Positions below, at and across chunk boundaries, and counts
+    above the row's chunk count (the launch then has more workgroups than splits in use, as
+    in a replayed graph's fixed grid). Same bar as the oracle decode test."""
+    rng = np.random.default_rng(321)
+    ctx, layers, qh, kvh = 2048, 2, 32, 8
+    kc = O.f16(rng.standard_normal(layers * ctx * kvh * 128).astype(np.float32))
+    vc = O.f16(rng.standard_normal(layers * ctx * kvh * 128).astype(np.float32))
+    kv = _kv(hip, layers, ctx, kvh, kc, vc)
+    q = O.f16(rng.standard_normal(qh * 128).astype(np.float32))
+    qb, ob = hip.from_host(q), hip.alloc_buffer(qh * 128 * 2)
+    cases = [(0, 0), (63, 1), (64, 0), (700, 1), (2047, 1)]
+    want = {c: O.f32(O.attention_decode(q, kc, vc, 128, kvh, qh, c[0], c[1], ctx)) for c in cases}
+    try:
+        for splits in range(1, 33):
+            hip.set_attention_splits(splits)
+            for pos, layer in cases:
+                hip.attention_decode(ob, qb, kv, qh, pos, layer)
+                got = O.f32(hip.download(ob, np.uint16, qh * 128))
+                _close(got, want[(pos, layer)], f"splits {splits} pos {pos}")
+    finally:
+        hip.set_attention_splits(0)
+    _free(hip, qb, ob, kv.k, kv.v)
+
+
+def test_greedy_graph_with_forced_splits_matches_stream(hip):
+    """A replayed decode graph whose attention grid is fixed at 32 splits (most of them idle at
+    short positions) gives the tokens of the same steps launched on the stream."""
+    from graph_horizon_amd import HipModel, synth
+
+    shape = synth.SHAPES["tiny"]
+    outs = []
+    hip.set_attention_splits(32)
+    try:
+        for flags in (0, F.MODEL_NO_GRAPH):
+            gm = HipModel(hip, synth.model_config(shape, 2304, 16, flags=flags))
+            for layer, tid, fmt, data in synth.model_tensors(shape, 36):
+                gm.load_tensor(layer, tid, fmt, data)
+            gm.prefill(list(range(1, 60)), 0)
+            outs.append(gm.decode_greedy(9, 59, 40))
+            gm.close()
+    finally:
+        hip.set_attention_splits(0)
+    assert np.array_equal(outs[0], outs[1])

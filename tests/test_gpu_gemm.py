@@ -5,8 +5,10 @@ Bars:
     weights (the GEMM's stated operands), |got - want| <= 1e-3·|want| + 2e-6·Σ|terms| — FP32
     accumulation plus the FP16 rounding of the output (2^-11 relative at most);
   * reference CPU kernel (q4k.rs:218-325 / q6k.rs:157-235 restated in the oracle) on the same
-    seeded inputs: the bar above widened by the FP16 rounding envelope of the weights,
-    + 2^-11·Σ|terms| (each RNE-rounded weight is within 2^-11 of its FP32 value);
+    seeded inputs: the bar above widened by + 2^-12·Σ|terms| for the FP16 rounding of the
+    weights. Each rounded weight is within 2^-11 of its FP32 value (the worst-case envelope
+    2^-11·Σ|terms|); the errors of thousands of independently rounded weights cancel, and
+    the measured deviation (printed, run with -s) stays far below half that envelope;
   * the reference's own prefill parity tests (vulkan/kernels/matmul/prefill/mod.rs:160-300,
     330-450): their weight/activation generators and shapes, their bar
     |got - want| <= 5e-2 or <= 5e-3·max(|want|, 1) (mod.rs:275,440).
@@ -55,13 +57,18 @@ def _check_fp64(fmt, w, a16, got, rows, in_dim, n, what, f16_weights=True):
 def _check_reference(fmt, w, a16, got, rows, in_dim, n, what, tokens=None):
     tokens = range(n) if tokens is None else tokens
     deq = O.dequant(fmt, w, rows, in_dim).astype(np.float64)
+    worst = 0.0
     for t in tokens:
         x = a16[t * in_dim:(t + 1) * in_dim]
         want = O.f32(O.matmul_batched(fmt, x, w, in_dim, rows, 1)).astype(np.float64)
         terms = np.abs(deq) @ np.abs(O.f32(x).astype(np.float64))
-        tol = 1e-3 * np.abs(want) + (2e-6 + 2.0 ** -11) * terms
-        bad = np.abs(got[t] - want) > tol
+        tol = 1e-3 * np.abs(want) + (2e-6 + 2.0 ** -12) * terms
+        dev = np.abs(got[t] - want)
+        worst = max(worst, float(np.max(np.maximum(dev - 1e-3 * np.abs(want), 0.0) / terms)))
+        bad = dev > tol
         assert not bad.any(), f"{what} token {t}: {bad.sum()} outside the FP16-weight envelope"
+    print(f"{what}: worst deviation from the reference kernel beyond the output rounding "
+          f"= {worst:.3e}·Σ|terms| (envelope 2^-11 = {2.0 ** -11:.3e}, bar 2^-12 + 2e-6)")
 
 
 def _reference_bar(got, want, what):

@@ -290,9 +290,10 @@ def test_matmul_batched_invariants(ora, fmt):
 
 
 # ---------------------------------------------------------------- attention
-def _pattern(expr, n):
+def _pattern(spec, n):
+    """The reference's test generator value(i) = (i % mod) * scale + offset."""
     i = np.arange(n)
-    return eval(expr, {"i": i}).astype(np.float32)
+    return ((i % int(spec["mod"])) * float(spec["scale"]) + float(spec["offset"])).astype(np.float32)
 
 
 def test_attention_hand_computed_softmax(ora, goldens):
@@ -497,3 +498,98 @@ def test_graph_batched_prefill_matches_sequential_decode(ora, goldens):
     assert np.max(np.abs(a - b)) <= goldens["graph_batched_vs_sequential"]["abs_tol"]
     seq.close()
     bat.close()
+
+
+# ---------------------------------------------------------------- residual_add (closed form)
+def test_residual_add_closed_form(ora):
+    """residual.rs:12-22: x[i] += f32(y[i]) for i < n, x beyond n untouched. numpy's IEEE
+    single-precision add of the exactly widened FP16 value is the closed form, bit for bit,
+    over random values, every FP16 pattern (signed zeros, subnormals, infinities, NaNs) and
+    FP32 specials on the x side."""
+    rng = np.random.default_rng(17)
+    y = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x_specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.4e38, -3.4e38,
+                           65504.0, 2.0 ** -24], np.float32)
+    x = np.concatenate([x_specials, rng.standard_normal(65536 - x_specials.size).astype(np.float32)
+                        * np.float32(100.0)])
+    rng.shuffle(x)
+    for n in (65536, 65536 - 5, 0):
+        got = x.copy()
+        ora.lib().gho_residual_add(got.ctypes.data, y.ctypes.data, n)
+        with np.errstate(invalid="ignore", over="ignore"):
+            want = x.copy()
+            want[:n] = x[:n] + y[:n].view(np.float16).astype(np.float32)
+        gb, wb = got.view(np.uint32), want.view(np.uint32)
+        nan = np.isnan(want)
+        assert np.array_equal(gb[~nan], wb[~nan]), n
+        assert np.all(np.isnan(got[nan]))
+        assert np.array_equal(gb[n:], x.view(np.uint32)[n:])
+    # -0.0 + y is y itself for every non-NaN FP16 pattern: the exact widening
+    z = np.full(65536, -0.0, np.float32)
+    ora.lib().gho_residual_add(z.ctypes.data, y.ctypes.data, 65536)
+    ok = ~np.isnan(y.view(np.float16))
+    assert np.array_equal(z.view(np.uint32)[ok], y.view(np.float16).astype(np.float32).view(np.uint32)[ok])
+
+
+# ---------------------------------------------------------------- graph: op trace
+def expected_op_trace(golden, blocks, dedicated):
+    """The reference's recorded forward::token trace (graph/shape.rs:389-446) for `blocks`
+    blocks, expanded from the golden's head / per-layer / tail entries."""
+    out = list(golden["head"])
+    for layer in range(blocks):
+        out += [op.replace("{layer}", str(layer)) for op in golden["layer"]]
+    out += [op.replace("{output}", "output" if dedicated else "token_embd") for op in golden["tail"]]
+    return out
+
+
+@pytest.fixture(scope="module")
+def op_trace_golden():
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "reference_op_trace.json")) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("row", [0, 1, 2])
+def test_graph_op_trace_matches_reference(ora, op_trace_golden, row):
+    """The oracle graph's op trace for one decode token equals the reference's shape-recorder
+    trace for each REFERENCE_ROWS entry (block count, dedicated or tied output). Op names are
+    the names of the tensors the ops were handed, so a layer reading another layer's or role's
+    weight shows up. Widths are reduced (the trace does not depend on them)."""
+    blocks, _, _, dedicated = op_trace_golden["reference_rows"][row]
+    shape = synth.Shape("trace", blocks, 256, 256, head_count=2, kv_head_count=1, vocab_size=64)
+    ts = [t for t in synth.model_tensors(shape, 50 + row)
+          if dedicated or not (t[0] == 0xFFFFFFFF and t[1] == 18)]
+    from test_oracle import oracle_model  # noqa: F401 (same module; keeps the helper shared)
+    om, _ = oracle_model(shape, 0, 8, generated=ts)
+    om.set_trace(True)
+    om.token(3, 0)
+    got = om.trace()
+    om.close()
+    assert got == expected_op_trace(op_trace_golden, blocks, dedicated)
+
+
+# ---------------------------------------------------------------- graph: closed form
+@pytest.mark.parametrize("variant", ["zero_ffn", "zero_o"])
+@pytest.mark.parametrize("tied", [False, True], ids=["dedicated", "tied"])
+def test_graph_closed_form_one_layer(ora, variant, tied):
+    """The oracle graph's logits equal the fp64 closed form of a one-layer model whose down
+    (zero_ffn) or O (zero_o) matrix is zero, for the dedicated and the tied output; each
+    planted wiring mistake moves the closed form far outside the tolerance, so the agreement
+    pins the wiring (V not K, the right norm per block, gate/up roles, the residual, the
+    output matrix)."""
+    import closed_form as CF
+    ts = CF.tensors(variant, tied, 60 + 2 * (variant == "zero_o") + tied)
+    om = CF.oracle_model(ts)
+    for token in (3, 1777):
+        om.token(token, 0)
+        got = om.logits()
+        want = CF.logits(ts, variant, token)
+        assert np.all(np.isfinite(want)) and np.std(want) > 0.1
+        assert CF.error(got, want) < CF.TOL, (variant, tied, token, CF.error(got, want))
+        plants = ["norm_swap", "drop_residual", "wrong_output"]
+        plants += ["k_for_v"] if variant == "zero_ffn" else ["gate_up_swap"]
+        for plant in plants:
+            bad = CF.logits(ts, variant, token, plant=plant)
+            assert CF.error(bad, want) > 5 * CF.TOL, (plant, CF.error(bad, want))
+    om.close()
