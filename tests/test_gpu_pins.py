@@ -143,7 +143,8 @@ def test_f16_narrowing_sweep_on_device(hip):
     assert np.array_equal(got, O.silu_mul(g, u))
     # the sweep reaches the cases it is for
     half = (prod.view(np.uint32) & 0x1FFF) == 0x1000
-    assert (np.isinf(prod.astype(np.float16)) & np.isfinite(prod)).any()  # overflow
+    with np.errstate(over="ignore"):
+        assert (np.isinf(prod.astype(np.float16)) & np.isfinite(prod)).any()  # overflow
     assert (np.abs(prod) < 2.0 ** -14).any() and half.sum() > 100       # subnormals, ties
     for b in (gb, ub, ob):
         hip.free_buffer(b)
