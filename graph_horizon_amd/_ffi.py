@@ -113,6 +113,7 @@ SIGNATURES = {
     "gh_silu_mul": (I32, [P, P, BUFP, BUFP, BUFP, U32]),
     "gh_residual_add": (I32, [P, P, BUFP, BUFP, U32]),
     "gh_attention_decode": (I32, [P, P, BUFP, BUFP, C.POINTER(GhKv), U32, U32, U32]),
+    "gh_attention_decode_noalloc": (I32, [P, P, BUFP, BUFP, C.POINTER(GhKv), U32, U32, U32]),
     "gh_attention_prefill": (I32, [P, P, BUFP, BUFP, C.POINTER(GhKv), U32, U32, U32, U32]),
     "gh_read_logits": (I32, [P, BUFP, U64, P]),
     "gh_read_argmax": (I32, [P, BUFP, U64, C.POINTER(U32)]),

@@ -49,6 +49,7 @@ const KernelName kKernels[] = {
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
+    {K_FILL_U32, "gh_fill_u32"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -71,18 +72,6 @@ inline uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1)
 
 bool is_weight(const gh_buf* w) {
     return w && w->kind == GH_BUF_WEIGHT && (w->format == GH_FMT_Q4_K || w->format == GH_FMT_Q6_K);
-}
-
-int check_enc(gh_backend* b, gh_encoder* enc) {
-    if (!b) return GH_E_INVALID;
-    if (!enc || enc != &b->enc || !b->enc_open) return gh::fail(b, GH_E_STATE, "no open encoder");
-    return GH_OK;
-}
-
-// Record an op's status in the encoder (errors surface again at gh_submit).
-int latch(gh_encoder* enc, int rc) {
-    if (rc != GH_OK && enc && enc->latched == GH_OK) enc->latched = rc;
-    return rc;
 }
 
 bool fits(const gh_buf* buf, uint64_t bytes) { return buf && buf->addr && buf->bytes >= bytes; }
@@ -142,6 +131,17 @@ namespace gh {
 int fail(gh_backend* b, int code, const std::string& msg) {
     if (b) b->err = msg;
     return code;
+}
+
+int check_enc(gh_backend* b, gh_encoder* enc) {
+    if (!b) return GH_E_INVALID;
+    if (!enc || enc != &b->enc || !b->enc_open) return fail(b, GH_E_STATE, "no open encoder");
+    return GH_OK;
+}
+
+int latch(gh_encoder* enc, int rc) {
+    if (rc != GH_OK && enc && enc->latched == GH_OK) enc->latched = rc;
+    return rc;
 }
 
 int hip_check(gh_backend* b, hipError_t e, const char* what) {
@@ -297,7 +297,7 @@ constexpr uint32_t kAttnPrefillMinRows = 32;
 
 int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
                  uint32_t q_heads, uint32_t base, uint32_t rows, uint32_t layer,
-                 const void* pos_ptr, uint32_t max_pos) {
+                 const void* pos_ptr, uint32_t max_pos, const AttnScratch* fixed) {
     const uint32_t group = q_heads / kv->kv_heads;
     GhKernel k;
     switch (group) {
@@ -329,14 +329,27 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         return launch(b, K_ATTN_PREFILL_G4, ceil_div(rows, 32), kv->kv_heads, 1, 256, &a);
     }
     const uint32_t splits = attention_splits(b, max_pos + 1, kv->kv_heads, rows);
-    // bound the partials: rows in groups that fit a 256 MiB workspace
-    const size_t per_row = attention_workspace(1, q_heads, splits);
-    uint32_t group_rows = (uint32_t)std::max<size_t>(1, ((size_t)256 << 20) / per_row);
-    group_rows = std::min(group_rows, rows);
-    int rc = ensure_workspace(b, attention_workspace(group_rows, q_heads, splits));
-    if (!rc) rc = ensure_counters(b, (size_t)group_rows * kv->kv_heads);
-    if (rc) return rc;
-    char* ws = (char*)b->ws + kArgmaxBytes;
+    char* ws = nullptr;
+    void* counters = nullptr;
+    uint32_t group_rows = rows;
+    int rc = GH_OK;
+    if (fixed) {
+        if (attention_workspace(rows, q_heads, splits) > fixed->part_bytes ||
+            (size_t)rows * kv->kv_heads > fixed->counter_slots)
+            return fail(b, GH_E_RANGE, "attention: launch needs more scratch than the caller's");
+        ws = fixed->parts;
+        counters = fixed->counters;
+    } else {
+        // bound the partials: rows in groups that fit a 256 MiB workspace
+        const size_t per_row = attention_workspace(1, q_heads, splits);
+        group_rows = (uint32_t)std::max<size_t>(1, ((size_t)256 << 20) / per_row);
+        group_rows = std::min(group_rows, rows);
+        rc = ensure_workspace(b, attention_workspace(group_rows, q_heads, splits));
+        if (!rc) rc = ensure_counters(b, (size_t)group_rows * kv->kv_heads);
+        if (rc) return rc;
+        ws = (char*)b->ws + kArgmaxBytes;
+        counters = b->counters;
+    }
     for (uint32_t r0 = 0; r0 < rows; r0 += group_rows) {
         const uint32_t nr = std::min(group_rows, rows - r0);
         const size_t n = (size_t)nr * q_heads * splits;
@@ -349,7 +362,7 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.part_l = (uint64_t)(ws + n * 4);
         a.part_acc = (uint64_t)(ws + n * 8);
         a.pos_ptr = (uint64_t)pos_ptr;
-        a.counters = (uint64_t)b->counters;
+        a.counters = (uint64_t)counters;
         a.key_dim = kv->head_dim;
         a.value_dim = kv->value_dim;
         a.kv_heads = kv->kv_heads;
@@ -367,6 +380,19 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
                        "hipModuleLaunchKernel");
         if (rc) return rc;
     }
+    return GH_OK;
+}
+
+int check_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
+                    uint32_t q_heads, uint32_t last_pos, uint32_t rows, uint32_t layer) {
+    if (!kv || kv->scheme != GH_KV_F16) return fail(b, GH_E_UNSUPPORTED, "attention: only the f16 KV scheme");
+    if (kv->head_dim != 128 || kv->value_dim != 128) return fail(b, GH_E_UNSUPPORTED, "attention: head_dim 128 only");
+    if (kv->kv_heads == 0 || q_heads % kv->kv_heads) return fail(b, GH_E_INVALID, "attention: q_heads not a multiple of kv_heads");
+    if (layer >= kv->block_count || last_pos >= kv->context) return fail(b, GH_E_RANGE, "attention: position beyond context");
+    const uint64_t cache = (uint64_t)kv->block_count * kv->context * kv->kv_heads * 128 * 2;
+    if (!fits(&kv->k, cache) || !fits(&kv->v, cache)) return fail(b, GH_E_RANGE, "attention: cache too small");
+    if (!fits(q, (uint64_t)rows * q_heads * 256) || !fits(out, (uint64_t)rows * q_heads * 256))
+        return fail(b, GH_E_RANGE, "attention: buffer too small");
     return GH_OK;
 }
 
@@ -589,6 +615,7 @@ int gh_create(const gh_config* cfg, gh_backend** out) {
         b->fn[kn.id] = f;
     }
     if (!rc) rc = ensure_workspace(b, 0);
+    if (!rc) rc = noalloc_init(b);
     if (rc) {
         gh_destroy(b);
         return rc;
@@ -940,18 +967,6 @@ int gh_residual_add(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_bu
     return latch(enc, launch(b, K_RESIDUAL_ADD, ceil_div(n, 256), 1, 1, 256, &a));
 }
 
-static int check_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
-                           uint32_t q_heads, uint32_t last_pos, uint32_t rows, uint32_t layer) {
-    if (!kv || kv->scheme != GH_KV_F16) return fail(b, GH_E_UNSUPPORTED, "attention: only the f16 KV scheme");
-    if (kv->head_dim != 128 || kv->value_dim != 128) return fail(b, GH_E_UNSUPPORTED, "attention: head_dim 128 only");
-    if (kv->kv_heads == 0 || q_heads % kv->kv_heads) return fail(b, GH_E_INVALID, "attention: q_heads not a multiple of kv_heads");
-    if (layer >= kv->block_count || last_pos >= kv->context) return fail(b, GH_E_RANGE, "attention: position beyond context");
-    const uint64_t cache = (uint64_t)kv->block_count * kv->context * kv->kv_heads * 128 * 2;
-    if (!fits(&kv->k, cache) || !fits(&kv->v, cache)) return fail(b, GH_E_RANGE, "attention: cache too small");
-    if (!fits(q, (uint64_t)rows * q_heads * 256) || !fits(out, (uint64_t)rows * q_heads * 256))
-        return fail(b, GH_E_RANGE, "attention: buffer too small");
-    return GH_OK;
-}
 
 int gh_attention_decode(gh_backend* b, gh_encoder* enc, const gh_buf* out, const gh_buf* q,
                         const gh_kv* kv, uint32_t q_heads, uint32_t pos, uint32_t layer) {

@@ -69,6 +69,7 @@ enum GhKernel : int {
     K_GEMM3_Q6K_R96,
     K_TOPK_PARTIAL,
     K_TOPK_FINAL,
+    K_FILL_U32,
     K_COUNT
 };
 
@@ -107,6 +108,7 @@ struct gh_backend {
     size_t counter_slots = 0;
     GhRopeTable rope;  // the trait ops' table (gh_rope_yarn, gh_rope_yarn_batched)
     uint32_t attn_splits = 0;  // gh_set_attention_splits: 0 = attention_splits' policy
+    void* noalloc_scratch = nullptr;  // this device's copy of the no-allocation scratch array
     uint64_t gen = 0;  // bumped whenever the workspace or rope table moves (captured graphs hold them)
 };
 
@@ -120,6 +122,14 @@ inline int total_key(float f) {
 }
 
 int fail(gh_backend* b, int code, const std::string& msg);
+// 0 when enc is b's open encoder, else a latched GH_E_STATE
+int check_enc(gh_backend* b, gh_encoder* enc);
+// records an op's status in the encoder (reported again by gh_submit)
+int latch(gh_encoder* enc, int rc);
+int check_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
+                    uint32_t q_heads, uint32_t last_pos, uint32_t rows, uint32_t layer);
+// Resolves this device's address of the no-allocation scratch array (at gh_create).
+int noalloc_init(gh_backend* b);
 int hip_check(gh_backend* b, hipError_t e, const char* what);
 int launch(gh_backend* b, GhKernel k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
            const void* args, uint32_t shmem = 0);
@@ -136,9 +146,19 @@ int op_rope(gh_backend* b, const GhRopeTable& t, const gh_buf* x, uint32_t heads
             uint32_t head_dim, uint32_t base, uint32_t rows, uint32_t role, const void* pos_ptr);
 int op_kv_write(gh_backend* b, const gh_kv* kv, const gh_buf* k, const gh_buf* v,
                 uint64_t k_elem_off, uint64_t v_elem_off, uint32_t vectors, const void* pos_ptr);
+// Caller-provided attention scratch: split partials and merge counters (zero on entry; every
+// launch leaves them zero).
+struct AttnScratch {
+    char* parts;
+    size_t part_bytes;
+    void* counters;
+    size_t counter_slots;
+};
+// fixed: use this scratch instead of the backend's growable workspace (GH_E_RANGE when the
+// launch needs more than it holds).
 int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
                  uint32_t q_heads, uint32_t base, uint32_t rows, uint32_t layer,
-                 const void* pos_ptr, uint32_t max_pos);
+                 const void* pos_ptr, uint32_t max_pos, const AttnScratch* fixed = nullptr);
 int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, uint32_t embd,
              const void* token_ptr);
 int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2);

@@ -67,6 +67,13 @@ GH_KERNEL __launch_bounds__(256) void gh_residual_add(GhEltArgs a) {
     x[i] = x[i] + gh_h2f(((const uint16_t*)a.b)[i]);
 }
 
+// Fill n u32 words at `out` with the value `pad`: a clear that a captured graph records as a
+// kernel node, not a memset node.
+GH_KERNEL __launch_bounds__(256) void gh_fill_u32(GhEltArgs a) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < a.n) gh_gpw<uint32_t>(a.out)[i] = a.pad;
+}
+
 // kv_write f16 (cpu/kernels/attention/write.rs:50-63): raw FP16 copy of K and V into the
 // caches at element offsets; with pos_ptr the offsets advance by stride * (*pos_ptr).
 GH_KERNEL __launch_bounds__(256) void gh_kv_write(GhKvWriteArgs a) {

@@ -176,6 +176,18 @@ int gh_attention_prefill(gh_backend* b, gh_encoder* enc, const gh_buf* out, cons
                          const gh_kv* kv, uint32_t q_heads, uint32_t base, uint32_t n,
                          uint32_t layer);
 
+/* attention_decode without allocation. No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same arguments, kernels and results as gh_attention_decode; the
+ * split partials and merge counters live in a fixed 1 MiB device array per GPU (4 KiB of
+ * counters, then q_heads x splits x 520 B of partials — 32 query heads at the 32-split
+ * maximum use 532 KiB), and launches that need more are rejected with GH_E_RANGE. Nothing is
+ * allocated. Calls on one GPU share the array: calls that overlap on the same GPU (other
+ * streams or backends) race. */
+int gh_attention_decode_noalloc(gh_backend* b, gh_encoder* enc, const gh_buf* out,
+                                const gh_buf* q, const gh_kv* kv, uint32_t q_heads, uint32_t pos,
+                                uint32_t layer);
+
 /* ---- read-back, contract.rs:300-318 (synchronous) ---- */
 int gh_read_logits(gh_backend* b, const gh_buf* logits, uint64_t vocab, float* dst);
 /* lowest index wins on equal logits (strict `>`) */
