@@ -1,5 +1,6 @@
 #!/usr/bin/env python3
-"""Benchmark of the gfx950 hot path: 8B-shaped Q4_K_M decode at bs=1 on one MI355X.
+"""Benchmark of the gfx950 hot path on one MI355X: the Q4_K decode GEMV (
+4096x4096) and 8B-shaped Q4_K_M decode at bs=1.
 
 A step is one greedy decode token of a random-init 8B-shaped decoder (34 blocks of the
 BASELINE configs[1] decode-step linear layers — Q/K/O/gate/up Q4_K, V/down Q6_K, d_model
@@ -8,11 +9,14 @@ attention, the Q6_K 131072x4096 output and the on-device argmax), replayed as on
 with weights and KV resident in HBM. `value` is tokens/s over exactly --steps timed steps.
 
 Also reported on the same line:
-  roofline      the dominant kernel (the Q4_K decode GEMV at the FFN gate/up shape,
-                12288x4096) timed with HIP events on the backend stream over the 68 distinct
-                gate/up weights of the model (1.9 GB, so the 256 MB MALL cannot serve them);
-  cpu_baseline  the CPU oracle (a C++ restatement of the reference's AVX2 CPU kernels) on a
-                bounded sample: one block's decode linear layers, scaled to tokens/s.
+  roofline      the metric's GEMV: Q4_K 4096x4096 with x ~ N(0,1), launched back to
+                back over the model's 68 distinct Q and O weights (642 MB, beyond the 256 MB
+                MALL), timed with HIP events on the backend stream;
+  config        the 12288x4096 gate/up-shape GEMV, the C3 prefill GEMMs, the C4 attention cases
+                and the C5 14B-shaped decoder (512-token prefill, greedy decode);
+  cpu_baseline  the CPU oracle (a C++ restatement of the reference's AVX2 CPU kernels) on all
+                host cores: greedy decode steps of the same 8B model, resumed from the GPU's
+                512-token KV cache, for a bounded time; plus the C1 GEMV and C4 decode attention.
 """
 from __future__ import annotations
 
@@ -29,6 +33,13 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Q4_K GEMV GB/s (% HBM peak); 8B-shaped Q4_K_M decode tok/s at bs=1"
 HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+# HBM bytes per launch of the roofline kernel (gh_gemv_q4k_r2_d at 4096x4096), from the two
+# rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --traffic-probe`, each scaled by
+# the same counter's reading for a 256 MiB device-to-device copy (profiles/q4k_gemv_c1_4096x4096.txt).
+# Re-measure whenever the kernel changes.
+ROOFLINE_TRAFFIC_BYTES = 9605002
 
 
 def log(*a):
@@ -47,49 +58,80 @@ def weight_bytes(shape):
     return per_block, shape.block_count * per_block + out
 
 
-def cpu_baseline(shape, seconds: float):
-    """Oracle GEMVs of one block's decode linear layers, rotated over 3 distinct blocks."""
-    import oracle as O
-    from graph_horizon_amd import synth
-
-    threads = min(len(os.sched_getaffinity(0)), 16)
-    O.lib().gho_set_threads(threads)
-    rng = np.random.default_rng(99)
-    blocks = []
-    for _ in range(3):
-        mats = []
-        for t, fmt in synth.LAYER_FORMATS.items():
-            ind, outd = synth.tensor_dims(shape, t)
-            mats.append((fmt, synth.quant_blocks(rng, fmt, outd, ind, 0.02), ind, outd))
-        blocks.append(mats)
-    xs = {n: O.f16(rng.standard_normal(n).astype(np.float32))
-          for n in (shape.embedding_length, shape.feed_forward_length,
-                    shape.head_count * shape.head_dim)}
-
-    def one(b):
-        for fmt, w, ind, outd in blocks[b % 3]:
-            O.matmul(fmt, xs[ind], w, ind, outd)
-
-    one(0)
-    t0 = time.perf_counter()
-    n = 0
-    while time.perf_counter() - t0 < seconds:
-        one(n)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    per_block, per_token = weight_bytes(shape)
-    tok_s = 1.0 / (dt * per_token / per_block)
-    cpu_model = ""
+def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
-            cpu_model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+            return next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
     except Exception:
-        pass
-    return {"value": round(tok_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} passes of one 8B-shaped block's 7 decode GEMVs ({per_block} B, "
-                      f"rotated over 3 blocks), {dt * 1e3:.2f} ms/block, scaled by the "
-                      f"{per_token} B/token weight stream; {cpu_model}",
-            "gbps": round(per_block / dt / 1e9, 2)}
+        return "unknown CPU"
+
+
+def cpu_baseline(shape, tensors, kv, kv_context, prompt_len, first, seconds):
+    """The oracle on every core of the affinity set: greedy decode steps of the bench's 8B model
+    resumed from the GPU's KV cache of the prompt (positions < prompt_len), for about `seconds`;
+    then the C1 GEMV over distinct Q/O weights and C4 decode attention at ctx 4096 / 32768."""
+    import oracle as O
+    from graph_horizon_amd import synth
+    from graph_horizon_amd import _ffi as F
+
+    cores = len(os.sched_getaffinity(0))
+    O.lib().gho_set_threads(cores)
+    table = {("g", tid) if layer == F.NO_LAYER else (layer, tid): (fmt, data)
+             for layer, tid, fmt, data in tensors}
+    y = synth.yarn_params(shape)
+    cfg = O.ModelCfg(shape.block_count, max(kv_context, 32768), shape.embedding_length,
+                     shape.feed_forward_length, shape.head_count, shape.kv_head_count,
+                     shape.head_dim, shape.head_dim, shape.vocab_size, 1e-5, O.Yarn(**y))
+    om = O.Model(cfg, table, kv_context)
+    om.load_kv(kv[0], kv[1], kv_context, prompt_len)
+    tok, pos, steps = first, prompt_len, 0
+    t0 = time.perf_counter()
+    while (steps < 4 or time.perf_counter() - t0 < seconds) and pos < kv_context:
+        om.token(tok, pos)
+        tok = int(np.argmax(om.logits()))
+        pos += 1
+        steps += 1
+    dt = (time.perf_counter() - t0) / steps
+    om.close()
+    _, per_token = weight_bytes(shape)
+    # C1: Q4_K 4096x4096 GEMV over the model's distinct Q and O weights (FP32 out, logits)
+    d = shape.embedding_length
+    ws = [data for layer, tid, fmt, data in tensors
+          if layer != F.NO_LAYER and tid in (F.T_ATTN_Q, F.T_ATTN_OUTPUT)]
+    rng = np.random.default_rng(3)
+    x16 = O.f16(rng.standard_normal(d).astype(np.float32))
+    n, t1 = 0, time.perf_counter()
+    while n < len(ws) or time.perf_counter() - t1 < 2.0:
+        O.logits(F.FMT_Q4_K, x16, ws[n % len(ws)], d, d)
+        n += 1
+    c1_s = (time.perf_counter() - t1) / n
+    c1_bytes = d * (d // 256) * 144 + d * 2 + d * 4
+    # C4: decode attention, 32 q / 8 kv heads x 128, f16 KV N(0,1), pos = ctx - 1
+    attn = {}
+    for ctx in (4096, 32768):
+        kc = O.f16(rng.standard_normal(ctx * 8 * 128).astype(np.float32))
+        vc = O.f16(rng.standard_normal(ctx * 8 * 128).astype(np.float32))
+        q = O.f16(rng.standard_normal(32 * 128).astype(np.float32))
+        n, t2 = 0, time.perf_counter()
+        while n < 3 or time.perf_counter() - t2 < 1.0:
+            O.attention_decode(q, kc, vc, 128, 8, 32, ctx - 1, 0, ctx)
+            n += 1
+        us = (time.perf_counter() - t2) / n * 1e6
+        attn[f"decode_{ctx}"] = {"avg_us": round(us, 1),
+                                 "gbps": round(2 * ctx * 8 * 128 * 2 / (us * 1e-6) / 1e9, 2)}
+    model = cpu_model()
+    log(f"bench: CPU baseline: {cores} threads ({model}): {1 / dt:.2f} tok/s, C1 "
+        f"{c1_bytes / c1_s / 1e9:.1f} GB/s, attention ctx 4096 {attn['decode_4096']['avg_us']:.0f} us")
+    return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{steps} greedy decode steps of the bench's 8B-shaped model (34 blocks with "
+                      f"attention, output GEMV and argmax) at context {prompt_len}..{pos - 1}, "
+                      f"resumed from the GPU's prompt KV cache: {dt * 1e3:.1f} ms/token "
+                      f"({per_token / dt / 1e9:.1f} GB/s of weights); {cores} threads "
+                      f"(nproc of the affinity set), {model}",
+            "q4k_gemv_c1": {"avg_us": round(c1_s * 1e6, 1), "gbps": round(c1_bytes / c1_s / 1e9, 2),
+                            "launches": n},
+            "attention_c4": attn,
+            "label": "C++ restatement of the graph_horizon CPU reference (AVX2 kernels)"}
 
 
 def main():
@@ -98,12 +140,14 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=512, help="prefilled context before decode")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shape", default="8b")
+    ap.add_argument("--no-c5", action="store_true", help="skip the 14B-shaped decoder (configs[4])")
     ap.add_argument("--launch", choices=("graph", "stream"), default="graph",
                     help="decode steps as one replayed HIP graph (default) or as direct "
                          "stream launches of the same kernels (for kernel tracers)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the roofline GEMV's timed launches (for rocprofv3 --kernel-trace)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the roofline kernel (4 distinct weights) and a 256 MiB "
                          "device copy of known size, for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE")
@@ -117,18 +161,22 @@ def main():
     from graph_horizon_amd import _ffi as F
 
     if args.traffic_probe:
-        traffic_probe(synth.SHAPES[args.shape])
+        traffic_probe(synth.SHAPES["8b"])
         return
-    shape = synth.SHAPES[args.shape]
+    shape = synth.SHAPES["8b"]
     per_block, per_token = weight_bytes(shape)
     kv_context = args.prompt + args.warmup + args.steps + 8
     hip = HipBackend(0)
     flags = F.MODEL_NO_GRAPH if args.launch == "stream" else 0
     model = HipModel(hip, synth.model_config(shape, kv_context, prefill_rows=512, flags=flags))
     t0 = time.perf_counter()
-    for layer, tid, fmt, data in synth.model_tensors(shape, seed=2024):
+    tensors = list(synth.model_tensors(shape, seed=2024))
+    for layer, tid, fmt, data in tensors:
         model.load_tensor(layer, tid, fmt, data)
-    log(f"bench: loaded {shape.name} weights in {time.perf_counter() - t0:.1f} s")
+    log(f"bench: generated and loaded {shape.name} weights in {time.perf_counter() - t0:.1f} s")
+    if args.roofline_only:
+        log(f"bench: roofline {json.dumps(c1_roofline(hip, model, shape))}")
+        return
 
     rng = np.random.default_rng(7)
     prompt = rng.integers(0, shape.vocab_size, args.prompt).astype(np.uint32)
@@ -140,45 +188,22 @@ def main():
     log(f"bench: prefill {args.prompt} tokens in {prefill_ms:.2f} ms "
         f"({args.prompt / (prefill_ms / 1e3):.0f} tok/s)")
     first = model.read_argmax()
+    kv = model.kv()
+    n_kv = shape.block_count * kv_context * shape.kv_head_count * shape.head_dim
+    kv_host = (hip.download(kv.k, np.uint16, n_kv), hip.download(kv.v, np.uint16, n_kv))
     pos = args.prompt
+    tok = first
     if args.warmup:
-        out = model.decode_greedy(first, pos, args.warmup)
-        first, pos = int(out[-1]), pos + args.warmup
+        out = model.decode_greedy(tok, pos, args.warmup)
+        tok, pos = int(out[-1]), pos + args.warmup
     hip.synchronize()
     hip.timer_start()
-    toks = model.decode_greedy(first, pos, args.steps)
+    model.decode_greedy(tok, pos, args.steps)
     ms = hip.timer_stop()
-    hip.synchronize()
     tok_s = args.steps / (ms / 1e3)
     log(f"bench: {args.steps} decode steps in {ms:.2f} ms -> {tok_s:.1f} tok/s")
 
-    # Dominant kernel: Q4_K decode GEMV at the gate/up shape over the model's own weights.
-    d, ffn = shape.embedding_length, shape.feed_forward_length
-    xb = hip.from_host(synth.f16_bits(rng.standard_normal(d)))
-    yb = hip.alloc_buffer(ffn * 2)
-    lib = hip.lib
-    import ctypes as C
-
-    weights = []
-    for li in range(shape.block_count):
-        for tid in (F.T_FFN_GATE, F.T_FFN_UP):
-            weights.append(model_weight(model, li, tid))
-    enc = hip.begin()
-    for w in weights[:4]:
-        lib.gh_matmul(hip.h, enc, C.byref(yb), C.byref(xb), C.byref(w), d, ffn)
-    hip.submit()
-    reps = 3
-    enc = hip.begin()
-    hip.timer_start()
-    for _ in range(reps):
-        for w in weights:
-            lib.gh_matmul(hip.h, enc, C.byref(yb), C.byref(xb), C.byref(w), d, ffn)
-    gemv_ms = hip.timer_stop() / (reps * len(weights))
-    hip.submit()
-    gemv_bytes = ffn * (d // 256) * 144 + d * 2 + ffn * 2
-    gemv_gbps = gemv_bytes / (gemv_ms * 1e-3) / 1e9
-    log(f"bench: Q4_K GEMV {ffn}x{d}: {gemv_ms * 1e3:.2f} us, {gemv_gbps:.0f} GB/s")
-
+    roofline = c1_roofline(hip, model, shape)
     result = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -193,86 +218,30 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded random-init Q4_K_M weights, random prompt ids)",
         "config": {
-            "workload": f"{shape.name}-shaped Q4_K_M decoder, greedy decode bs=1 "
-                        f"({shape.block_count} blocks"
-                        f"{' of BASELINE configs[1]' if shape.name == '8b' else ''}"
-                        f"{'; BASELINE configs[4]' if shape.name == '14b' else ''}: d {d}, FFN {ffn}, "
-                        f"32/8 heads x 128, Q/K/O/gate/up Q4_K, V/down Q6_K; Q6_K output "
-                        f"{shape.vocab_size}x{d}); context {args.prompt}..{pos + args.steps}; "
-                        f"{args.launch} launch",
+            "workload": f"8b-shaped Q4_K_M decoder, greedy decode bs=1 ({shape.block_count} "
+                        f"blocks of BASELINE configs[1]: d {shape.embedding_length}, FFN "
+                        f"{shape.feed_forward_length}, 32/8 heads x 128, Q/K/O/gate/up Q4_K, "
+                        f"V/down Q6_K; Q6_K output {shape.vocab_size}x{shape.embedding_length}); "
+                        f"context {args.prompt}..{pos + args.steps}; {args.launch} launch",
             "weight_bytes_per_token": per_token,
             "prefill": {"tokens": args.prompt, "ms": round(prefill_ms, 3),
                         "tok_s": round(args.prompt / (prefill_ms / 1e3), 1)},
             "decode_weight_roofline_frac": round(per_token * tok_s / (HBM_PEAK_GBPS * 1e9), 4),
-            "q4k_gemv_c1_shape": None,
+            "q4k_gemv_12288x4096": gemv_gate_shape(hip, model, shape),
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(gemv_gbps, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": ROOFLINE_TRAFFIC_BYTES if (d, ffn) == (4096, 12288) else None,
-            "kernel": f"{gemv_kernel_name(d, ffn)} (Q4_K GEMV {ffn}x{d}, {gemv_bytes} B/launch)",
-            "avg_us": round(gemv_ms * 1e3, 3),
-        },
+        "roofline": roofline,
     }
-    c1 = c1_gemv(hip, model, shape)
-    result["config"]["q4k_gemv_c1_shape"] = c1
     result["config"]["prefill_gemm_c3"] = prefill_gemm(hip, model, shape, 512)
     model.close()
-    result["config"]["attention_c4"] = c4_attention(hip, shape)
+    result["config"]["attention_c4"] = c4_attention(hip)
+    if not args.no_c5:
+        result["config"]["decoder_c5"] = c5_decoder(hip, HipModel, args.prompt)
     hip.close()
     if not args.no_cpu:
         log("bench: CPU baseline ...")
-        result["cpu_baseline"] = cpu_baseline(shape, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(shape, tensors, kv_host, kv_context, args.prompt,
+                                              first, args.cpu_seconds)
     print(json.dumps(result), flush=True)
-
-
-def gemv_kernel_name(in_dim, rows):
-    """The kernel gh_matmul launches for one token (the host's selection in op_gemv)."""
-    if in_dim <= 4096:
-        return "gh_gemv_q4k_r1_d" if rows >= 8192 else "gh_gemv_q4k_r2_d"
-    return "gh_gemv_q4k_r2_k"
-
-
-# HBM bytes per launch of the roofline kernel (gh_gemv_q4k_r1_d at 12288x4096), from the two
-# rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --traffic-probe`, each scaled by
-# the same counter's reading for a 256 MiB device-to-device copy (FETCH_SIZE x 2.0, WRITE_SIZE
-# x 1.0): profiles/q4k_gemv_12288x4096.txt. Re-measure whenever the kernel changes.
-ROOFLINE_TRAFFIC_BYTES = 28531416
-
-
-def traffic_probe(shape):
-    """Roofline kernel launches plus a copy of known size, nothing else (for PMC passes)."""
-    import ctypes as C
-
-    from graph_horizon_amd import HipBackend, synth
-
-    hip = HipBackend(0)
-    d, ffn = shape.embedding_length, shape.feed_forward_length
-    rng = np.random.default_rng(5)
-    ws = [hip.load_weight(12, synth.quant_blocks(rng, 12, ffn, d, 0.02), d, ffn) for _ in range(4)]
-    xb = hip.from_host(synth.f16_bits(rng.standard_normal(d)))
-    yb = hip.alloc_buffer(ffn * 2)
-    enc = hip.begin()
-    for w in ws:
-        hip.lib.gh_matmul(hip.h, enc, C.byref(yb), C.byref(xb), C.byref(w), d, ffn)
-    hip.submit()
-    rt = C.CDLL("libamdhip64.so")
-    nbytes = 256 << 20
-    src, dst = C.c_void_p(), C.c_void_p()
-    assert rt.hipMalloc(C.byref(src), C.c_size_t(nbytes)) == 0
-    assert rt.hipMalloc(C.byref(dst), C.c_size_t(nbytes)) == 0
-    assert rt.hipMemset(src, 1, C.c_size_t(nbytes)) == 0
-    for _ in range(2):  # device-to-device: the runtime's blit copy kernel
-        assert rt.hipMemcpy(dst, src, C.c_size_t(nbytes), 3) == 0
-    assert rt.hipDeviceSynchronize() == 0
-    log(f"bench: traffic probe: 4 x gh_matmul {ffn}x{d} ({ffn * (d // 256) * 144} B of weights "
-        f"each), 2 x copy of {nbytes} B")
-    rt.hipFree(src)
-    rt.hipFree(dst)
-    hip.close()
 
 
 def model_weight(model, layer, tid):
@@ -287,7 +256,118 @@ def model_weight(model, layer, tid):
     return buf
 
 
-MFMA_F16_PEAK_TFLOPS = 2500.0
+def time_gemv(hip, weights, x, y, in_dim, out_dim, reps=3, each=False):
+    """gh_matmul launches over `weights` (warm-up pass first), timed with HIP events on the
+    backend stream. Returns the average microseconds per launch of back-to-back launches (the
+    period, launch gaps included) and, with each=True, of launches bracketed one by one by
+    their own event pair (the dispatch's duration, as a kernel tracer reports it)."""
+    import ctypes as C
+
+    lib = hip.lib
+    enc = hip.begin()
+    for w in weights[:4]:
+        lib.gh_matmul(hip.h, enc, C.byref(y), C.byref(x), C.byref(w), in_dim, out_dim)
+    hip.submit()
+    enc = hip.begin()
+    hip.timer_start()
+    for _ in range(reps):
+        for w in weights:
+            lib.gh_matmul(hip.h, enc, C.byref(y), C.byref(x), C.byref(w), in_dim, out_dim)
+    period = hip.timer_stop() * 1e3 / (reps * len(weights))
+    hip.submit()
+    if not each:
+        return period, None
+    total = 0.0
+    for _ in range(reps):
+        for w in weights:
+            enc = hip.begin()
+            hip.timer_start()
+            lib.gh_matmul(hip.h, enc, C.byref(y), C.byref(x), C.byref(w), in_dim, out_dim)
+            total += hip.timer_stop()
+            hip.submit()
+    return period, total * 1e3 / (reps * len(weights))
+
+
+def c1_roofline(hip, model, shape):
+    """The metric's GEMV: Q4_K 4096x4096, x ~ N(0,1) in FP16, one token,
+    over the model's 68 distinct 4096x4096 Q4_K weights (Q and O of 34 blocks, 642 MB)."""
+    from graph_horizon_amd import _ffi as F
+    from graph_horizon_amd import synth
+
+    d = shape.embedding_length
+    ws = [model_weight(model, li, t) for li in range(shape.block_count)
+          for t in (F.T_ATTN_Q, F.T_ATTN_OUTPUT)]
+    x = hip.from_host(synth.f16_bits(np.random.default_rng(11).standard_normal(d)))
+    y = hip.alloc_buffer(d * 2)
+    period, us = time_gemv(hip, ws, x, y, d, d, each=True)
+    nbytes = d * (d // 256) * 144 + d * 2 + d * 2
+    gbps = nbytes / (us * 1e-6) / 1e9
+    hip.free_buffer(x)
+    hip.free_buffer(y)
+    log(f"bench: Q4_K GEMV {d}x{d} (C1): {us:.3f} us per launch, {gbps:.0f} GB/s "
+        f"({gbps / HBM_PEAK_GBPS:.1%}); back to back {period:.3f} us")
+    return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": ROOFLINE_TRAFFIC_BYTES,
+            "kernel": f"gh_gemv_q4k_r2_d (Q4_K GEMV {d}x{d}, BASELINE configs[0], x ~ N(0,1); "
+                      f"{nbytes} algorithmic B/launch: weights {d * (d // 256) * 144} + x + y)",
+            "avg_us": round(us, 3), "period_us": round(period, 3),
+            "period_frac": round(nbytes / (period * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+            "launches": 3 * len(ws), "distinct_weights": len(ws),
+            "timing": "avg_us: each launch between its own HIP event pair on the backend stream "
+                      "(the dispatch's duration); period_us: back-to-back launches"}
+
+
+def gemv_gate_shape(hip, model, shape):
+    """The decode GEMV at the FFN gate/up shape (12288x4096) over the 68 distinct gate/up
+    weights of the model (1.9 GB)."""
+    from graph_horizon_amd import _ffi as F
+    from graph_horizon_amd import synth
+
+    d, ffn = shape.embedding_length, shape.feed_forward_length
+    ws = [model_weight(model, li, t) for li in range(shape.block_count)
+          for t in (F.T_FFN_GATE, F.T_FFN_UP)]
+    x = hip.from_host(synth.f16_bits(np.random.default_rng(12).standard_normal(d)))
+    y = hip.alloc_buffer(ffn * 2)
+    us, _ = time_gemv(hip, ws, x, y, d, ffn)
+    nbytes = ffn * (d // 256) * 144 + d * 2 + ffn * 2
+    gbps = nbytes / (us * 1e-6) / 1e9
+    hip.free_buffer(x)
+    hip.free_buffer(y)
+    log(f"bench: Q4_K GEMV {ffn}x{d}: {us:.2f} us, {gbps:.0f} GB/s")
+    return {"avg_us": round(us, 3), "gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "bytes_per_launch": nbytes, "kernel": "gh_gemv_q4k_r1_d"}
+
+
+def traffic_probe(shape):
+    """Roofline kernel launches plus a copy of known size, nothing else (for PMC passes)."""
+    import ctypes as C
+
+    from graph_horizon_amd import HipBackend, synth
+
+    hip = HipBackend(0)
+    d = shape.embedding_length
+    rng = np.random.default_rng(5)
+    ws = [hip.load_weight(12, synth.quant_blocks(rng, 12, d, d, 0.02), d, d) for _ in range(4)]
+    xb = hip.from_host(synth.f16_bits(rng.standard_normal(d)))
+    yb = hip.alloc_buffer(d * 2)
+    enc = hip.begin()
+    for w in ws:
+        hip.lib.gh_matmul(hip.h, enc, C.byref(yb), C.byref(xb), C.byref(w), d, d)
+    hip.submit()
+    rt = C.CDLL("libamdhip64.so")
+    nbytes = 256 << 20
+    src, dst = C.c_void_p(), C.c_void_p()
+    assert rt.hipMalloc(C.byref(src), C.c_size_t(nbytes)) == 0
+    assert rt.hipMalloc(C.byref(dst), C.c_size_t(nbytes)) == 0
+    assert rt.hipMemset(src, 1, C.c_size_t(nbytes)) == 0
+    for _ in range(2):  # device-to-device: the runtime's blit copy kernel
+        assert rt.hipMemcpy(dst, src, C.c_size_t(nbytes), 3) == 0
+    assert rt.hipDeviceSynchronize() == 0
+    log(f"bench: traffic probe: 4 x gh_matmul {d}x{d} ({d * (d // 256) * 144} B of weights "
+        f"each), 2 x copy of {nbytes} B")
+    rt.hipFree(src)
+    rt.hipFree(dst)
+    hip.close()
 
 
 def prefill_gemm(hip, model, shape, n):
@@ -326,8 +406,8 @@ def prefill_gemm(hip, model, shape, n):
     return out
 
 
-def c4_attention(hip, shape):
-    """GQA attention over the f16 KV cache at the model's heads — the
+def c4_attention(hip):
+    """GQA attention over the f16 KV cache (32 q / 8 kv heads x 128) — the
     2048-row causal prefill on the matrix cores, and single-token decode at ctx 4096 and 32768.
     Decode rotates over distinct layers of a >= 671 MB cache (40 x 4096 / 5 x 32768 positions),
     so the 256 MB MALL cannot serve the K/V stream. HIP-event timing on the backend stream."""
@@ -335,7 +415,7 @@ def c4_attention(hip, shape):
 
     from graph_horizon_amd import _ffi as F
 
-    qh, kvh, hd = shape.head_count, shape.kv_head_count, shape.head_dim
+    qh, kvh, hd = 32, 8, 128
     rng = np.random.default_rng(13)
     out = {}
     for ctx, layers in ((2048, 8), (4096, 40), (32768, 5)):
@@ -380,44 +460,46 @@ def c4_attention(hip, shape):
     return out
 
 
+def c5_decoder(hip, HipModel, prompt_len, steps=64):
+    """the 14B-shaped decoder (40 blocks, d 5120, FFN 16384, vocab 131072,
+    attn_v / ffn_down / output Q6_K, the rest Q4_K): a random-id prompt prefilled in one chunk,
+    then greedy decode steps as one replayed HIP graph, timed with HIP events."""
+    from graph_horizon_amd import synth
+
+    shape = synth.SHAPES["14b"]
+    _, per_token = weight_bytes(shape)
+    kv_context = prompt_len + 8 + steps + 8
+    model = HipModel(hip, synth.model_config(shape, kv_context, prefill_rows=prompt_len))
+    t0 = time.perf_counter()
+    for layer, tid, fmt, data in synth.model_tensors(shape, seed=1405):
+        model.load_tensor(layer, tid, fmt, data)
+    log(f"bench: generated and loaded 14b weights in {time.perf_counter() - t0:.1f} s")
+    prompt = np.random.default_rng(1405).integers(0, shape.vocab_size, prompt_len).astype(np.uint32)
+    model.prefill(prompt[:16], 0)
+    hip.synchronize()
+    hip.timer_start()
+    model.prefill(prompt, 0)
+    prefill_ms = hip.timer_stop()
+    out = model.decode_greedy(model.read_argmax(), prompt_len, 8)
+    hip.synchronize()
+    hip.timer_start()
+    model.decode_greedy(int(out[-1]), prompt_len + 8, steps)
+    ms = hip.timer_stop()
+    model.close()
+    tok_s = steps / (ms / 1e3)
+    log(f"bench: 14b prefill {prompt_len} tokens {prefill_ms:.2f} ms; decode {tok_s:.1f} tok/s")
+    return {"workload": "14b-shaped Q4_K_M decoder (BASELINE configs[4]: 40 blocks, d 5120, FFN "
+                        f"16384, vocab 131072), {prompt_len}-token prompt, greedy decode bs=1",
+            "prefill_ms": round(prefill_ms, 3), "prefill_tok_s": round(prompt_len / (prefill_ms / 1e3), 1),
+            "decode_tok_s": round(tok_s, 2), "decode_ms_per_step": round(ms / steps, 4),
+            "weight_bytes_per_token": per_token,
+            "decode_weight_roofline_frac": round(per_token * tok_s / (HBM_PEAK_GBPS * 1e9), 4)}
+
+
 def synth_f16(rng, count):
     from graph_horizon_amd import synth
 
     return synth.f16_bits(rng.standard_normal(count))
-
-
-def c1_gemv(hip, model, shape):
-    """BASELINE configs[0] shape (Q4_K 4096x4096): the 68 distinct Q and O weights."""
-    import ctypes as C
-
-    from graph_horizon_amd import _ffi as F
-
-    d = shape.embedding_length
-    if shape.head_count * shape.head_dim != d:
-        return None
-    ws = [model_weight(model, li, t) for li in range(shape.block_count)
-          for t in (F.T_ATTN_Q, F.T_ATTN_OUTPUT)]
-    xb = hip.from_host(np.zeros(d, np.uint16))
-    yb = hip.alloc_buffer(d * 2)
-    enc = hip.begin()
-    for w in ws[:4]:
-        hip.lib.gh_matmul(hip.h, enc, C.byref(yb), C.byref(xb), C.byref(w), d, d)
-    hip.submit()
-    enc = hip.begin()
-    hip.timer_start()
-    reps = 3
-    for _ in range(reps):
-        for w in ws:
-            hip.lib.gh_matmul(hip.h, enc, C.byref(yb), C.byref(xb), C.byref(w), d, d)
-    ms = hip.timer_stop() / (reps * len(ws))
-    hip.submit()
-    nbytes = d * (d // 256) * 144 + d * 2 + d * 2
-    gbps = nbytes / (ms * 1e-3) / 1e9
-    hip.free_buffer(xb)
-    hip.free_buffer(yb)
-    return {"shape": f"{d}x{d}", "avg_us": round(ms * 1e3, 3), "gbps": round(gbps, 1),
-            "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": nbytes,
-            "distinct_weights": len(ws)}
 
 
 if __name__ == "__main__":
