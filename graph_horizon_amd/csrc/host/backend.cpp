@@ -284,7 +284,8 @@ int ensure_counters(gh_backend* b, size_t slots) {
     b->counters = nullptr;
     b->counter_slots = 0;
     rc = hip_check(b, hipMalloc(&b->counters, slots * 4), "hipMalloc(counters)");
-    if (!rc) rc = hip_check(b, hipMemset(b->counters, 0, slots * 4), "hipMemset(counters)");
+    // on the (non-blocking) backend stream, so the clear is ordered before every launch
+    if (!rc) rc = hip_check(b, hipMemsetAsync(b->counters, 0, slots * 4, b->stream), "hipMemsetAsync(counters)");
     if (rc) return rc;
     b->counter_slots = slots;
     ++b->gen;

@@ -717,9 +717,7 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h)
         }
         ((float*)&sums[iu])[iq] = sq;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    gh_lds_barrier();
     if (gw >= h.tasks) return;  // wave-uniform
     const Masks mk = make_masks();
     for (uint32_t k = gw; k < h.tasks; k += waves) {

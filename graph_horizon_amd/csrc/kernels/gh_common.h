@@ -28,6 +28,15 @@ __device__ __forceinline__ float gh_dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(gh_as_h2(a), gh_as_h2(b), c, false);
 }
 
+// Workgroup barrier that orders LDS accesses only: unlike __syncthreads() (whose workgroup
+// fence waits for every outstanding global load and store, vmcnt(0)), global accesses stay
+// in flight across it.
+__device__ __forceinline__ void gh_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Sum across the 64 lanes of a wavefront (every lane receives the total).
 __device__ __forceinline__ float gh_wave_sum(float v) {
 #pragma unroll

@@ -128,14 +128,16 @@ def test_reference_prefill_attention_vectors(hip, context):
     _free(hip, kv.k, kv.v)
 
 
-def test_decode_every_forced_split_count(hip):
-    """Decode attention with each split count 1..32 forced (gh_set_attention_splits): the split
-    partials cross workgroups through agent-scope atomics and the last workgroup of each
-    (row, kv head) merges them. Positions below, at and across chunk boundaries, and counts
-    above the row's chunk count (the launch then has more workgroups than splits in use, as
-    in a replayed graph's fixed grid). Same bar as the oracle decode test."""
-    rng = np.random.default_rng(321)
-    ctx, layers, qh, kvh = 2048, 2, 32, 8
+@pytest.mark.parametrize("qh,kvh", [(32, 8), (8, 8), (16, 8), (64, 8)], ids=["g4", "g1", "g2", "g8"])
+def test_decode_every_forced_split_count(hip, qh, kvh):
+    """Decode attention with each split count 1..32 forced (gh_set_attention_splits), for each
+    GQA group size: the split partials cross workgroups through agent-scope atomics and the
+    last workgroup of each (row, kv head) merges them. Positions below, at and across chunk
+    boundaries, and counts above the row's chunk count (the launch then has more workgroups
+    than splits in use, as in a replayed graph's fixed grid). Same bar as the oracle decode
+    test."""
+    rng = np.random.default_rng(321 + qh)
+    ctx, layers = 2048, 2
     kc = O.f16(rng.standard_normal(layers * ctx * kvh * 128).astype(np.float32))
     vc = O.f16(rng.standard_normal(layers * ctx * kvh * 128).astype(np.float32))
     kv = _kv(hip, layers, ctx, kvh, kc, vc)
