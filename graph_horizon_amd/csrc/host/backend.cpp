@@ -329,6 +329,9 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         // 248 VGPRs keep two workgroups resident per CU)
         return launch(b, K_ATTN_PREFILL_G4, ceil_div(rows, 32), kv->kv_heads, 1, 256, &a);
     }
+    // decode reads a layer's K/V through 32-bit buffer ranges
+    if (((uint64_t)kv->context + 2048) * kv->kv_heads * kv->head_dim * 2 >= (1ull << 31))
+        return fail(b, GH_E_UNSUPPORTED, "attention: a layer's K or V cache of 2 GiB or more");
     const uint32_t splits = attention_splits(b, max_pos + 1, kv->kv_heads, rows);
     char* ws = nullptr;
     void* counters = nullptr;

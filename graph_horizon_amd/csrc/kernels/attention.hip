@@ -20,6 +20,8 @@
 
 namespace {
 constexpr uint32_t kChunk = 64;  // positions per chunk
+// Buffer resource word 3 for gfx9-family raw buffers (32-bit data format, no swizzle).
+constexpr int kBufWord3 = 0x00020000;
 constexpr int kWaves = 4;
 constexpr uint32_t kMaxSplits = 32;
 
@@ -29,26 +31,38 @@ struct ChunkRegs {
     uint32_t v[16];   // V dims 2·lane, 2·lane+1 of positions 16·wave + i
 };
 
-// Positions are clamped to lim - 1: the row's last position (lim = len), or for the first
-// chunk, whose loads go out before the position is read, the cache's last slot (lim = context).
-template <int G>
-__device__ __forceinline__ void load_chunk(const uint16_t* kc, const uint16_t* vc, size_t kv_row,
-                                           uint32_t c, uint32_t lim, ChunkRegs<G>& r) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t p0 = c * kChunk + wave * 16;
-    const uint32_t pk = min(p0 + (lane >> 2), lim - 1);
-    const GH_GLOBAL uint4* src = gh_gp<uint4>((uint64_t)(kc + (size_t)pk * kv_row + (lane & 3u) * 32));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.k[i] = src[i];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const uint32_t pv = min(p0 + (uint32_t)i, lim - 1);
-        r.v[i] = gh_gp<uint32_t>((uint64_t)(vc + (size_t)pv * kv_row))[lane];
-    }
+// K and V of one kv head are read through raw buffer resources whose range ends at position
+// lim: the row's length (lim = len), or for the first chunk, whose loads go out before the
+// position is read, the cache's context. Positions past the range read as zero without a
+// memory access, so the request for a chunk past the last (the loop's unconditional
+// prefetch) costs no round trip.
+struct KVRsrc {
+    __amdgpu_buffer_rsrc_t k, v;
+};
+__device__ __forceinline__ KVRsrc kv_rsrc(const uint16_t* kc, const uint16_t* vc, size_t kv_row, uint32_t lim) {
+    // the host keeps (context + 2048) x kv_row x 2 bytes below 2^31, so every offset below
+    // (chunks up to max(32, nchunk) + 1) fits
+    const int bytes = (int)((size_t)lim * kv_row * 2);
+    return {__builtin_amdgcn_make_buffer_rsrc((void*)kc, 0, bytes, kBufWord3),
+            __builtin_amdgcn_make_buffer_rsrc((void*)vc, 0, bytes, kBufWord3)};
 }
 
-// Zero the V values of positions >= len (slots past the row may hold anything, and their
-// weight 0 times a NaN would not be 0); their scores are replaced by -inf in chunk_step.
+template <int G>
+__device__ __forceinline__ void load_chunk(const KVRsrc& rs, uint32_t row_bytes, uint32_t c, ChunkRegs<G>& r) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t p0 = c * kChunk + wave * 16;
+    const uint32_t ok = (p0 + (lane >> 2)) * row_bytes + (lane & 3u) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.k, ok + 16 * i, 0, 0));
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        r.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rs.v, (p0 + (uint32_t)i) * row_bytes + lane * 4, 0, 0);
+}
+
+// Zero the V values of positions >= len in the first chunk, which is read before the
+// position is known (slots past the row may hold anything, and their weight 0 times a NaN
+// would not be 0); their scores are replaced by -inf in chunk_step.
 template <int G>
 __device__ __forceinline__ void mask_chunk(uint32_t c, uint32_t len, ChunkRegs<G>& r) {
     const uint32_t p0 = c * kChunk + (threadIdx.x >> 6) * 16;
@@ -139,9 +153,10 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
     const size_t cache0 = (size_t)hot.layer * hot.context * kv_row + (size_t)kvh * 128;
     const uint16_t* kc = (const uint16_t*)hot.kc + cache0;
     const uint16_t* vc = (const uint16_t*)hot.vc + cache0;
+    const uint32_t row_bytes = (uint32_t)kv_row * 2;
     // this split's first chunk (chunk `split`) is requested before the position arrives
     ChunkRegs<G> ra, rb;
-    load_chunk<G>(kc, vc, kv_row, split, hot.context, ra);
+    load_chunk<G>(kv_rsrc(kc, vc, kv_row, hot.context), row_bytes, split, ra);
     const uint32_t pos = (hot.pos_ptr ? *gh_gp<uint32_t>(hot.pos_ptr) : 0u) + a.base + row;
     const uint32_t len = pos + 1;
     const uint32_t nchunk = (len + kChunk - 1) / kChunk;
@@ -156,14 +171,17 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
         acc[h][0] = acc[h][1] = 0.0f;
     }
     // chunks split, split + nsplit, ...; a wave whose 16 positions of a chunk all lie past
-    // the row's length still runs it (every weight is 0) so the loop stays wave-uniform
+    // the row's length still runs it (every weight is 0) so the loop stays wave-uniform. The
+    // next chunk is requested unconditionally (a load under a branch makes the compiler wait
+    // for every load at the join); past the last chunk the request is out of range.
+    const KVRsrc rs = kv_rsrc(kc, vc, kv_row, len);
     for (uint32_t c = split; c < nchunk; c += 2 * nsplit) {
         const uint32_t c1 = c + nsplit, c2 = c + 2 * nsplit;
-        load_chunk<G>(kc, vc, kv_row, min(c1, nchunk - 1), len, rb);
+        load_chunk<G>(rs, row_bytes, min(c1, nchunk), rb);
         if (c == split) mask_chunk<G>(c, len, ra);  // after the next chunk's loads are out
         if (c * kChunk + wave * 16 < len) chunk_step<G>(ra, qv, a.scale, c, len, m, l, acc);
         if (c1 >= nchunk) break;
-        load_chunk<G>(kc, vc, kv_row, min(c2, nchunk - 1), len, ra);
+        load_chunk<G>(rs, row_bytes, min(c2, nchunk), ra);
         if (c1 * kChunk + wave * 16 < len) chunk_step<G>(rb, qv, a.scale, c1, len, m, l, acc);
     }
 
@@ -315,9 +333,6 @@ constexpr int kVP = kPK + 16;    // V^T tile pitch (FP16): [128 dims][64 keys, s
 __device__ __forceinline__ uint32_t vt_slot(uint32_t key) {
     return (key & ~31u) + 8 * ((key >> 2) & 3u) + 4 * ((key >> 4) & 1u) + (key & 3u);
 }
-
-// Buffer resource word 3 for gfx9-family raw buffers (32-bit data format, no swizzle).
-constexpr int kBufWord3 = 0x00020000;
 
 struct KVStage {
     uint4 k0, k1, k2, k3;  // K: chunk (key c/16, dims 8·(c%16)), c = tid + 256 i
