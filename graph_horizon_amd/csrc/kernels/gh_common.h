@@ -37,18 +37,6 @@ __device__ __forceinline__ void gh_lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Sum across the 64 lanes of a wavefront (every lane receives the total).
-__device__ __forceinline__ float gh_wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ float gh_wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
 
 #define GH_GLOBAL __attribute__((address_space(1)))
 
@@ -76,6 +64,29 @@ __device__ __forceinline__ float gh_wave_sum63(float v) {
     v += GH_DPP(v, 0x143, 0xC);  // row_bcast:31 into rows 2 and 3
     return v;
 }
+
+// Maximum across a wavefront with the same DPP steps (lanes a step does not write keep their
+// own value); the maximum lands in lane 63.
+#define GH_DPP_KEEP(v, ctrl, rmask) \
+    __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), ctrl, rmask, 0xF, false))
+__device__ __forceinline__ float gh_wave_max63(float v) {
+    v = fmaxf(v, GH_DPP_KEEP(v, 0xB1, 0xF));
+    v = fmaxf(v, GH_DPP_KEEP(v, 0x4E, 0xF));
+    v = fmaxf(v, GH_DPP_KEEP(v, 0x141, 0xF));
+    v = fmaxf(v, GH_DPP_KEEP(v, 0x140, 0xF));
+    v = fmaxf(v, GH_DPP_KEEP(v, 0x142, 0xA));
+    v = fmaxf(v, GH_DPP_KEEP(v, 0x143, 0xC));
+    return v;
+}
+
+__device__ __forceinline__ float gh_lane63(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum / maximum across the 64 lanes of a wavefront, returned to every lane (DPP steps, then
+// lane 63 read into a scalar: no LDS round trips, unlike lane shuffles through ds_bpermute).
+__device__ __forceinline__ float gh_wave_sum(float v) { return gh_lane63(gh_wave_sum63(v)); }
+__device__ __forceinline__ float gh_wave_max(float v) { return gh_lane63(gh_wave_max63(v)); }
 
 // RMSNorm scale of one FP32 row over a 256-thread workgroup, in one fixed order (each thread
 // sums its float4 chunks tid, tid + 256, ... as (x²+y²)+(z²+w²); DPP wave sums; the four wave
