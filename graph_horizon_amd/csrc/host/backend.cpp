@@ -40,8 +40,8 @@ const KernelName kKernels[] = {
     {K_SILU_MUL, "gh_silu_mul"},           {K_RESIDUAL_ADD, "gh_residual_add"},
     {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
     {K_ARGMAX_FINAL, "gh_argmax_final"},   {K_ATTN_G1, "gh_attn_g1"},
-    {K_ATTN_G2, "gh_attn_g2"},             {K_ATTN_G4, "gh_attn_g4"},
-    {K_ATTN_G8, "gh_attn_g8"},
+    {K_ATTN_G2, "gh_attn_g2"},             {K_ATTN_MFMA_G4, "gh_attn_mfma_g4"},
+    {K_ATTN_MFMA_G8, "gh_attn_mfma_g8"},
     {K_STEP_ADVANCE, "gh_step_advance"},
     {K_GEMM_Q4K_T128_R64, "gh_gemm_q4k_t128_r64"},   {K_GEMM_Q4K_T128_R128, "gh_gemm_q4k_t128_r128"},
     {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},   {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"},
@@ -304,8 +304,10 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
     switch (group) {
         case 1: k = K_ATTN_G1; break;
         case 2: k = K_ATTN_G2; break;
-        case 4: k = K_ATTN_G4; break;
-        case 8: k = K_ATTN_G8; break;
+        // four or eight query heads per kv head: the matrix-core decode (the K and value dims
+        // are 128, which check_attention and the model enforce)
+        case 4: k = K_ATTN_MFMA_G4; break;
+        case 8: k = K_ATTN_MFMA_G8; break;
         default: return fail(b, GH_E_UNSUPPORTED, "attention: GQA group must be 1, 2, 4 or 8");
     }
     // Batched prefill on the matrix cores: 32-row query blocks x kv heads (G = 4, head 128).

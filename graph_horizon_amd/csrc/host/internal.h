@@ -53,8 +53,8 @@ enum GhKernel : int {
     K_ARGMAX_FINAL,
     K_ATTN_G1,
     K_ATTN_G2,
-    K_ATTN_G4,
-    K_ATTN_G8,
+    K_ATTN_MFMA_G4,
+    K_ATTN_MFMA_G8,
     K_STEP_ADVANCE,
     // prefill GEMM tile variants (tokens x rows per workgroup), Q4_K then Q6_K
     K_GEMM_Q4K_T128_R64,

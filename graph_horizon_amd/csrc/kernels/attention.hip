@@ -4,13 +4,15 @@
 // q_heads/kv_heads query heads sharing it (each K/V row is read once for all G), and every
 // nsplit-th chunk of 64 positions of one query row (pos_r = base + r, or *pos_ptr + base + r).
 // Wave w owns positions 16 w .. 16 w + 15 of each chunk and keeps its own online-softmax
-// state, so chunks need no workgroup barrier:
-//   scores  4 lanes per position, 32 FP16 of the K row each, v_dot2_f32_f16 against the FP16
-//           query (products of FP16 values are exact in FP32), quad DPP sum, x 1/sqrt(128);
-//   softmax running max m, Σe l, Σe·V acc per head (each lane owns 2 value dims; the weights
-//           of the wave's 16 positions are broadcast with v_readlane).
-// The next chunk's K/V loads are issued before the current chunk is computed. At the end the
-// four waves merge in LDS; with one split the workgroup writes the output, otherwise it writes
+// state, so chunks need no workgroup barrier. Two forms of the per-wave work:
+//   G = 4, 8 (attn_mfma_body): scores and the weighted V sum on the matrix cores (below);
+//   G = 1, 2 (attn_body): 4 lanes per position, 32 FP16 of the K row each, v_dot2_f32_f16
+//           against the FP16 query (products of FP16 values are exact in FP32), quad DPP
+//           sum; running max m, Σe l and Σe·V per head (each lane owns 2 value dims; the
+//           weights of the wave's 16 positions are broadcast with v_readlane).
+// K and V are read through range-bounded buffer loads (kv_rsrc); the next chunk's loads are
+// issued before the current chunk is computed. At the end the four waves merge in LDS
+// (attn_finish); with one split the workgroup writes the output, otherwise it writes
 // (m, l, acc) to the workspace and the last workgroup of its (row, kv head) (agent-scope atomic
 // counter, reset by that workgroup for the next launch) merges the splits:
 //   out = Σ_s e^{m_s-M} acc_s / Σ_s e^{m_s-M} l_s,  M = max_s m_s
@@ -130,13 +132,23 @@ struct AttnHot {
     uint32_t layer, context, q_heads, kv_heads;
 };
 
+// Per-wave softmax state of a decode workgroup, merged by attn_finish.
+template <int G>
+struct AttnShared {
+    float wm[kWaves][G], wl[kWaves][G];  // running max and Σe of each wave, per head
+    float wacc[kWaves][G][128];          // Σe·V of each wave, per head and value dim
+    float wsplit[G][kMaxSplits];
+    uint32_t last;
+};
+
+template <int G>
+__device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& hot, AttnShared<G>& sh,
+                                            uint32_t nsplit);
+
 template <int G>
 __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& hot) {
-    __shared__ float wm[kWaves][G], wl[kWaves][G];
-    __shared__ float wacc[kWaves][G][128];
-    __shared__ float wsplit[G][kMaxSplits];
-    __shared__ uint32_t last;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    __shared__ AttnShared<G> sh;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
     const uint32_t h0 = kvh * G;
     // FP16 query slices [32·qd, +32) of the G heads, as 16 pairs each (issued before the
@@ -185,17 +197,34 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
         if (c1 * kChunk + wave * 16 < len) chunk_step<G>(rb, qv, a.scale, c1, len, m, l, acc);
     }
 
-    // merge the four waves: M = max m_w, L = Σ l_w e^{m_w - M}, ACC = Σ acc_w e^{m_w - M}
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         const float lt = gh_wave_sum(l[h]);
         if (lane == 0) {
-            wm[wave][h] = m[h];
-            wl[wave][h] = lt;
+            sh.wm[wave][h] = m[h];
+            sh.wl[wave][h] = lt;
         }
-        wacc[wave][h][2 * lane] = acc[h][0];
-        wacc[wave][h][2 * lane + 1] = acc[h][1];
+        sh.wacc[wave][h][2 * lane] = acc[h][0];
+        sh.wacc[wave][h][2 * lane + 1] = acc[h][1];
     }
+    attn_finish<G>(a, hot, sh, nsplit);
+}
+
+// Merge of the four waves' states (in sh) into the workgroup's partial or, with one split,
+// the output; with several splits the last workgroup of the (row, kv head) merges them:
+//   M = max m_w, L = Σ l_w e^{m_w - M}, ACC = Σ acc_w e^{m_w - M}, then across splits
+//   out = Σ_s e^{m_s-M} acc_s / Σ_s e^{m_s-M} l_s.
+template <int G>
+__device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& hot, AttnShared<G>& sh,
+                                            uint32_t nsplit) {
+    auto& wm = sh.wm;
+    auto& wl = sh.wl;
+    auto& wacc = sh.wacc;
+    auto& wsplit = sh.wsplit;
+    auto& last = sh.last;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
+    const uint32_t h0 = kvh * G;
     __syncthreads();
     const size_t pbase = ((size_t)row * hot.q_heads + h0) * a.splits;
     for (uint32_t i = tid; i < (uint32_t)G * 128; i += 256) {
@@ -288,6 +317,182 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// The same decode on the matrix cores, for G = 4 or 8 query heads per kv head (head_dim =
+// value_dim = 128). Same grid, chunking, splits and merge as attn_body; per wave and 16
+// positions of a chunk:
+//   S^T = K · Q^T   4 x v_mfma_f32_16x16x32_f16: A = the 16 K rows straight from memory (lane
+//                   l: position l % 16, dims 32 s + 8 (l / 16) .. + 8), B = the FP16 query
+//                   (column n = l % 16 is head n; columns >= G are zero). Lane l receives the
+//                   scores of head n = l % 16 at positions 4 (l / 16) + i, i < 4;
+//   softmax         per lane, for its head: the running max is shared by the head's four
+//                   lanes (permlane swaps), each lane keeps its partial Σe;
+//   O^T += V^T·P^T  per 8-dim tile t, 2 x v_mfma_f32_16x16x16_f16: B = the lane's own four
+//                   weights (P split into FP16 hi + lo, so P·V keeps FP32-level accuracy),
+//                   A = V^T with output row m standing for value dim 8 m + t: lane l loads the
+//                   16-byte V row slice of dims 8 (l % 16) .. + 8 at its four positions and
+//                   picks element t of each. Lane l then holds head n's value dims
+//                   8 (4 (l / 16) + i) + t, i.e. 32 (l / 16) .. + 32.
+// Products of FP16 values are exact in FP32; accumulation is FP32 (in a different order from
+// attn_body's, within the tests' bar against the oracle).
+typedef _Float16 dh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 dh4 __attribute__((ext_vector_type(4)));
+typedef float df4 __attribute__((ext_vector_type(4)));
+
+// max / sum over the four lanes n, n + 16, n + 32, n + 48 of a head (the 16-lane rows)
+__device__ __forceinline__ float rows_max(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+struct MChunk {
+    uint4 k[4];  // K: position l % 16, dims 32 s + 8 (l / 16) .. + 8 (s = k-step)
+    uint4 v[4];  // V: position 4 (l / 16) + i, dims 8 (l % 16) .. + 8
+};
+
+__device__ __forceinline__ void load_mchunk(const KVRsrc& rs, uint32_t row_bytes, uint32_t c, MChunk& r) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, n = lane & 15u, g = lane >> 4;
+    const uint32_t p0 = c * kChunk + wave * 16;
+    const uint32_t ok = (p0 + n) * row_bytes + 16 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        r.k[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.k, ok + 64 * s, 0, 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rs.v, (p0 + 4 * g + (uint32_t)i) * row_bytes + 16 * n, 0, 0));
+}
+
+// element t of the 16-byte slices of four positions, as one A fragment (k = the positions)
+__device__ __forceinline__ dh4 v_column(const uint4 (&v)[4], int t) {
+    auto word = [&](int i) __attribute__((always_inline)) {
+        const uint4 x = v[i];
+        const uint32_t w = (t >> 1) == 0 ? x.x : (t >> 1) == 1 ? x.y : (t >> 1) == 2 ? x.z : x.w;
+        return w;
+    };
+    uint32_t d0, d1;
+    if (t & 1) {
+        d0 = (word(0) >> 16) | (word(1) & 0xFFFF0000u);
+        d1 = (word(2) >> 16) | (word(3) & 0xFFFF0000u);
+    } else {
+        d0 = (word(0) & 0xFFFFu) | (word(1) << 16);
+        d1 = (word(2) & 0xFFFFu) | (word(3) << 16);
+    }
+    return __builtin_bit_cast(dh4, make_uint2(d0, d1));
+}
+
+__device__ __forceinline__ void mchunk_step(const MChunk& r, const dh8 (&qf)[4], float scale, uint32_t c,
+                                            uint32_t len, float& m, float& l, df4 (&acc)[8]) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, g = lane >> 4;
+    const uint32_t p0 = c * kChunk + wave * 16 + 4 * g;  // this lane's first position
+    df4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        st = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dh8, r.k[s]), qf[s], st, 0, 0, 0);
+    float sc[4];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sc[i] = p0 + (uint32_t)i < len ? st[i] * scale : -__builtin_inff();
+        mx = fmaxf(mx, sc[i]);
+    }
+    const float m_new = fmaxf(m, rows_max(mx));  // finite: the wave's first position is valid
+    const float f = m_new == -__builtin_inff() ? 1.0f : expf(m - m_new);
+    float p[4], ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        p[i] = p0 + (uint32_t)i < len ? expf(sc[i] - m_new) : 0.0f;
+        ps += p[i];
+    }
+    m = m_new;
+    l = l * f + ps;
+    dh4 ph, pl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ph[i] = (_Float16)p[i];
+        pl[i] = (_Float16)(p[i] - (float)ph[i]);
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        acc[t] *= f;
+        const dh4 vt = v_column(r.v, t);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, ph, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pl, acc[t], 0, 0, 0);
+    }
+}
+
+template <int G>
+__device__ __forceinline__ void attn_mfma_body(const GhAttnArgs& a, const AttnHot& hot) {
+    static_assert(G == 4 || G == 8, "matrix-core decode serves 4 or 8 query heads per kv head");
+    __shared__ AttnShared<G> sh;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, n = lane & 15u, g = lane >> 4;
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
+    const uint32_t h0 = kvh * G;
+    // B fragments of the query: head n (zero past G), dims 32 s + 8 g .. + 8
+    dh8 qf[4];
+    const GH_GLOBAL uint4* qp =
+        gh_gp<uint4>(hot.q + (((uint64_t)row * hot.q_heads + h0 + min(n, (uint32_t)G - 1)) * 128 + 8 * g) * 2);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const uint4 x = qp[4 * s];
+        qf[s] = __builtin_bit_cast(dh8, n < (uint32_t)G ? x : make_uint4(0u, 0u, 0u, 0u));
+    }
+    const size_t kv_row = (size_t)hot.kv_heads * 128;
+    const size_t cache0 = (size_t)hot.layer * hot.context * kv_row + (size_t)kvh * 128;
+    const uint16_t* kc = (const uint16_t*)hot.kc + cache0;
+    const uint16_t* vc = (const uint16_t*)hot.vc + cache0;
+    const uint32_t row_bytes = (uint32_t)kv_row * 2;
+    MChunk ra, rb;
+    load_mchunk(kv_rsrc(kc, vc, kv_row, hot.context), row_bytes, split, ra);
+    const uint32_t pos = (hot.pos_ptr ? *gh_gp<uint32_t>(hot.pos_ptr) : 0u) + a.base + row;
+    const uint32_t len = pos + 1;
+    const uint32_t nchunk = (len + kChunk - 1) / kChunk;
+    const uint32_t nsplit = min(nchunk, a.splits);
+    if (split >= nsplit) return;  // fixed grids (replayed graphs) may exceed the causal range
+
+    float m = -__builtin_inff(), l = 0.0f;
+    df4 acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = df4{0.0f, 0.0f, 0.0f, 0.0f};
+    const KVRsrc rs = kv_rsrc(kc, vc, kv_row, len);
+    for (uint32_t c = split; c < nchunk; c += 2 * nsplit) {
+        const uint32_t c1 = c + nsplit, c2 = c + 2 * nsplit;
+        load_mchunk(rs, row_bytes, min(c1, nchunk), rb);
+        if (c == split) {
+            // the first chunk was read up to the context: zero V past the row (its weights
+            // are 0, and 0 times a stale NaN would not be)
+            const uint32_t pv0 = c * kChunk + wave * 16 + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (pv0 + (uint32_t)i >= len) ra.v[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (c * kChunk + wave * 16 < len) mchunk_step(ra, qf, a.scale, c, len, m, l, acc);
+        if (c1 >= nchunk) break;
+        load_mchunk(rs, row_bytes, min(c2, nchunk), ra);
+        if (c1 * kChunk + wave * 16 < len) mchunk_step(rb, qf, a.scale, c1, len, m, l, acc);
+    }
+    const float lt = rows_sum(l);
+    if (n < (uint32_t)G) {
+        if (g == 0) {
+            sh.wm[wave][n] = m;
+            sh.wl[wave][n] = lt;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) sh.wacc[wave][n][32 * g + 8 * i + t] = acc[t][i];
+    }
+    attn_finish<G>(a, hot, sh, nsplit);
+}
+
 }  // namespace
 
 #define GH_ATTN_PARAMS                                                                          \
@@ -296,8 +501,8 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
 #define GH_ATTN_HOT AttnHot{q, kc, vc, pos_ptr, layer, context, q_heads, kv_heads}
 GH_KERNEL __launch_bounds__(256) void gh_attn_g1(GH_ATTN_PARAMS) { attn_body<1>(a, GH_ATTN_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_attn_g2(GH_ATTN_PARAMS) { attn_body<2>(a, GH_ATTN_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_g4(GH_ATTN_PARAMS) { attn_body<4>(a, GH_ATTN_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_g8(GH_ATTN_PARAMS) { attn_body<8>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4(GH_ATTN_PARAMS) { attn_mfma_body<4>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g8(GH_ATTN_PARAMS) { attn_mfma_body<8>(a, GH_ATTN_HOT); }
 
 // ---------------------------------------------------------------------------------------------
 // Causal GQA prefill attention on the matrix cores (flash attention, G = 4 query heads per kv
