@@ -248,7 +248,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
     constexpr int WT = 64, TI = WT / 32, TJ = BR / 32;
     constexpr int kS = 3, kL = 4;
     // one LDS block: kS weight stages, then each consumer wave's activation rows
-    __shared__ __attribute__((aligned(16))) _Float16 lds3[kS * BR * LDK + 4 * WT * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 lds3[kS * BR * LDK + 4 * 2 * WT * 64];
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t r0 = blockIdx.x * BR;
@@ -290,43 +290,51 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
     }
 
     // ---- consumers ----
-    // Activations are fetched as whole lines (lane l: token row 8 i + l / 8 of the wave's 64,
-    // 16-byte chunk l % 8 of the unit's 128 bytes) one unit ahead, and staged through the wave's
-    // own LDS rows (no barrier: only this wave touches them), from which the A fragments are
-    // read — each 128-byte line is requested once instead of once per 16-k step.
+    // Activations are fetched as whole lines, one unit ahead, straight into the wave's own LDS
+    // rows (only this wave touches them; the per-unit barrier's wait completes the loads), from
+    // which the A fragments are read — each 128-byte line is requested once instead of once per
+    // 16-k step, and no registers hold it on the way (8B prefill gate/up 85 -> 80 us).
     const uint32_t t0 = blockIdx.y * (4 * WT) + wave * WT;
     const uint32_t fm = lane & 31u, fg = lane >> 5;
     const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
     uint32_t xrow[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) xrow[i] = min(t0 + 8 * i + (lane >> 3), a.n - 1) * a.in_dim;
-    auto load_rows = [&](uint32_t u, u4v (&r)[8]) __attribute__((always_inline)) {
+    // Activations go straight to LDS (global_load_lds_dwordx4: lane l of a load lands at byte
+    // 16 l of its 1 KiB destination). Load i covers rows 8 i .. 8 i + 7 of the wave's 64; lane
+    // l fetches chunk (l % 8) ^ sw(r) of row r = 8 i + l / 8, so chunk c of row r sits at slot
+    // c ^ sw(r), sw(r) = (r / 4) % 8: a fragment read (rows fm = 0..31 of one chunk) then
+    // covers 32 distinct four-bank groups. Two buffers per wave, one unit each.
+    _Float16* xw = lds3 + kS * BR * LDK + wave * (2 * WT * 64);
+    auto load_rows = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = *(const GH_GLOBAL u4v*)(x + xrow[i] + chunk_k<FMT>(u, lane & 7u));
-    };
-    _Float16* xw = lds3 + kS * BR * LDK + wave * (WT * LDK);
-    auto put_rows = [&](const u4v (&r)[8]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) *(u4v*)(xw + (8 * i + (lane >> 3)) * LDK + (lane & 7u) * 8) = r[i];
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t r = 8 * i + (lane >> 3), c = (lane & 7u) ^ ((r >> 2) & 7u);
+            __builtin_amdgcn_global_load_lds((const GH_GLOBAL void*)(x + xrow[i] + chunk_k<FMT>(u, c)),
+                                             (__attribute__((address_space(3))) void*)(xw + b * (WT * 64) + i * 512),
+                                             16, 0, 0);
+        }
     };
     f16v acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f16v{};
-    u4v ra[8], rb[8];
-    load_rows(u0, ra);
+    load_rows(u0, 0);
     __syncthreads();
-    auto step = [&](uint32_t u, const u4v (&rcur)[8], u4v (&rnext)[8]) __attribute__((always_inline)) {
-        load_rows(uc(u + 1), rnext);
+    auto step = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
+        load_rows(uc(u + 1), b ^ 1u);
         __builtin_amdgcn_sched_barrier(0);  // the loads go out before anything waits
-        put_rows(rcur);
         const _Float16* wb = wstage((u - u0) % kS);
+        const _Float16* xb = xw + b * (WT * 64);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             h8 af[TI], bf[TJ];
 #pragma unroll
-            for (int i = 0; i < TI; ++i) af[i] = *(const h8*)(xw + (32 * i + fm) * LDK + 16 * ks + 8 * fg);
+            for (int i = 0; i < TI; ++i) {
+                const uint32_t r = 32 * i + fm, c = (2 * ks + fg) ^ ((r >> 2) & 7u);
+                af[i] = *(const h8*)(xb + r * 64 + c * 8);
+            }
 #pragma unroll
             for (int j = 0; j < TJ; ++j) bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
 #pragma unroll
@@ -340,10 +348,10 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
     // the unrolled body has no exits (exact wait counts across the back edge); tail after
     uint32_t u = u0;
     for (; u + 2 <= u1; u += 2) {
-        step(u, ra, rb);
-        step(u + 1, rb, ra);
+        step(u, 0);
+        step(u + 1, 1);
     }
-    if (u < u1) step(u, ra, rb);
+    if (u < u1) step(u, 0);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
