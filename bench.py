@@ -151,6 +151,9 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the roofline kernel (4 distinct weights) and a 256 MiB "
                          "device copy of known size, for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="only the C3 prefill GEMMs (512 tokens, 8 random weights each), for "
+                         "rocprofv3 --pmc passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -162,6 +165,9 @@ def main():
 
     if args.traffic_probe:
         traffic_probe(synth.SHAPES["8b"])
+        return
+    if args.gemm_probe:
+        gemm_probe(synth.SHAPES["8b"])
         return
     shape = synth.SHAPES["8b"]
     per_block, per_token = weight_bytes(shape)
@@ -368,6 +374,33 @@ def traffic_probe(shape):
         f"each), 2 x copy of {nbytes} B")
     rt.hipFree(src)
     rt.hipFree(dst)
+    hip.close()
+
+
+def gemm_probe(shape, n=512):
+    """The C3 prefill GEMMs alone: gate/up (Q4_K d -> FFN) then down (Q6_K FFN -> d) over 8
+    random weights each, 4 passes, nothing else (for PMC passes)."""
+    import ctypes as C
+
+    from graph_horizon_amd import HipBackend, synth
+
+    hip = HipBackend(0)
+    d, ffn = shape.embedding_length, shape.feed_forward_length
+    rng = np.random.default_rng(3)
+    y = hip.alloc_buffer(n * ffn * 2)
+    for fmt, ind, outd in ((12, d, ffn), (14, ffn, d)):
+        ws = [hip.load_weight(fmt, synth.quant_blocks(rng, fmt, outd, ind, synth.model_d_std(ind)), ind, outd)
+              for _ in range(8)]
+        a = hip.from_host(synth.f16_bits(rng.standard_normal(n * ind) * 0.5))
+        enc = hip.begin()
+        for _ in range(4):
+            for w in ws:
+                hip.lib.gh_matmul_batched(hip.h, enc, C.byref(y), C.byref(a), C.byref(w), ind, outd, n)
+        hip.submit()
+        hip.synchronize()
+        for b in ws + [a]:
+            hip.free_buffer(b)
+    log(f"bench: gemm probe: 32 x {n}x{d}->{ffn} Q4_K, 32 x {n}x{ffn}->{d} Q6_K")
     hip.close()
 
 
