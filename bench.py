@@ -154,6 +154,9 @@ def main():
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only the C3 prefill GEMMs (512 tokens, 8 random weights each), for "
                          "rocprofv3 --pmc passes")
+    ap.add_argument("--attn-probe", action="store_true",
+                    help="only the C4 attention cases (bench.py c4_attention), for rocprofv3 "
+                         "--pmc passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -168,6 +171,11 @@ def main():
         return
     if args.gemm_probe:
         gemm_probe(synth.SHAPES["8b"])
+        return
+    if args.attn_probe:
+        hip = HipBackend(0)
+        log(f"bench: attention probe {json.dumps(c4_attention(hip))}")
+        hip.close()
         return
     shape = synth.SHAPES["8b"]
     per_block, per_token = weight_bytes(shape)
