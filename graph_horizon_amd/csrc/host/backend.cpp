@@ -42,7 +42,7 @@ const KernelName kKernels[] = {
     {K_ARGMAX_FINAL, "gh_argmax_final"},   {K_ATTN_G1, "gh_attn_g1"},
     {K_ATTN_G2, "gh_attn_g2"},             {K_ATTN_MFMA_G4, "gh_attn_mfma_g4"},
     {K_ATTN_MFMA_G8, "gh_attn_mfma_g8"},
-    {K_STEP_ADVANCE, "gh_step_advance"},
+
     {K_GEMM_Q4K_T128_R64, "gh_gemm_q4k_t128_r64"},   {K_GEMM_Q4K_T128_R128, "gh_gemm_q4k_t128_r128"},
     {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},   {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"},
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
@@ -416,7 +416,8 @@ int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, ui
                   ceil_div(embd, 256), 1, 1, 256, &a);
 }
 
-int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2) {
+int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2,
+              void* step_scalars, void* step_history) {
     int rc = ensure_workspace(b, 0);
     if (rc) return rc;
     GhArgmaxArgs a{};
@@ -425,6 +426,8 @@ int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, vo
     a.part_i = (uint64_t)((char*)b->ws + 1024);
     a.out = out ? (uint64_t)out : (uint64_t)((char*)b->ws + 2048);
     a.out2 = (uint64_t)out2;
+    a.step_scalars = (uint64_t)step_scalars;
+    a.step_history = (uint64_t)step_history;
     a.n = (uint32_t)vocab;
     a.blocks = std::min<uint32_t>(kArgmaxBlocks, ceil_div(vocab, 256));
     rc = launch(b, K_ARGMAX_PARTIAL, a.blocks, 1, 1, 256, &a);
@@ -573,10 +576,6 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
                      "hipModuleLaunchKernel");
 }
 
-int op_step_advance(gh_backend* b, void* scalars, void* history) {
-    GhStepArgs a{(uint64_t)scalars, (uint64_t)history};
-    return launch(b, K_STEP_ADVANCE, 1, 1, 1, 64, &a);
-}
 
 }  // namespace gh
 

@@ -55,7 +55,6 @@ enum GhKernel : int {
     K_ATTN_G2,
     K_ATTN_MFMA_G4,
     K_ATTN_MFMA_G8,
-    K_STEP_ADVANCE,
     // prefill GEMM tile variants (tokens x rows per workgroup), Q4_K then Q6_K
     K_GEMM_Q4K_T128_R64,
     K_GEMM_Q4K_T128_R128,
@@ -161,8 +160,9 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
                  const void* pos_ptr, uint32_t max_pos, const AttnScratch* fixed = nullptr);
 int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, uint32_t embd,
              const void* token_ptr);
-int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2);
-int op_step_advance(gh_backend* b, void* scalars, void* history);
+// step_scalars / step_history: also end a replayed greedy decode step (see GhArgmaxArgs)
+int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2,
+              void* step_scalars = nullptr, void* step_history = nullptr);
 // Decode GEMVs with fused epilogues (n = 1). Segments are launched as one grid.
 struct GemvSeg {
     const gh_buf* w;

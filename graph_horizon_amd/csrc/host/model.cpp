@@ -200,8 +200,9 @@ int record_step(gh_model* m, gh_encoder* enc) {
     int rc = op_embed(m->b, &m->dec.x, &m->token_embd, 0, c.embedding_length, tok_ptr);
     for (uint32_t li = 0; li < c.block_count && !rc; ++li) rc = layer(m, enc, m->dec, li, 0, 1, pos_ptr);
     if (!rc) rc = tail(m, enc, &m->dec.x, &m->dec.normed);
-    if (!rc) rc = op_argmax(m->b, &m->logits, c.vocab_size, (void*)(m->scalars.addr + 8), nullptr);
-    if (!rc) rc = op_step_advance(m->b, (void*)m->scalars.addr, (void*)m->history.addr);
+    // the argmax's final pass also stores it in history[pos] and advances (token, pos)
+    if (!rc) rc = op_argmax(m->b, &m->logits, c.vocab_size, (void*)(m->scalars.addr + 8), nullptr,
+                            (void*)m->scalars.addr, (void*)m->history.addr);
     return rc;
 }
 

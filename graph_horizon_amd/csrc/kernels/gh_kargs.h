@@ -186,15 +186,14 @@ struct GhArgmaxArgs {
     uint64_t part_i;   // u32 [blocks]
     uint64_t out;      // u32 result
     uint64_t out2;     // optional second u32 destination (next token id for graph replay)
+    // optional end of a replayed greedy decode step: scalars u32[0] = position, [1] = token
+    // id; gh_argmax_final stores the result r in history[position], then sets token = r and
+    // position + 1 (0: not a decode step)
+    uint64_t step_scalars;
+    uint64_t step_history;
     uint32_t n;
     uint32_t blocks;
 };
 
-// End of a replayed greedy decode step: scalars u32[0] = position, [1] = token id,
-// [2] = argmax of this step. history[pos] = argmax; token = argmax; pos += 1.
-struct GhStepArgs {
-    uint64_t scalars;
-    uint64_t history;
-};
 
 #endif

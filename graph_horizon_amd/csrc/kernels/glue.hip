@@ -142,16 +142,14 @@ GH_KERNEL __launch_bounds__(256) void gh_argmax_final(GhArgmaxArgs a) {
         const uint32_t r = (idx == 0xFFFFFFFFu) ? 0u : idx;
         *(uint32_t*)a.out = r;
         if (a.out2) *(uint32_t*)a.out2 = r;
+        if (a.step_scalars) {  // end of a replayed greedy decode step
+            uint32_t* s = (uint32_t*)a.step_scalars;
+            const uint32_t pos = s[0];
+            ((uint32_t*)a.step_history)[pos] = r;
+            s[1] = r;
+            s[0] = pos + 1;
+        }
     }
-}
-
-GH_KERNEL void gh_step_advance(GhStepArgs a) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    uint32_t* s = (uint32_t*)a.scalars;
-    const uint32_t pos = s[0], r = s[2];
-    ((uint32_t*)a.history)[pos] = r;
-    s[1] = r;
-    s[0] = pos + 1;
 }
 
 // ---- top-k: read_topk (backend/contract.rs:303-318, cpu/readback.rs:59-69) on the device ----
