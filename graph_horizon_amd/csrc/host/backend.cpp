@@ -485,7 +485,7 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     const bool direct = !norm && n == 1 && nseg == 1 && !swiglu && in_dim <= 4096;
     // direct launches of 8192 rows or more take one-row tasks (more waves in flight: 12288x4096
     // Q4_K measured 6.84 us against 7.21 us with two-row tasks; 4096x4096 stays at two rows,
-    // 3.94 us against 4.06 us)
+    // 4.01 us against 4.16 us with one-row tasks)
     if (direct && total_rows >= 8192 && (k == K_GEMV_Q4K_R2 || k == K_GEMV_Q6K_R2)) {
         k = k == K_GEMV_Q4K_R2 ? K_GEMV_Q4K_R1 : K_GEMV_Q6K_R1;
         r = 1;
@@ -566,9 +566,10 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
     // + the normalized FP16 row and 16 bytes of reduction scratch when RMSNorm is fused
     uint32_t shmem = (in_dim / 64) * 144 * (mixed ? 2 : 1) + (norm ? in_dim * 2 + 16 : 0);
     if (direct || splitk) shmem = 0;
+    if (direct) block = 64 * GH_DIRECT_WAVES;
     const uint32_t cap = resident_wgs(b, k, block, shmem);
-    // split-K: one task per workgroup (four waves share it); otherwise one per wave
-    const uint32_t want = splitk ? task : ceil_div(task, 4);
+    // split-K: one task per workgroup (its waves share it); otherwise one per wave
+    const uint32_t want = splitk ? task : ceil_div(task, block / 64);
     a.groups = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
     // the kernels' leading scalar parameters (preloaded into SGPRs), then the full arguments
     void* params[] = {&a.x, &a.seg[0].w, &a.norm_w, &a.in_dim, &a.seg[0].rows, &a.tasks, &a.groups, &a};

@@ -675,13 +675,16 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
 // tasks of a 12288x4096 launch run in one round (pairs held per wave: 104 VGPRs, four waves
 // per SIMD, one and a half rounds; 7.7 -> 7.3 us). x fetched per wave instead of staged
 // (8 KiB each, 16 waves per CU) measured ~1.5 us of a 10 us 12288x4096 launch.
+// Workgroups of GH_DIRECT_WAVES = 8 waves: a 4096x4096 launch is 256 workgroups, one per CU,
+// each staging x once (four-wave workgroups, two per CU: Q4_K 4.08 -> 4.01 us, Q6_K 5.00 ->
+// 4.90 us back to back over distinct weights; sixteen waves leave half the CUs idle, 5.3 us).
 template <int R, uint32_t FMT>
 __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h) {
     __shared__ uint4 xs[512];     // x as FP16 pairs, stage_x's layout (in_dim <= 4096)
     __shared__ float4 sums[64];
     const uint32_t lane = threadIdx.x & 63u, nb = h.in_dim >> 8, units = nb * 4;
-    const uint32_t waves = h.groups * 4;  // 256-thread workgroups
-    const uint32_t gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t waves = h.groups * GH_DIRECT_WAVES;
+    const uint32_t gw = blockIdx.x * GH_DIRECT_WAVES + (threadIdx.x >> 6);
     GhGemvSeg sg = a.seg[0];
     sg.w = h.w0;
     sg.rows = h.rows0;
@@ -689,12 +692,13 @@ __device__ __forceinline__ void gemv_direct(const GhGemvArgs& a, const GhHot& h)
     const uint8_t* w[1] = {(const uint8_t*)sg.w};
     const GH_GLOBAL uint4* xh = gh_gp<uint4>(h.x);
     // thread t pairs item t = (unit t/4, quarter t%4): 16 FP16 values, two 16-byte loads
+    // (threads past the last item load it again and store nothing)
     const uint32_t t = threadIdx.x, it = min(t, units * 4 - 1), iu = it >> 2, iq = it & 3u;
     const uint32_t e = FMT == kQ4K ? 16 * it
                                    : (iu >> 2) * 256 + ((iu >> 1) & 1u) * 128 + iq * 32 + (iu & 1u) * 16;
     const uint4 x0 = xh[e >> 3], x1 = xh[(e >> 3) + 1];
     __builtin_amdgcn_sched_barrier(0);
-    // waves past the last task (the grid has at most three, all in the last workgroup) load
+    // waves past the last task (the grid has at most seven, all in the last workgroup) load
     // the last task's rows, take part in the barrier, and leave
     const uint32_t t0 = min(gw, h.tasks - 1);
     WRow<FMT> wr[1][R];
@@ -832,10 +836,10 @@ GH_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gh
 GH_GEMV(gh_gemv_swiglu_r1, 1, kModeSwiglu)
 GH_GEMV(gh_gemv_swiglu_r2, 2, kModeSwiglu)
 // direct-x variants (suffix _d): single token, one matrix, in_dim <= 4096, no RMSNorm
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ4K>(a, GH_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ4K>(a, GH_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ6K>(a, GH_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ6K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(512) void gh_gemv_q4k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ4K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(512) void gh_gemv_q4k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ4K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(512) void gh_gemv_q6k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ6K>(a, GH_HOT); }
+GH_KERNEL __launch_bounds__(512) void gh_gemv_q6k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ6K>(a, GH_HOT); }
 // split-K variants (suffix _k): single token, one matrix, 4096 < in_dim <= 16384, no RMSNorm
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r1_k(GH_HOT_PARAMS) { gemv_splitk<1, kQ4K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_k(GH_HOT_PARAMS) { gemv_splitk<2, kQ4K>(a, GH_HOT); }

@@ -58,6 +58,9 @@ struct GhGemvSeg {
     uint32_t task0;  // first task index
 };
 
+// Waves per workgroup of the direct-x GEMV kernels (gh_gemv_q*_r*_d): 512-thread workgroups.
+#define GH_DIRECT_WAVES 8u
+
 struct GhGemvArgs {
     GhGemvSeg seg[3];
     uint64_t x;        // f16 activations, token-major [n][in_dim]
