@@ -90,16 +90,26 @@ __device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* 
         const float d = gh_h2f(ws.hd.x & 0xFFFFu), dmin = gh_h2f(ws.hd.x >> 16);
         const float d1 = d * (float)sc0, m1 = dmin * (float)mn0;
         const float d2 = d * (float)sc1, m2 = dmin * (float)mn1;
-        // nibbles four at a time: byte e of lo4 / hi4 is the low / high nibble of byte e
+        // nibbles four at a time: byte e of lo4 / hi4 is the low / high nibble of byte e.
+        // d·sc and dmin·mn are exact in FP32 (an FP16 times a 6-bit integer), and so is
+        // (d·sc)·q for a 4-bit q (at most 21 significant bits): the reference's product,
+        // then difference, rounds once, as one FMA does, so the FMA gives the same FP32 value.
         auto w2 = [](uint32_t q4, int e, float sc, float mn) __attribute__((always_inline)) {
             typedef _Float16 hv2 __attribute__((ext_vector_type(2)));
             const float f0 = (float)((q4 >> (8 * e)) & 0xFFu), f1 = (float)((q4 >> (8 * e + 8)) & 0xFFu);
-            const hv2 r = {(_Float16)(sc * f0 - mn), (_Float16)(sc * f1 - mn)};  // mul, then sub
+            float v0 = __builtin_fmaf(sc, f0, -mn), v1 = __builtin_fmaf(sc, f1, -mn);
+            // the FP32 values are rounded to FP16 as a second step (v_cvt_pk_f16_f32), not fused
+            // into one rounding of the exact value (v_fma_mix), which differs on FP16 ties
+            asm volatile("" : "+v"(v0), "+v"(v1));
+            const hv2 r = {(_Float16)v0, (_Float16)v1};
             return __builtin_bit_cast(uint32_t, r);
         };
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t lo4 = qw[j] & 0x0F0F0F0Fu, hi4 = (qw[j] >> 4) & 0x0F0F0F0Fu;
+            uint32_t lo4 = qw[j] & 0x0F0F0F0Fu, hi4 = (qw[j] >> 4) & 0x0F0F0F0Fu;
+            // opaque: with the masks' known zero bits the compiler would extract each byte
+            // separately instead of converting it in place (v_cvt_f32_ubyte1..3)
+            asm volatile("" : "+v"(lo4), "+v"(hi4));
             lo[2 * j] = w2(lo4, 0, d1, m1);
             lo[2 * j + 1] = w2(lo4, 2, d1, m1);
             hi[2 * j] = w2(hi4, 0, d2, m2);
@@ -303,13 +313,15 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
     // Activations go straight to LDS (global_load_lds_dwordx4: lane l of a load lands at byte
     // 16 l of its 1 KiB destination). Load i covers rows 8 i .. 8 i + 7 of the wave's 64; lane
     // l fetches chunk (l % 8) ^ sw(r) of row r = 8 i + l / 8, so chunk c of row r sits at slot
-    // c ^ sw(r), sw(r) = (r / 4) % 8: a fragment read (rows fm = 0..31 of one chunk) then
-    // covers 32 distinct four-bank groups. Two buffers per wave, one unit each.
+    // c ^ sw(r). Every row starts at bank 0 (128-byte pitch); with sw(r) = (r / 2) % 8 a
+    // fragment read (rows fm = 0..31 of one chunk) is free of bank conflicts, as measured with
+    // SQ_LDS_BANK_CONFLICT on gfx950 (sw(r) = (r / 4) % 8 and r % 8 are two-way conflicted:
+    // 7.3 against 3.8 LDS-active cycles per read). Two buffers per wave, one unit each.
     _Float16* xw = lds3 + kS * BR * LDK + wave * (2 * WT * 64);
     auto load_rows = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t r = 8 * i + (lane >> 3), c = (lane & 7u) ^ ((r >> 2) & 7u);
+            const uint32_t r = 8 * i + (lane >> 3), c = (lane & 7u) ^ ((r >> 1) & 7u);
             __builtin_amdgcn_global_load_lds((const GH_GLOBAL void*)(x + xrow[i] + chunk_k<FMT>(u, c)),
                                              (__attribute__((address_space(3))) void*)(xw + b * (WT * 64) + i * 512),
                                              16, 0, 0);
@@ -332,7 +344,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
             h8 af[TI], bf[TJ];
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
-                const uint32_t r = 32 * i + fm, c = (2 * ks + fg) ^ ((r >> 2) & 7u);
+                const uint32_t r = 32 * i + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
                 af[i] = *(const h8*)(xb + r * 64 + c * 8);
             }
 #pragma unroll
