@@ -416,6 +416,23 @@ int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, ui
                   ceil_div(embd, 256), 1, 1, 256, &a);
 }
 
+// Embedding rows of a token list already on the device (u32[rows]): one launch for a whole
+// prefill chunk, row r of x = dequantized row tokens[r] (the same values as op_embed per row).
+int op_embed_rows(gh_backend* b, const gh_buf* x, const gh_buf* w, const void* tokens, uint32_t rows,
+                  uint32_t embd) {
+    if (!is_weight(w) || w->cols != embd) return fail(b, GH_E_UNSUPPORTED, "embed: token_embd must be a Q4_K/Q6_K weight of width embd");
+    if (!fits(x, (uint64_t)rows * embd * 4)) return fail(b, GH_E_RANGE, "embed: x too small");
+    GhDequantArgs a{};
+    a.w = w->addr;
+    a.out = x->addr;
+    a.row_list = (uint64_t)tokens;
+    a.wrows = w->rows;
+    a.nb = embd / 256;
+    a.rows = rows;
+    return launch(b, w->format == GH_FMT_Q4_K ? K_DEQUANT_Q4K : K_DEQUANT_Q6K,
+                  (uint32_t)ceil_div((uint64_t)rows * embd, (uint64_t)256), 1, 1, 256, &a);
+}
+
 int op_argmax(gh_backend* b, const gh_buf* logits, uint64_t vocab, void* out, void* out2,
               void* step_scalars, void* step_history) {
     int rc = ensure_workspace(b, 0);

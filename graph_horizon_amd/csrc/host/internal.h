@@ -158,6 +158,8 @@ struct AttnScratch {
 int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv* kv,
                  uint32_t q_heads, uint32_t base, uint32_t rows, uint32_t layer,
                  const void* pos_ptr, uint32_t max_pos, const AttnScratch* fixed = nullptr);
+int op_embed_rows(gh_backend* b, const gh_buf* x, const gh_buf* w, const void* tokens, uint32_t rows,
+                  uint32_t embd);
 int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, uint32_t embd,
              const void* token_ptr);
 // step_scalars / step_history: also end a replayed greedy decode step (see GhArgmaxArgs)

@@ -33,6 +33,7 @@ struct gh_model {
     gh_buf logits{};
     gh_buf scalars{};  // u32[4]: position, token, argmax, spare
     gh_buf history{};  // u32[kv_context]
+    gh_buf prompt{};   // u32[kv_context]: the token ids of a prefill call, for the batched embed
     gh_kv kv{};
     GhRopeTable rope;  // this model's YaRN table for positions 0 .. kv_context - 1
     std::vector<gh_buf> owned;
@@ -306,6 +307,7 @@ int gh_model_create(gh_backend* b, const gh_model_config* cfg, gh_model** out) {
     if (!rc) rc = alloc(m, (uint64_t)c.vocab_size * 4, &m->logits);
     if (!rc) rc = alloc(m, 16, &m->scalars);
     if (!rc) rc = alloc(m, (uint64_t)c.kv_context * 4, &m->history);
+    if (!rc) rc = alloc(m, (uint64_t)c.kv_context * 4, &m->prompt);
     if (!rc) rc = ensure_rope(b, m->rope, &c.yarn, c.kv_context);
     // partials for a decode step and for one prefill chunk
     const uint32_t dsplits = attention_splits(b, c.kv_context, c.kv_head_count, 1);
@@ -403,16 +405,17 @@ int gh_model_prefill(gh_model* m, const uint32_t* tokens, uint32_t n, uint32_t b
         if (tokens[i] >= c.vocab_size) return fail(m->b, GH_E_RANGE, "model: token beyond vocabulary");
     const uint32_t cap = c.prefill_rows;
     const uint64_t d = c.embedding_length;
+    // the chunk's embedding rows in one launch from the token ids on the device (the values
+    // of embed per row, encode.rs:16-106, without a launch per token)
+    int urc = gh_upload(m->b, &m->prompt, 0, tokens, (uint64_t)n * 4);
+    if (urc) return urc;
     for (uint32_t off = 0; off < n; off += cap) {
         const uint32_t rows = std::min(cap, n - off);
         gh_encoder* enc = nullptr;
         int rc = gh_begin(m->b, &enc);
         if (rc) return rc;
-        for (uint32_t r = 0; r < rows && !rc; ++r) {
-            gh_buf xr;
-            rc = gh_view(m->b, &m->pre.x, r * d * 4, d * 4, &xr);
-            if (!rc) rc = gh_embed(m->b, enc, &xr, &m->token_embd, tokens[off + r], c.embedding_length);
-        }
+        rc = latch_rc(enc, op_embed_rows(m->b, &m->pre.x, &m->token_embd, (const void*)(m->prompt.addr + (uint64_t)off * 4),
+                                         rows, c.embedding_length));
         for (uint32_t li = 0; li < c.block_count && !rc; ++li)
             rc = layer(m, enc, m->pre, li, base + off, rows, nullptr);
         if (!rc && off + rows == n) {  // the tail belongs to the last chunk's last row

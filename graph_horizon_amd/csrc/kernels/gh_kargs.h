@@ -36,6 +36,7 @@ struct GhDequantArgs {
     uint32_t nb;
     uint32_t row0;
     uint32_t rows;
+    uint64_t row_list;  // optional u32[rows] on the device: row r dequantizes row_list[r]
 };
 
 // Decode GEMV epilogues (what happens to an output row's FP32 dot product).

@@ -65,7 +65,8 @@ GH_KERNEL __launch_bounds__(256) void gh_dequant_q4k(GhDequantArgs a) {
     if (t >= total) return;
     const uint32_t r = (uint32_t)(t / in_dim);
     const uint32_t i = (uint32_t)(t % in_dim);
-    const uint32_t row = (a.row_ptr ? *(const uint32_t*)a.row_ptr : a.row0) + r;
+    const uint32_t row = a.row_list ? ((const uint32_t*)a.row_list)[r]
+                                    : (a.row_ptr ? *(const uint32_t*)a.row_ptr : a.row0) + r;
     const uint32_t b = i >> 8, within = i & 255;
     const uint32_t j = within >> 5, l = within & 31;  // sub-block, index inside it
     const uint32_t g = j >> 1, h = l >> 4;
@@ -94,7 +95,8 @@ GH_KERNEL __launch_bounds__(256) void gh_dequant_q6k(GhDequantArgs a) {
     if (t >= total) return;
     const uint32_t r = (uint32_t)(t / in_dim);
     const uint32_t i = (uint32_t)(t % in_dim);
-    const uint32_t row = (a.row_ptr ? *(const uint32_t*)a.row_ptr : a.row0) + r;
+    const uint32_t row = a.row_list ? ((const uint32_t*)a.row_list)[r]
+                                    : (a.row_ptr ? *(const uint32_t*)a.row_ptr : a.row0) + r;
     const uint32_t b = i >> 8, within = i & 255;
     const uint32_t s = within >> 7, quarter = (within >> 5) & 3, l = within & 31;
     const uint32_t h = l >> 4;
