@@ -45,7 +45,7 @@ const KernelName kKernels[] = {
 
     {K_GEMM_Q4K_T128_R64, "gh_gemm_q4k_t128_r64"},   {K_GEMM_Q4K_T128_R128, "gh_gemm_q4k_t128_r128"},
     {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},   {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"},
-    {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
+    {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
@@ -827,11 +827,16 @@ int gh_embed(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* w, u
     return latch(enc, op_embed(b, x, w, token, embd, nullptr));
 }
 
+}  // extern "C"
+
+namespace gh {
+
 // Matrix-core GEMM for n >= kGemmMinTokens. Batches of 256 tokens or more take the
 // warp-specialized kernels (256 tokens x 128 or 96 rows per 512-thread workgroup); shorter
 // batches take the 256-thread tiles of 128 tokens x 64 rows (outputs below 4096 rows) or
 // x 128 rows. Either splits K over the units when the tiles alone would leave CUs idle.
 constexpr uint32_t kGemmMinTokens = 8;
+constexpr uint32_t kGemmTailMaxRows = 8192;  // gh_gemm_tail: two 16-value items per thread
 
 struct GemmTile {
     uint32_t tokens, rows, index;
@@ -839,9 +844,12 @@ struct GemmTile {
 constexpr GemmTile kGemmTiles[2] = {{128, 64, 0}, {128, 128, 1}};
 
 // One GEMM launch over tr x tt tiles and `splits` K ranges; with splits > 1 the kernel writes
-// FP32 partials to the workspace and gh_gemm_reduce sums them in split order.
+// FP32 partials to the workspace and gh_gemm_reduce sums them in split order. `e` adds the
+// SiLU epilogue (in the GEMM or the reduce) or replaces the reduce by gh_gemm_tail (residual
+// add and RMSNorm of each output row).
 static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, uint32_t tt,
-                       uint32_t splits, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n) {
+                       uint32_t splits, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n,
+                       const GemmEpi* e) {
     // the kernels give split z the units [z per, min(units, (z + 1) per)), per = ceil(units /
     // splits): shrink splits to ceil(units / per) until every split is non-empty
     const uint32_t units = w->cols / 64;
@@ -851,19 +859,31 @@ static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, u
         splits = s;
     }
     GhGemmArgs ga{a->addr, w->addr, out, 0, w->cols, w->rows, n, splits};
+    const bool tail = e && e->resid;
+    if (e && !tail) {
+        ga.epi = e->epi;
+        ga.aux = e->aux;
+    }
     if (splits > 1) {
         int rc = ensure_workspace(b, (size_t)splits * n * w->rows * 4);
         if (rc) return rc;
         ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
     }
     int rc = launch(b, k, tr, tt, splits, block, &ga);
+    if (!rc && tail) {
+        ga.aux = e->resid;
+        ga.norm = e->norm;
+        ga.normed = e->normed;
+        ga.eps = e->eps;
+        return launch(b, K_GEMM_TAIL, n, 1, 1, 256, &ga);
+    }
     if (rc || splits == 1) return rc;
     const uint64_t total = (uint64_t)n * w->rows;
     return launch(b, K_GEMM_REDUCE, (uint32_t)std::min<uint64_t>(ceil_div(total, (uint64_t)256), 4096), 1, 1,
                   256, &ga);
 }
 
-int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n) {
+int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n, const GemmEpi* e) {
     const uint32_t in_dim = w->cols, rows = w->rows, units = in_dim / 64;
     // splits: at most 16 and at least 8 units of 64 k per split
     auto clamp_splits = [&](uint32_t s) {
@@ -888,14 +908,50 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
                                     : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
         const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
         const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
-        return gemm_launch(b, k, 512, tr, tt, clamp_splits(std::max<uint32_t>(1, slots / tiles)), out, a, w, n);
+        return gemm_launch(b, k, 512, tr, tt, clamp_splits(std::max<uint32_t>(1, slots / tiles)), out, a, w, n, e);
     }
     const GemmTile tile = rows >= 4096 ? kGemmTiles[1] : kGemmTiles[0];
     const GhKernel k = (GhKernel)((q4 ? K_GEMM_Q4K_T128_R64 : K_GEMM_Q6K_T128_R64) + tile.index);
     const uint32_t tr = ceil_div(rows, tile.rows), tt = ceil_div(n, tile.tokens), tiles = tr * tt;
     return gemm_launch(b, k, 256, tr, tt, clamp_splits(std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles)),
-                       out, a, w, n);
+                       out, a, w, n, e);
 }
+
+// The SiLU epilogue is compiled into the warp-specialized kernels (n >= 256) only; the tail
+// runs after any GEMM (n >= kGemmMinTokens).
+bool gemm_epi_applies(uint32_t n, uint32_t out_dim, bool tail) {
+    return tail ? n >= kGemmMinTokens && out_dim % 4 == 0 && out_dim <= kGemmTailMaxRows : n >= 256;
+}
+
+int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,
+                  uint32_t out_dim, uint32_t n, const gh_buf* gate, const gh_buf* resid,
+                  const gh_buf* norm, const gh_buf* normed, float eps) {
+    const bool tail = resid != nullptr;
+    if ((gate != nullptr) == tail || (norm != nullptr) != (normed != nullptr) || (norm && !tail))
+        return fail(b, GH_E_INVALID, "matmul epilogue: SiLU, or residual (+ norm)");
+    if (!gemm_epi_applies(n, out_dim, tail)) return fail(b, GH_E_UNSUPPORTED, "matmul epilogue: GEMM path only");
+    if (!is_weight(w)) return fail(b, GH_E_UNSUPPORTED, "matmul: weight must be Q4_K or Q6_K");
+    if (w->cols != in_dim || w->rows != out_dim) return fail(b, GH_E_INVALID, "matmul: weight shape mismatch");
+    const uint64_t cells = (uint64_t)n * out_dim;
+    if (!fits(a, (uint64_t)n * in_dim * 2) || !fits(out, cells * 2) || (gate && !fits(gate, cells * 2)) ||
+        (tail && !fits(resid, cells * 4)) || (norm && (!fits(norm, (uint64_t)out_dim * 2) || !fits(normed, cells * 2))))
+        return fail(b, GH_E_RANGE, "matmul epilogue: buffer too small");
+    GemmEpi e;
+    if (gate) {
+        e.epi = GH_GEMM_EPI_SILU;
+        e.aux = gate->addr;
+    } else {
+        e.resid = resid->addr;
+        e.norm = norm ? norm->addr : 0;
+        e.normed = normed ? normed->addr : 0;
+        e.eps = eps;
+    }
+    return op_gemm(b, out->addr, a, w, n, &e);
+}
+
+}  // namespace gh
+
+extern "C" {
 
 static int gemv_launch(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w,
                        uint32_t in_dim, uint32_t out_dim, uint32_t n, bool f32) {

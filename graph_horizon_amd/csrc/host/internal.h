@@ -61,6 +61,7 @@ enum GhKernel : int {
     K_GEMM_Q6K_T128_R64,
     K_GEMM_Q6K_T128_R128,
     K_GEMM_REDUCE,
+    K_GEMM_TAIL,
     K_ATTN_PREFILL_G4,
     K_GEMM3_Q4K_R128,
     K_GEMM3_Q6K_R128,
@@ -178,6 +179,24 @@ constexpr uint32_t kFusedNormMaxDim = 5120;
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
             uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up,
             const gh_buf* norm = nullptr, float eps = 0.0f, const GhRopeTable* rope = nullptr);
+// Epilogue of a prefill GEMM (n >= 8 tokens). epi/aux: GH_GEMM_EPI_SILU with the FP16 gate
+// (out = silu_mul(gate, f16(acc))). resid != 0: the output row is folded into the FP32 residual
+// x[n][out_dim] (residual_add) and, with norm != 0, its RMSNorm written to normed — the bits of
+// the separate reduce, residual_add and rmsnorm_x ops (out then only holds the FP16 projection).
+struct GemmEpi {
+    uint32_t epi = GH_GEMM_EPI_F16;
+    uint64_t aux = 0;
+    uint64_t resid = 0, norm = 0, normed = 0;
+    float eps = 0.0f;
+};
+int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n,
+            const GemmEpi* e = nullptr);
+bool gemm_epi_applies(uint32_t n, uint32_t out_dim, bool tail);
+// gh_matmul_batched with an epilogue (checked buffers): gate != nullptr selects the SiLU
+// epilogue; resid != nullptr the residual add, and norm/normed the RMSNorm after it.
+int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,
+                  uint32_t out_dim, uint32_t n, const gh_buf* gate, const gh_buf* resid,
+                  const gh_buf* norm = nullptr, const gh_buf* normed = nullptr, float eps = 0.0f);
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
 uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows);
 int ensure_counters(gh_backend* b, size_t slots);

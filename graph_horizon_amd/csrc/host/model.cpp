@@ -127,9 +127,13 @@ bool fusable(const gh_model* m, uint32_t li) {
 }
 
 // One transformer layer over `rows` packed rows at absolute positions base + r
-// (+ *pos_ptr when the position lives on the device).
+// (+ *pos_ptr when the position lives on the device). With `normed` (prefill), the GEMM path's
+// epilogues carry the glue: the O and down projections' output rows go straight into the
+// residual and the following RMSNorm (gh_gemm_tail), the up projection applies silu_mul to the
+// gate; *normed on return says the next layer's attention norm is already in s.normed. The
+// values are those of the separate ops below.
 int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t base,
-          uint32_t rows, const void* pos_ptr) {
+          uint32_t rows, const void* pos_ptr, bool* normed = nullptr) {
     if (rows == 1 && fusable(m, li)) return layer_decode_fused(m, enc, s, li, base, pos_ptr);
     gh_backend* b = m->b;
     const gh_model_config& c = m->cfg;
@@ -137,7 +141,10 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
     const uint32_t d = c.embedding_length, ffn = c.feed_forward_length;
     const uint32_t qw = c.head_count * c.key_length, kw = c.kv_head_count * c.key_length;
     const uint32_t vw = c.kv_head_count * c.value_length, aw = c.head_count * c.value_length;
-    int rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_ATTN_NORM], d, c.rms_epsilon, rows);
+    const bool fuse = normed != nullptr;
+    int rc = GH_OK;
+    if (!(fuse && *normed)) rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_ATTN_NORM], d, c.rms_epsilon, rows);
+    if (fuse) *normed = false;
     gh_no_barrier(b);
     if (!rc) rc = gh_matmul_batched(b, enc, &s.q, &s.normed, &w[GH_T_ATTN_Q], d, qw, rows);
     gh_no_barrier(b);
@@ -154,16 +161,35 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
     if (!rc) rc = op_kv_write(b, &m->kv, &s.k, &s.v, koff, voff, rows * c.kv_head_count, pos_ptr);
     const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base + rows - 1;
     if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, rows, li, pos_ptr, max_pos);
-    if (!rc) rc = gh_matmul_batched(b, enc, &s.proj, &s.attn, &w[GH_T_ATTN_OUTPUT], aw, d, rows);
-    if (!rc) rc = gh_residual_add(b, enc, &s.x, &s.proj, d * rows);
-    // mlp::record
-    if (!rc) rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_FFN_NORM], d, c.rms_epsilon, rows);
+    if (fuse && gemm_epi_applies(rows, d, true)) {
+        // out-projection, residual add and mlp::record's norm in one GEMM + tail
+        if (!rc) rc = op_matmul_epi(b, &s.proj, &s.attn, &w[GH_T_ATTN_OUTPUT], aw, d, rows, nullptr, &s.x,
+                                    &w[GH_T_FFN_NORM], &s.normed, c.rms_epsilon);
+    } else {
+        if (!rc) rc = gh_matmul_batched(b, enc, &s.proj, &s.attn, &w[GH_T_ATTN_OUTPUT], aw, d, rows);
+        if (!rc) rc = gh_residual_add(b, enc, &s.x, &s.proj, d * rows);
+        // mlp::record
+        if (!rc) rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_FFN_NORM], d, c.rms_epsilon, rows);
+    }
     gh_no_barrier(b);
     if (!rc) rc = gh_matmul_batched(b, enc, &s.gate, &s.normed, &w[GH_T_FFN_GATE], d, ffn, rows);
-    if (!rc) rc = gh_matmul_batched(b, enc, &s.up, &s.normed, &w[GH_T_FFN_UP], d, ffn, rows);
-    if (!rc) rc = gh_silu_mul(b, enc, &s.act, &s.gate, &s.up, ffn * rows);
-    if (!rc) rc = gh_matmul_batched(b, enc, &s.ffn_out, &s.act, &w[GH_T_FFN_DOWN], ffn, d, rows);
-    if (!rc) rc = gh_residual_add(b, enc, &s.x, &s.ffn_out, d * rows);
+    if (fuse && gemm_epi_applies(rows, ffn, false)) {
+        if (!rc) rc = op_matmul_epi(b, &s.act, &s.normed, &w[GH_T_FFN_UP], d, ffn, rows, &s.gate, nullptr);
+    } else {
+        if (!rc) rc = gh_matmul_batched(b, enc, &s.up, &s.normed, &w[GH_T_FFN_UP], d, ffn, rows);
+        if (!rc) rc = gh_silu_mul(b, enc, &s.act, &s.gate, &s.up, ffn * rows);
+    }
+    if (fuse && gemm_epi_applies(rows, d, true)) {
+        // down projection and residual add, with the next layer's attention norm when there is one
+        const bool next = li + 1 < c.block_count;
+        const gh_buf* nw = next ? &m->layers[li + 1][GH_T_ATTN_NORM] : nullptr;
+        if (!rc) rc = op_matmul_epi(b, &s.ffn_out, &s.act, &w[GH_T_FFN_DOWN], ffn, d, rows, nullptr, &s.x, nw,
+                                    next ? &s.normed : nullptr, c.rms_epsilon);
+        if (!rc) *normed = next;
+    } else {
+        if (!rc) rc = gh_matmul_batched(b, enc, &s.ffn_out, &s.act, &w[GH_T_FFN_DOWN], ffn, d, rows);
+        if (!rc) rc = gh_residual_add(b, enc, &s.x, &s.ffn_out, d * rows);
+    }
     return latch_rc(enc, rc);
 }
 
@@ -416,8 +442,9 @@ int gh_model_prefill(gh_model* m, const uint32_t* tokens, uint32_t n, uint32_t b
         if (rc) return rc;
         rc = latch_rc(enc, op_embed_rows(m->b, &m->pre.x, &m->token_embd, (const void*)(m->prompt.addr + (uint64_t)off * 4),
                                          rows, c.embedding_length));
+        bool normed = false;
         for (uint32_t li = 0; li < c.block_count && !rc; ++li)
-            rc = layer(m, enc, m->pre, li, base + off, rows, nullptr);
+            rc = layer(m, enc, m->pre, li, base + off, rows, nullptr, &normed);
         if (!rc && off + rows == n) {  // the tail belongs to the last chunk's last row
             gh_buf xr, nr;
             rc = gh_view(m->b, &m->pre.x, (rows - 1) * d * 4, d * 4, &xr);

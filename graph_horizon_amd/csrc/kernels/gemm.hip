@@ -154,6 +154,55 @@ __device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* 
     *(uint4*)(dst + 40 + 16 * part) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
 }
 
+// One FP16 output of the GEMM (its FP32 sum `acc`), with the launch's epilogue.
+__device__ __forceinline__ void gemm_store(const GhGemmArgs& a, uint64_t i, float acc) {
+    uint16_t h = gh_f2h(acc);
+    if (a.epi == GH_GEMM_EPI_SILU) h = gh_silu_mul_h(gh_gp<uint16_t>(a.aux)[i], h);
+    gh_gpw<uint16_t>(a.out)[i] = h;
+}
+
+// The accumulator tiles of one wave to memory. D of tile (i, j), register r: token
+// t0 + 32 i + 8 (r / 4) + 4 fg + r % 4, row r0 + 32 j + fm. FP32 partials of split z when the
+// launch splits K; otherwise FP16 with the epilogue. The SiLU epilogue (SILU: compiled in; the
+// warp-specialized kernels only, whose registers have room) requests a tile column's 16 x TJ
+// gate values at once (clamped addresses, no branch around the loads) before using any,
+// rather than one round trip per output.
+template <int TI, int TJ, bool SILU>
+__device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc)[TI][TJ], uint32_t t0,
+                                           uint32_t r0, uint32_t fm, uint32_t fg, uint32_t z) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        uint16_t g[16][TJ];
+        if (SILU && a.splits == 1 && a.epi == GH_GEMM_EPI_SILU) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const uint32_t t = min(t0 + 32 * i + 8 * (r >> 2) + 4 * fg + (r & 3), a.n - 1);
+                    const uint32_t row = min(r0 + 32 * j + fm, a.rows - 1);
+                    g[r][j] = gh_gp<uint16_t>(a.aux)[(uint64_t)t * a.rows + row];
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t t = t0 + 32 * i + 8 * (r >> 2) + 4 * fg + (r & 3);
+            if (t >= a.n) continue;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const uint32_t row = r0 + 32 * j + fm;
+                if (row >= a.rows) continue;
+                const uint64_t o = (uint64_t)t * a.rows + row;
+                if (a.splits > 1)
+                    gh_gpw<float>(a.part)[(uint64_t)z * a.n * a.rows + o] = acc[i][j][r];
+                else if (SILU && a.epi == GH_GEMM_EPI_SILU)
+                    gh_gpw<uint16_t>(a.out)[o] = gh_silu_mul_h(g[r][j], gh_f2h(acc[i][j][r]));
+                else
+                    gh_gpw<uint16_t>(a.out)[o] = gh_f2h(acc[i][j][r]);
+            }
+        }
+    }
+}
+
 // Tiling: 4 waves stacked along tokens; wave w owns tokens t0 + WT·w .. + WT, all BR rows of
 // the workgroup, as (WT/32) x (BR/32) tiles of v_mfma_f32_32x32x16_f16 (A = activations
 // straight from global memory into registers, B = weights from the LDS tile).
@@ -226,24 +275,7 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
         }
     }
 
-    // D of tile (i, j), register r: token t0 + 32 i + 8 (r / 4) + 4 fg + r % 4, row
-    // r0 + 32 j + fm
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t t = t0 + 32 * i + 8 * (r >> 2) + 4 * fg + (r & 3);
-            if (t >= a.n) continue;
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const uint32_t row = r0 + 32 * j + fm;
-                if (row >= a.rows) continue;
-                if (a.splits == 1)
-                    gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] = gh_f2h(acc[i][j][r]);
-                else
-                    gh_gpw<float>(a.part)[((uint64_t)blockIdx.z * a.n + t) * a.rows + row] = acc[i][j][r];
-            }
-        }
+    gemm_write<TI, TJ, false>(a, acc, t0, r0, fm, fg, blockIdx.z);
 }
 
 // Warp-specialized variant for long batches: a 512-thread workgroup owns 256 tokens x BR rows.
@@ -364,22 +396,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
         step(u + 1, 1);
     }
     if (u < u1) step(u, 0);
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t t = t0 + 32 * i + 8 * (r >> 2) + 4 * fg + (r & 3);
-            if (t >= a.n) continue;
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const uint32_t row = r0 + 32 * j + fm;
-                if (row >= a.rows) continue;
-                if (a.splits == 1)
-                    gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] = gh_f2h(acc[i][j][r]);
-                else
-                    gh_gpw<float>(a.part)[((uint64_t)blockIdx.z * a.n + t) * a.rows + row] = acc[i][j][r];
-            }
-        }
+    gemm_write<TI, TJ, true>(a, acc, t0, r0, fm, fg, blockIdx.z);
 }
 
 }  // namespace
@@ -404,6 +421,103 @@ GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce(GhGemmArgs a) {
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += groups * 256) {
         float s = 0.0f;
         for (uint32_t k = 0; k < a.splits; ++k) s += gh_gp<float>(a.part)[k * total + i];
-        gh_gpw<uint16_t>(a.out)[i] = gh_f2h(s);
+        gemm_store(a, i, s);
     }
+}
+
+// The GEMM's output row t folded into the residual stream, one 256-thread workgroup per row:
+// h = f16(Σ_s part[s][t][c]) in split order (gh_gemm_reduce; with one split the GEMM's FP16
+// output), x[t][c] += f32(h) (residual_add, residual.rs:12-22), and with a norm weight the
+// row's RMSNorm f16(x · inverse · f16 w) into `normed` — gh_rmsnorm_x's arithmetic, its Σx²
+// in gh_rms_inverse_256's order (thread t: the 16-value items t, t + 256 of the row) — so the
+// three ops' bits in one pass. rows (the row width) is a multiple of 16 and at most 8192.
+GH_KERNEL __launch_bounds__(256) void gh_gemm_tail(GhGemmArgs a) {
+#pragma clang fp contract(off)
+    const uint32_t t = blockIdx.x, d = a.rows, n4 = d >> 2;
+    const uint64_t total = (uint64_t)a.n * d, row0 = (uint64_t)t * d;
+    GH_GLOBAL float4* x = gh_gpw<float4>(a.aux) + row0 / 4;
+    __shared__ float red[4];
+    float4 v[2][4];
+    float ss = 0.0f;
+    // every load of a group of four splits is requested before any is summed (clamped chunk
+    // and split indices: no branch around the loads)
+    float4 s[2][4], xv[2][4];
+#pragma unroll
+    for (uint32_t it = 0; it < 2; ++it)
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            s[it][q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            xv[it][q] = x[min(4 * (threadIdx.x + 256 * it) + q, n4 - 1)];
+        }
+    if (a.splits > 1) {
+        for (uint32_t k0 = 0; k0 < a.splits; k0 += 4) {
+            float4 p[4][2][4];
+#pragma unroll
+            for (uint32_t kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (uint32_t it = 0; it < 2; ++it)
+#pragma unroll
+                    for (uint32_t q = 0; q < 4; ++q) {
+                        const uint32_t k = min(k0 + kk, a.splits - 1), c = min(4 * (threadIdx.x + 256 * it) + q, n4 - 1);
+                        p[kk][it][q] = gh_gp<float4>(a.part)[(k * total + row0) / 4 + c];
+                    }
+#pragma unroll
+            for (uint32_t kk = 0; kk < 4; ++kk)
+                if (k0 + kk < a.splits)
+#pragma unroll
+                    for (uint32_t it = 0; it < 2; ++it)
+#pragma unroll
+                        for (uint32_t q = 0; q < 4; ++q) {
+                            s[it][q].x += p[kk][it][q].x;
+                            s[it][q].y += p[kk][it][q].y;
+                            s[it][q].z += p[kk][it][q].z;
+                            s[it][q].w += p[kk][it][q].w;
+                        }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t it = 0; it < 2; ++it)
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                const uint2 o = gh_gp<uint2>(a.out)[row0 / 4 + min(4 * (threadIdx.x + 256 * it) + q, n4 - 1)];
+                s[it][q] = make_float4(gh_h2f(o.x & 0xFFFFu), gh_h2f(o.x >> 16), gh_h2f(o.y & 0xFFFFu), gh_h2f(o.y >> 16));
+            }
+    }
+#pragma unroll
+    for (uint32_t it = 0; it < 2; ++it)
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t c = 4 * (threadIdx.x + 256 * it) + q;
+            if (c >= n4) continue;
+            // one split: s already holds the FP16 output; several: round their sum to FP16
+            const float4 h = a.splits > 1 ? make_float4(gh_h2f(gh_f2h(s[it][q].x)), gh_h2f(gh_f2h(s[it][q].y)),
+                                                        gh_h2f(gh_f2h(s[it][q].z)), gh_h2f(gh_f2h(s[it][q].w)))
+                                          : s[it][q];
+            float4 y = xv[it][q];
+            y.x = y.x + h.x;
+            y.y = y.y + h.y;
+            y.z = y.z + h.z;
+            y.w = y.w + h.w;
+            x[c] = y;
+            v[it][q] = y;
+            ss = gh_rms_add(ss, y);
+        }
+    if (!a.norm) return;  // launch-uniform
+    const float inverse = gh_rms_finish_256(ss, d, a.eps, red);
+    const GH_GLOBAL uint2* w = gh_gp<uint2>(a.norm);
+    GH_GLOBAL uint2* out = gh_gpw<uint2>(a.normed) + row0 / 4;
+#pragma unroll
+    for (uint32_t it = 0; it < 2; ++it)
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t c = 4 * (threadIdx.x + 256 * it) + q;
+            if (c >= n4) continue;
+            const float4 xv = v[it][q];
+            const uint2 wv = w[c];
+            const uint32_t o0 = gh_f2h(xv.x * inverse * gh_h2f(wv.x & 0xFFFFu));
+            const uint32_t o1 = gh_f2h(xv.y * inverse * gh_h2f(wv.x >> 16));
+            const uint32_t o2 = gh_f2h(xv.z * inverse * gh_h2f(wv.y & 0xFFFFu));
+            const uint32_t o3 = gh_f2h(xv.w * inverse * gh_h2f(wv.y >> 16));
+            out[c] = make_uint2(o0 | (o1 << 16), o2 | (o3 << 16));
+        }
 }

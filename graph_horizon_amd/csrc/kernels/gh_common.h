@@ -88,6 +88,15 @@ __device__ __forceinline__ float gh_lane63(float v) {
 __device__ __forceinline__ float gh_wave_sum(float v) { return gh_lane63(gh_wave_sum63(v)); }
 __device__ __forceinline__ float gh_wave_max(float v) { return gh_lane63(gh_wave_max63(v)); }
 
+// silu_mul of one FP16 gate/up pair (cpu/kernels/elementwise/activation.rs:16-29):
+// f16(f16(g / (1 + e^-g)) · u) in FP32, contraction off.
+__device__ __forceinline__ uint16_t gh_silu_mul_h(uint32_t g16, uint32_t u16) {
+#pragma clang fp contract(off)
+    const float g = gh_h2f(g16), u = gh_h2f(u16);
+    const float silu = g / (1.0f + expf(-g));
+    return gh_f2h(gh_h2f(gh_f2h(silu)) * u);
+}
+
 // RMSNorm scale of one FP32 row over a 256-thread workgroup, in one fixed order (each thread
 // sums its float4 chunks tid, tid + 256, ... as (x²+y²)+(z²+w²); DPP wave sums; the four wave
 // sums added in wave order), so every kernel that uses it gets the same bits:

@@ -85,6 +85,8 @@ struct GhGemvArgs {
 };
 
 // Prefill GEMM (gemm.hip): out f16 [n][rows] (or FP32 split partials [splits][n][rows]).
+#define GH_GEMM_EPI_F16 0   // out = f16(acc)
+#define GH_GEMM_EPI_SILU 1  // out = silu_mul(gate, f16(acc)), gate FP16 [n][rows] in `aux`
 struct GhGemmArgs {
     uint64_t x;     // f16 activations [n][in_dim]
     uint64_t w;     // device layout weights [rows][in_dim]
@@ -94,6 +96,11 @@ struct GhGemmArgs {
     uint32_t rows;
     uint32_t n;
     uint32_t splits;
+    uint64_t aux;     // GH_GEMM_EPI_SILU: the gate; gh_gemm_tail: the FP32 residual x [n][rows]
+    uint64_t norm;    // gh_gemm_tail: FP16 RMSNorm weight [rows] (0: residual add only)
+    uint64_t normed;  // gh_gemm_tail: FP16 normalized rows [n][rows]
+    uint32_t epi;     // GH_GEMM_EPI_*
+    float eps;        // gh_gemm_tail
 };
 
 struct GhRmsnormArgs {

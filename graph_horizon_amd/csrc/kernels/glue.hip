@@ -49,14 +49,9 @@ GH_KERNEL __launch_bounds__(256) void gh_rope(GhRopeArgs a) {
 
 // silu_mul (cpu/kernels/elementwise/activation.rs:16-29): out = f16(f16(g/(1+exp(-g))) * u).
 GH_KERNEL __launch_bounds__(256) void gh_silu_mul(GhEltArgs a) {
-#pragma clang fp contract(off)
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= a.n) return;
-    const float g = gh_h2f(((const uint16_t*)a.a)[i]);
-    const float u = gh_h2f(((const uint16_t*)a.b)[i]);
-    const float silu = g / (1.0f + expf(-g));
-    const float rounded = gh_h2f(gh_f2h(silu));
-    ((uint16_t*)a.out)[i] = gh_f2h(rounded * u);
+    ((uint16_t*)a.out)[i] = gh_silu_mul_h(((const uint16_t*)a.a)[i], ((const uint16_t*)a.b)[i]);
 }
 
 // residual_add (cpu/kernels/elementwise/residual.rs:12-22): x(f32) += f16 y.
