@@ -148,17 +148,31 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
     gh_no_barrier(b);
     if (!rc) rc = gh_matmul_batched(b, enc, &s.q, &s.normed, &w[GH_T_ATTN_Q], d, qw, rows);
     gh_no_barrier(b);
-    if (!rc) rc = gh_matmul_batched(b, enc, &s.k, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);
-    if (!rc) rc = gh_matmul_batched(b, enc, &s.v, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
-    // rope_yarn (block.rs:147-166) / rope_yarn_batched (prefill/layer.rs:79-89)
-    if (!rc) rc = op_rope(b, m->rope, &s.q, c.head_count, c.key_length, base, rows, GH_ROPE_QUERY, pos_ptr);
-    if (!rc) rc = op_rope(b, m->rope, &s.k, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, pos_ptr);
     // kv_cache::append_batch (kv_cache/mod.rs:133-177): payload offsets of (layer, base)
     const uint64_t per_pos_k = (uint64_t)c.kv_head_count * c.key_length;
     const uint64_t per_pos_v = (uint64_t)c.kv_head_count * c.value_length;
     const uint64_t koff = ((uint64_t)li * m->kv.context + base) * per_pos_k;
     const uint64_t voff = ((uint64_t)li * m->kv.context + base) * per_pos_v;
-    if (!rc) rc = op_kv_write(b, &m->kv, &s.k, &s.v, koff, voff, rows * c.kv_head_count, pos_ptr);
+    if (fuse) {
+        // The cache rows of positions base .. base + rows - 1 ([position][kv_heads][dim]) are the
+        // K/V projections' output layout: the GEMMs write there and RoPE rotates K in place —
+        // the bytes of projecting, rotating and append_batch's copy.
+        gh_buf kd{}, vd{};
+        if (!rc) rc = gh_view(b, &m->kv.k, koff * 2, (uint64_t)rows * kw * 2, &kd);
+        if (!rc) rc = gh_view(b, &m->kv.v, voff * 2, (uint64_t)rows * vw * 2, &vd);
+        if (!rc) rc = gh_matmul_batched(b, enc, &kd, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);
+        if (!rc) rc = gh_matmul_batched(b, enc, &vd, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
+        // rope_yarn_batched (prefill/layer.rs:79-89)
+        if (!rc) rc = op_rope(b, m->rope, &s.q, c.head_count, c.key_length, base, rows, GH_ROPE_QUERY, pos_ptr);
+        if (!rc) rc = op_rope(b, m->rope, &kd, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, pos_ptr);
+    } else {
+        if (!rc) rc = gh_matmul_batched(b, enc, &s.k, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);
+        if (!rc) rc = gh_matmul_batched(b, enc, &s.v, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
+        // rope_yarn (block.rs:147-166) / rope_yarn_batched (prefill/layer.rs:79-89)
+        if (!rc) rc = op_rope(b, m->rope, &s.q, c.head_count, c.key_length, base, rows, GH_ROPE_QUERY, pos_ptr);
+        if (!rc) rc = op_rope(b, m->rope, &s.k, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, pos_ptr);
+        if (!rc) rc = op_kv_write(b, &m->kv, &s.k, &s.v, koff, voff, rows * c.kv_head_count, pos_ptr);
+    }
     const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base + rows - 1;
     if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, rows, li, pos_ptr, max_pos);
     if (fuse && gemm_epi_applies(rows, d, true)) {
