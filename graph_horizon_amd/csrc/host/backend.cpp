@@ -45,7 +45,8 @@ const KernelName kKernels[] = {
 
     {K_GEMM_Q4K_T128_R64, "gh_gemm_q4k_t128_r64"},   {K_GEMM_Q4K_T128_R128, "gh_gemm_q4k_t128_r128"},
     {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},   {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"},
-    {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
+    {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},
+    {K_GEMM_REDUCE_ROPE, "gh_gemm_reduce_rope"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
@@ -870,6 +871,22 @@ static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, u
         ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
     }
     int rc = launch(b, k, tr, tt, splits, block, &ga);
+    if (!rc && e && e->rope) {
+        if (splits == 1) {
+            gh_buf o{};
+            o.addr = out;
+            o.bytes = (uint64_t)n * w->rows * 2;
+            return op_rope(b, *e->rope, &o, w->rows / e->head_dim, e->head_dim, e->rope_base, n, e->rope_role, nullptr);
+        }
+        ga.table = (uint64_t)e->rope->table;
+        ga.post = e->rope_role == GH_ROPE_QUERY ? (uint64_t)e->rope->post : 0;
+        ga.base = e->rope_base;
+        ga.head_dim = e->head_dim;
+        ga.pairs = e->rope->yarn.rope_dim / 2;
+        const uint64_t npairs = (uint64_t)n * w->rows / 2;
+        return launch(b, K_GEMM_REDUCE_ROPE, (uint32_t)std::min<uint64_t>(ceil_div(npairs, (uint64_t)256), 4096), 1,
+                      1, 256, &ga);
+    }
     if (!rc && tail) {
         ga.aux = e->resid;
         ga.norm = e->norm;
@@ -946,6 +963,28 @@ int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_bu
         e.normed = normed ? normed->addr : 0;
         e.eps = eps;
     }
+    return op_gemm(b, out->addr, a, w, n, &e);
+}
+
+bool gemm_rope_applies(uint32_t n, uint32_t out_dim, uint32_t head_dim, const GhRopeTable& rope) {
+    return n >= kGemmMinTokens && head_dim && head_dim % 2 == 0 && out_dim % head_dim == 0 && rope.table &&
+           rope.yarn.rope_dim <= head_dim;
+}
+
+int op_matmul_rope(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,
+                   uint32_t out_dim, uint32_t n, const GhRopeTable& rope, uint32_t role, uint32_t base,
+                   uint32_t head_dim) {
+    if (!gemm_rope_applies(n, out_dim, head_dim, rope) || (uint64_t)base + n > rope.positions)
+        return fail(b, GH_E_UNSUPPORTED, "matmul rope: GEMM path, whole heads, positions in the table");
+    if (!is_weight(w)) return fail(b, GH_E_UNSUPPORTED, "matmul: weight must be Q4_K or Q6_K");
+    if (w->cols != in_dim || w->rows != out_dim) return fail(b, GH_E_INVALID, "matmul: weight shape mismatch");
+    if (!fits(a, (uint64_t)n * in_dim * 2) || !fits(out, (uint64_t)n * out_dim * 2))
+        return fail(b, GH_E_RANGE, "matmul: buffer too small");
+    GemmEpi e;
+    e.rope = &rope;
+    e.rope_role = role;
+    e.rope_base = base;
+    e.head_dim = head_dim;
     return op_gemm(b, out->addr, a, w, n, &e);
 }
 

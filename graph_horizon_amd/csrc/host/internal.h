@@ -62,6 +62,7 @@ enum GhKernel : int {
     K_GEMM_Q6K_T128_R128,
     K_GEMM_REDUCE,
     K_GEMM_TAIL,
+    K_GEMM_REDUCE_ROPE,
     K_ATTN_PREFILL_G4,
     K_GEMM3_Q4K_R128,
     K_GEMM3_Q6K_R128,
@@ -183,11 +184,15 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
 // (out = silu_mul(gate, f16(acc))). resid != 0: the output row is folded into the FP32 residual
 // x[n][out_dim] (residual_add) and, with norm != 0, its RMSNorm written to normed — the bits of
 // the separate reduce, residual_add and rmsnorm_x ops (out then only holds the FP16 projection).
+// rope != nullptr: the output rows (query or key heads of head_dim) are rotated at positions
+// base + t as op_rope does — in the split reduce, or by op_rope after an unsplit GEMM.
 struct GemmEpi {
     uint32_t epi = GH_GEMM_EPI_F16;
     uint64_t aux = 0;
     uint64_t resid = 0, norm = 0, normed = 0;
     float eps = 0.0f;
+    const GhRopeTable* rope = nullptr;
+    uint32_t rope_role = 0, rope_base = 0, head_dim = 0;
 };
 int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n,
             const GemmEpi* e = nullptr);
@@ -197,6 +202,12 @@ bool gemm_epi_applies(uint32_t n, uint32_t out_dim, bool tail);
 int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,
                   uint32_t out_dim, uint32_t n, const gh_buf* gate, const gh_buf* resid,
                   const gh_buf* norm = nullptr, const gh_buf* normed = nullptr, float eps = 0.0f);
+bool gemm_rope_applies(uint32_t n, uint32_t out_dim, uint32_t head_dim, const GhRopeTable& rope);
+// gh_matmul_batched then op_rope(role, positions base + t) on its output, the rotation folded
+// into the split reduce when the GEMM splits K (n >= 8 tokens, out_dim a multiple of head_dim).
+int op_matmul_rope(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,
+                   uint32_t out_dim, uint32_t n, const GhRopeTable& rope, uint32_t role, uint32_t base,
+                   uint32_t head_dim);
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
 uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows);
 int ensure_counters(gh_backend* b, size_t slots);

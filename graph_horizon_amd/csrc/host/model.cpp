@@ -146,8 +146,6 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
     if (!(fuse && *normed)) rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_ATTN_NORM], d, c.rms_epsilon, rows);
     if (fuse) *normed = false;
     gh_no_barrier(b);
-    if (!rc) rc = gh_matmul_batched(b, enc, &s.q, &s.normed, &w[GH_T_ATTN_Q], d, qw, rows);
-    gh_no_barrier(b);
     // kv_cache::append_batch (kv_cache/mod.rs:133-177): payload offsets of (layer, base)
     const uint64_t per_pos_k = (uint64_t)c.kv_head_count * c.key_length;
     const uint64_t per_pos_v = (uint64_t)c.kv_head_count * c.value_length;
@@ -160,12 +158,20 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
         gh_buf kd{}, vd{};
         if (!rc) rc = gh_view(b, &m->kv.k, koff * 2, (uint64_t)rows * kw * 2, &kd);
         if (!rc) rc = gh_view(b, &m->kv.v, voff * 2, (uint64_t)rows * vw * 2, &vd);
-        if (!rc) rc = gh_matmul_batched(b, enc, &kd, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);
+        // rope_yarn_batched (prefill/layer.rs:79-89) on the Q and K projections, folded into
+        // their split reduces
+        auto project_rope = [&](const gh_buf* out, const gh_buf* wt, uint32_t od, uint32_t role) {
+            if (gemm_rope_applies(rows, od, c.key_length, m->rope))
+                return op_matmul_rope(b, out, &s.normed, wt, d, od, rows, m->rope, role, base, c.key_length);
+            int r = gh_matmul_batched(b, enc, out, &s.normed, wt, d, od, rows);
+            if (!r) r = op_rope(b, m->rope, out, od / c.key_length, c.key_length, base, rows, role, nullptr);
+            return r;
+        };
+        if (!rc) rc = project_rope(&s.q, &w[GH_T_ATTN_Q], qw, GH_ROPE_QUERY);
+        if (!rc) rc = project_rope(&kd, &w[GH_T_ATTN_K], kw, GH_ROPE_KEY);
         if (!rc) rc = gh_matmul_batched(b, enc, &vd, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
-        // rope_yarn_batched (prefill/layer.rs:79-89)
-        if (!rc) rc = op_rope(b, m->rope, &s.q, c.head_count, c.key_length, base, rows, GH_ROPE_QUERY, pos_ptr);
-        if (!rc) rc = op_rope(b, m->rope, &kd, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, pos_ptr);
     } else {
+        if (!rc) rc = gh_matmul_batched(b, enc, &s.q, &s.normed, &w[GH_T_ATTN_Q], d, qw, rows);
         if (!rc) rc = gh_matmul_batched(b, enc, &s.k, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);
         if (!rc) rc = gh_matmul_batched(b, enc, &s.v, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
         // rope_yarn (block.rs:147-166) / rope_yarn_batched (prefill/layer.rs:79-89)
