@@ -46,7 +46,8 @@ const KernelName kKernels[] = {
     {K_GEMM_Q4K_T128_R64, "gh_gemm_q4k_t128_r64"},   {K_GEMM_Q4K_T128_R128, "gh_gemm_q4k_t128_r128"},
     {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},   {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"},
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},
-    {K_GEMM_REDUCE_ROPE, "gh_gemm_reduce_rope"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
+    {K_GEMM_REDUCE_ROPE, "gh_gemm_reduce_rope"}, {K_GEMM3_MIXED_R128, "gh_gemm3_mixed_r128"},
+    {K_GEMM_REDUCE_SEG, "gh_gemm_reduce_seg"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
@@ -964,6 +965,73 @@ int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_bu
         e.eps = eps;
     }
     return op_gemm(b, out->addr, a, w, n, &e);
+}
+
+bool gemm_multi_applies(uint32_t n) { return n >= 256; }
+
+int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint32_t nseg, uint32_t n,
+                  const GhRopeTable* rope, uint32_t base, uint32_t head_dim) {
+    constexpr uint32_t BR = 128;
+    if (nseg == 0 || nseg > 3 || !gemm_multi_applies(n)) return fail(b, GH_E_UNSUPPORTED, "gemm multi: 1..3 matrices, n >= 256");
+    const uint32_t in_dim = segs[0].w->cols;
+    GhGemmArgs ga{};
+    uint32_t tiles = 0, total = 0;
+    bool any_rope = false;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        const gh_buf* w = segs[i].w;
+        if (!is_weight(w) || w->cols != in_dim || w->rows % 2) return fail(b, GH_E_INVALID, "gemm multi: matrix shape");
+        if (!fits(segs[i].out, (uint64_t)n * w->rows * 2)) return fail(b, GH_E_RANGE, "gemm multi: output too small");
+        if (segs[i].role > GH_GEMM_ROLE_ROPE_KEY) return fail(b, GH_E_INVALID, "gemm multi: role");
+        if (segs[i].role) {
+            any_rope = true;
+            if (!rope || !gemm_rope_applies(n, w->rows, head_dim, *rope) || (uint64_t)base + n > rope->positions)
+                return fail(b, GH_E_UNSUPPORTED, "gemm multi: RoPE over whole heads, positions in the table");
+        }
+        ga.seg[i] = GhGemmSeg{w->addr, segs[i].out->addr, w->rows, w->format, tiles, total, segs[i].role, 0};
+        tiles += ceil_div(w->rows, BR);
+        total += w->rows;
+    }
+    if (!fits(a, (uint64_t)n * in_dim * 2)) return fail(b, GH_E_RANGE, "gemm multi: input too small");
+    const uint32_t tt = ceil_div(n, 256u), units = in_dim / 64;
+    // splits: the CUs over the tiles, at most 16 and at least 8 units per split, none empty
+    uint32_t splits = std::max<uint32_t>(1, std::min<uint32_t>({b->cus / (tiles * tt), std::max<uint32_t>(1, units / 8), 16u}));
+    for (;;) {
+        const uint32_t per = ceil_div(units, splits), s = ceil_div(units, per);
+        if (s == splits) break;
+        splits = s;
+    }
+    ga.x = a->addr;
+    ga.in_dim = in_dim;
+    ga.rows = total;
+    ga.n = n;
+    ga.splits = splits;
+    ga.nseg = nseg;
+    if (any_rope) {
+        ga.table = (uint64_t)rope->table;
+        ga.post = (uint64_t)rope->post;
+        ga.base = base;
+        ga.head_dim = head_dim;
+        ga.pairs = rope->yarn.rope_dim / 2;
+    } else {
+        ga.head_dim = 2;  // unused (no role): a nonzero divisor
+    }
+    if (splits > 1) {
+        int rc = ensure_workspace(b, (size_t)splits * n * total * 4);
+        if (rc) return rc;
+        ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
+    }
+    int rc = launch(b, K_GEMM3_MIXED_R128, tiles, tt, splits, 512, &ga);
+    if (rc) return rc;
+    if (splits > 1) {
+        const uint64_t npairs = (uint64_t)n * total / 2;
+        return launch(b, K_GEMM_REDUCE_SEG, (uint32_t)std::min<uint64_t>(ceil_div(npairs, (uint64_t)256), 4096), 1, 1,
+                      256, &ga);
+    }
+    for (uint32_t i = 0; i < nseg && !rc; ++i)
+        if (segs[i].role)
+            rc = op_rope(b, *rope, segs[i].out, segs[i].w->rows / head_dim, head_dim, base, n,
+                         segs[i].role == GH_GEMM_ROLE_ROPE_QUERY ? GH_ROPE_QUERY : GH_ROPE_KEY, nullptr);
+    return rc;
 }
 
 bool gemm_rope_applies(uint32_t n, uint32_t out_dim, uint32_t head_dim, const GhRopeTable& rope) {

@@ -63,6 +63,8 @@ enum GhKernel : int {
     K_GEMM_REDUCE,
     K_GEMM_TAIL,
     K_GEMM_REDUCE_ROPE,
+    K_GEMM3_MIXED_R128,
+    K_GEMM_REDUCE_SEG,
     K_ATTN_PREFILL_G4,
     K_GEMM3_Q4K_R128,
     K_GEMM3_Q6K_R128,
@@ -203,6 +205,18 @@ int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_bu
                   uint32_t out_dim, uint32_t n, const gh_buf* gate, const gh_buf* resid,
                   const gh_buf* norm = nullptr, const gh_buf* normed = nullptr, float eps = 0.0f);
 bool gemm_rope_applies(uint32_t n, uint32_t out_dim, uint32_t head_dim, const GhRopeTable& rope);
+// Several projections of one FP16 input (n >= 256 tokens) in one warp-specialized launch (row
+// tiles of 128, each in its matrix's format) and one split reduce that writes each matrix's
+// FP16 output and applies its RoPE role (GH_GEMM_ROLE_*; rows of head_dim, positions base + t)
+// — the values of separate gh_matmul_batched launches and op_rope.
+struct GemmSegSpec {
+    const gh_buf* w;
+    const gh_buf* out;
+    uint32_t role;
+};
+bool gemm_multi_applies(uint32_t n);
+int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint32_t nseg, uint32_t n,
+                  const GhRopeTable* rope, uint32_t base, uint32_t head_dim);
 // gh_matmul_batched then op_rope(role, positions base + t) on its output, the rotation folded
 // into the split reduce when the GEMM splits K (n >= 8 tokens, out_dim a multiple of head_dim).
 int op_matmul_rope(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,

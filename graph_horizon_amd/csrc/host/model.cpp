@@ -167,9 +167,17 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
             if (!r) r = op_rope(b, m->rope, out, od / c.key_length, c.key_length, base, rows, role, nullptr);
             return r;
         };
-        if (!rc) rc = project_rope(&s.q, &w[GH_T_ATTN_Q], qw, GH_ROPE_QUERY);
-        if (!rc) rc = project_rope(&kd, &w[GH_T_ATTN_K], kw, GH_ROPE_KEY);
-        if (!rc) rc = gh_matmul_batched(b, enc, &vd, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
+        if (gemm_multi_applies(rows)) {
+            // the three projections in one launch and one split reduce
+            const GemmSegSpec qkv[3] = {{&w[GH_T_ATTN_Q], &s.q, GH_GEMM_ROLE_ROPE_QUERY},
+                                        {&w[GH_T_ATTN_K], &kd, GH_GEMM_ROLE_ROPE_KEY},
+                                        {&w[GH_T_ATTN_V], &vd, GH_GEMM_ROLE_PLAIN}};
+            if (!rc) rc = op_gemm_multi(b, &s.normed, qkv, 3, rows, &m->rope, base, c.key_length);
+        } else {
+            if (!rc) rc = project_rope(&s.q, &w[GH_T_ATTN_Q], qw, GH_ROPE_QUERY);
+            if (!rc) rc = project_rope(&kd, &w[GH_T_ATTN_K], kw, GH_ROPE_KEY);
+            if (!rc) rc = gh_matmul_batched(b, enc, &vd, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
+        }
     } else {
         if (!rc) rc = gh_matmul_batched(b, enc, &s.q, &s.normed, &w[GH_T_ATTN_Q], d, qw, rows);
         if (!rc) rc = gh_matmul_batched(b, enc, &s.k, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);

@@ -167,9 +167,12 @@ __device__ __forceinline__ void gemm_store(const GhGemmArgs& a, uint64_t i, floa
 // warp-specialized kernels only, whose registers have room) requests a tile column's 16 x TJ
 // gate values at once (clamped addresses, no branch around the loads) before using any,
 // rather than one round trip per output.
+// Partials: element (t, row) of split z at part[z n ps + t ps + pc + row] (ps: the partials'
+// row length, pc: this matrix's first column in it).
 template <int TI, int TJ, bool SILU>
 __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc)[TI][TJ], uint32_t t0,
-                                           uint32_t r0, uint32_t fm, uint32_t fg, uint32_t z) {
+                                           uint32_t r0, uint32_t fm, uint32_t fg, uint32_t z,
+                                           uint64_t ps, uint64_t pc) {
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
         uint16_t g[16][TJ];
@@ -193,7 +196,7 @@ __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc
                 if (row >= a.rows) continue;
                 const uint64_t o = (uint64_t)t * a.rows + row;
                 if (a.splits > 1)
-                    gh_gpw<float>(a.part)[(uint64_t)z * a.n * a.rows + o] = acc[i][j][r];
+                    gh_gpw<float>(a.part)[((uint64_t)z * a.n + t) * ps + pc + row] = acc[i][j][r];
                 else if (SILU && a.epi == GH_GEMM_EPI_SILU)
                     gh_gpw<uint16_t>(a.out)[o] = gh_silu_mul_h(g[r][j], gh_f2h(acc[i][j][r]));
                 else
@@ -275,7 +278,7 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
         }
     }
 
-    gemm_write<TI, TJ, false>(a, acc, t0, r0, fm, fg, blockIdx.z);
+    gemm_write<TI, TJ, false>(a, acc, t0, r0, fm, fg, blockIdx.z, a.rows, 0);
 }
 
 // Warp-specialized variant for long batches: a 512-thread workgroup owns 256 tokens x BR rows.
@@ -285,18 +288,22 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
 // and dequantize each unit into a kS-stage LDS ring, kS - 1 units ahead of the consumers. One
 // barrier per unit: in the interval of unit u the consumers read stage (u - u0) % kS while the
 // producers fill unit u + kS - 1 into the stage read during unit u - 1.
+// LDS of gemm3_body: kS = 3 weight stages, then each consumer wave's two activation buffers.
+#define GH_GEMM3_LDS(BR) (3 * (BR) * LDK + 4 * 2 * 64 * 64)
+
+// Tile (bx, by) and split bz of one matrix (a.w, a.rows, a.out); lds3 holds GH_GEMM3_LDS(BR)
+// halves; partials go to columns pc .. of rows ps long.
 template <uint32_t FMT, int BR>
-__device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
+__device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, uint32_t bx, uint32_t by,
+                                           uint32_t bz, uint64_t ps, uint64_t pc) {
     constexpr int WT = 64, TI = WT / 32, TJ = BR / 32;
     constexpr int kS = 3, kL = 4;
-    // one LDS block: kS weight stages, then each consumer wave's activation rows
-    __shared__ __attribute__((aligned(16))) _Float16 lds3[kS * BR * LDK + 4 * 2 * WT * 64];
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t r0 = blockIdx.x * BR;
+    const uint32_t r0 = bx * BR;
     const uint32_t units = a.in_dim / 64;
     const uint32_t per = (units + a.splits - 1) / a.splits;
-    const uint32_t u0 = blockIdx.z * per, u1 = min(units, u0 + per);
+    const uint32_t u0 = bz * per, u1 = min(units, u0 + per);
     if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
     auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };
 
@@ -336,7 +343,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
     // rows (only this wave touches them; the per-unit barrier's wait completes the loads), from
     // which the A fragments are read — each 128-byte line is requested once instead of once per
     // 16-k step, and no registers hold it on the way (8B prefill gate/up 85 -> 80 us).
-    const uint32_t t0 = blockIdx.y * (4 * WT) + wave * WT;
+    const uint32_t t0 = by * (4 * WT) + wave * WT;
     const uint32_t fm = lane & 31u, fg = lane >> 5;
     const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
     uint32_t xrow[8];
@@ -396,7 +403,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
         step(u + 1, 1);
     }
     if (u < u1) step(u, 0);
-    gemm_write<TI, TJ, true>(a, acc, t0, r0, fm, fg, blockIdx.z);
+    gemm_write<TI, TJ, true>(a, acc, t0, r0, fm, fg, bz, ps, pc);
 }
 
 }  // namespace
@@ -408,10 +415,35 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a) {
 GH_GEMM(t128_r64, 32, 64)
 GH_GEMM(t128_r128, 32, 128)
 // warp-specialized 256-token tiles (512 threads)
-GH_KERNEL __launch_bounds__(512) void gh_gemm3_q4k_r128(GhGemmArgs a) { gemm3_body<kQ4K, 128>(a); }
-GH_KERNEL __launch_bounds__(512) void gh_gemm3_q6k_r128(GhGemmArgs a) { gemm3_body<kQ6K, 128>(a); }
-GH_KERNEL __launch_bounds__(512) void gh_gemm3_q4k_r96(GhGemmArgs a) { gemm3_body<kQ4K, 96>(a); }
-GH_KERNEL __launch_bounds__(512) void gh_gemm3_q6k_r96(GhGemmArgs a) { gemm3_body<kQ6K, 96>(a); }
+#define GH_GEMM3(NAME, FMT, BR)                                                                    \
+    GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
+        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(BR)];                   \
+        gemm3_body<FMT, BR>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);                \
+    }
+GH_GEMM3(gh_gemm3_q4k_r128, kQ4K, 128)
+GH_GEMM3(gh_gemm3_q6k_r128, kQ6K, 128)
+GH_GEMM3(gh_gemm3_q4k_r96, kQ4K, 96)
+GH_GEMM3(gh_gemm3_q6k_r96, kQ6K, 96)
+
+// Several matrices of one input in one launch (the prefill's Q, K and V projections): row tile
+// blockIdx.x belongs to the matrix whose tiles start at or below it, and runs that matrix's
+// format (Q4_K or Q6_K) over the shared LDS block; a.rows is the total row count, the
+// partials' row length.
+GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(128)];
+    uint32_t s = 0;
+    for (uint32_t i = 1; i < a.nseg; ++i)
+        if (blockIdx.x >= a.seg[i].tile0) s = i;
+    GhGemmArgs m = a;
+    m.w = a.seg[s].w;
+    m.rows = a.seg[s].rows;
+    m.out = a.seg[s].out;
+    const uint32_t bx = blockIdx.x - a.seg[s].tile0;
+    if (a.seg[s].fmt == kQ4K)
+        gemm3_body<kQ4K, 128>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+    else
+        gemm3_body<kQ6K, 128>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+}
 
 // Sum split-K partials in split order, round to FP16: out[i] = f16(Σ_s part[s][i]).
 GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce(GhGemmArgs a) {
@@ -453,6 +485,42 @@ GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce_rope(GhGemmArgs a) {
             h1 = gh_f2h((x0 * cs.y + x1 * cs.x) * scale);
         }
         gh_gpw<uint32_t>(a.out)[k] = h0 | (h1 << 16);
+    }
+}
+
+// Split-K sum of a multi-matrix launch (partials [splits][n][Σ rows]): one thread per adjacent
+// column pair, summed in split order and rounded to FP16 as gh_gemm_reduce does, then, for a
+// matrix with a RoPE role, rotated as gh_gemm_reduce_rope does; written to the matrix's own
+// output [n][rows].
+GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce_seg(GhGemmArgs a) {
+#pragma clang fp contract(off)
+    const uint64_t total = (uint64_t)a.n * a.rows, npairs = total / 2;
+    const uint64_t groups = min((npairs + 255) / 256, (uint64_t)4096);
+    for (uint64_t k = (uint64_t)blockIdx.x * 256 + threadIdx.x; k < npairs; k += groups * 256) {
+        const uint64_t i = 2 * k;
+        float s0 = 0.0f, s1 = 0.0f;
+        for (uint32_t z = 0; z < a.splits; ++z) {
+            const float2 p = gh_gp<float2>(a.part)[(z * total + i) / 2];
+            s0 += p.x;
+            s1 += p.y;
+        }
+        const uint32_t t = (uint32_t)(i / a.rows), col = (uint32_t)(i % a.rows);
+        uint32_t sg = 0;
+        for (uint32_t j = 1; j < a.nseg; ++j)
+            if (col >= a.seg[j].col0) sg = j;
+        const GhGemmSeg g = a.seg[sg];
+        const uint32_t c = col - g.col0;
+        uint32_t h0 = gh_f2h(s0), h1 = gh_f2h(s1);
+        const uint32_t pair = (c % a.head_dim) / 2;
+        if (g.role && pair < a.pairs) {
+            const uint32_t pos = a.base + t;
+            const float2 cs = gh_gp<float2>(a.table)[(uint64_t)pos * a.pairs + pair];
+            const float scale = g.role == GH_GEMM_ROLE_ROPE_QUERY ? gh_gp<float>(a.post)[pos] : 1.0f;
+            const float x0 = gh_h2f(h0), x1 = gh_h2f(h1);
+            h0 = gh_f2h((x0 * cs.x - x1 * cs.y) * scale);
+            h1 = gh_f2h((x0 * cs.y + x1 * cs.x) * scale);
+        }
+        gh_gpw<uint32_t>(g.out)[((uint64_t)t * g.rows + c) / 2] = h0 | (h1 << 16);
     }
 }
 

@@ -84,6 +84,23 @@ struct GhGemvArgs {
                        // from the dispatch packet, whose fields cost a memory round trip
 };
 
+// One matrix of a multi-matrix prefill GEMM launch (gh_gemm3_mixed_*): row tiles
+// [tile0, next tile0) of the launch belong to it; its columns sit at col0 .. col0 + rows - 1 of
+// the launch's FP32 partials [splits][n][Σ rows].
+#define GH_GEMM_ROLE_PLAIN 0
+#define GH_GEMM_ROLE_ROPE_QUERY 1  // RoPE with the query post-scale
+#define GH_GEMM_ROLE_ROPE_KEY 2    // RoPE without post-scale
+struct GhGemmSeg {
+    uint64_t w;      // device layout weights [rows][in_dim]
+    uint64_t out;    // f16 [n][rows]
+    uint32_t rows;
+    uint32_t fmt;    // 12 = Q4_K, 14 = Q6_K
+    uint32_t tile0;
+    uint32_t col0;
+    uint32_t role;   // split reduce: GH_GEMM_ROLE_*
+    uint32_t pad;
+};
+
 // Prefill GEMM (gemm.hip): out f16 [n][rows] (or FP32 split partials [splits][n][rows]).
 #define GH_GEMM_EPI_F16 0   // out = f16(acc)
 #define GH_GEMM_EPI_SILU 1  // out = silu_mul(gate, f16(acc)), gate FP16 [n][rows] in `aux`
@@ -106,7 +123,8 @@ struct GhGemmArgs {
     uint32_t base;    // gh_gemm_reduce_rope: position of token 0
     uint32_t head_dim;
     uint32_t pairs;   // rope_dim / 2 (pairs rotated per head)
-    uint32_t pad;
+    uint32_t nseg;    // > 0: gh_gemm3_mixed_* / gh_gemm_reduce_seg over seg[] (rows = Σ rows)
+    GhGemmSeg seg[3];
 };
 
 struct GhRmsnormArgs {

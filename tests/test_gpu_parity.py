@@ -523,8 +523,12 @@ def test_fused_decode_is_bit_identical_to_op_by_op(hip, shape_name):
 @pytest.mark.parametrize("n", [37, 300])
 def test_prefill_driver_is_bit_identical_to_op_by_op(hip, n):
     """The driver's prefill (one batch: GEMV for n < 8 rows, the MFMA GEMMs above, the
-    warp-specialized ones from 256 rows) leaves the same logits and KV bits as recording every
-    trait op separately (prefill::record_batch over the C ABI)."""
+    warp-specialized ones from 256 rows, with the glue folded into GEMM epilogues and split
+    reduces and Q/K/V in one launch) leaves the same logits and KV bits as recording every
+    trait op separately (prefill::record_batch over the C ABI). The tiny shape's GEMMs run one
+    K split each, so the fused and the separate launches sum in the same order; where the split
+    counts differ (the 8B shape's Q/K/V: 2 in the fused launch, 4/16/16 alone) the results
+    differ only by FP32 re-association, checked against the oracle in test_gpu_model_shapes."""
     from graph_horizon_amd import HipModel
     from graph_over_abi import AbiGraph
 
