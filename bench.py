@@ -39,7 +39,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 # rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --traffic-probe`, each scaled by
 # the same counter's reading for a 256 MiB device-to-device copy (profiles/q4k_gemv_c1_4096x4096.txt).
 # Re-measure whenever the kernel changes.
-ROOFLINE_TRAFFIC_BYTES = 9605002
+ROOFLINE_TRAFFIC_BYTES = 9596715
 
 
 def log(*a):
