@@ -48,6 +48,7 @@ const KernelName kKernels[] = {
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},
     {K_GEMM_REDUCE_ROPE, "gh_gemm_reduce_rope"}, {K_GEMM3_MIXED_R128, "gh_gemm3_mixed_r128"},
     {K_GEMM_REDUCE_SEG, "gh_gemm_reduce_seg"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
+    {K_ATTN_PREFILL_G4_R16, "gh_attn_prefill_g4_r16"},
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
@@ -330,7 +331,10 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.rows = rows;
         a.scale = 1.0f / std::sqrt((float)kv->head_dim);
         // 32 query rows per workgroup (K/V tiles shared by twice the rows of 16-row blocks;
-        // 248 VGPRs keep two workgroups resident per CU)
+        // 248 VGPRs keep two workgroups resident per CU), 16 when 32-row blocks would leave
+        // CUs without a workgroup
+        if ((uint64_t)ceil_div(rows, 32) * kv->kv_heads < b->cus)
+            return launch(b, K_ATTN_PREFILL_G4_R16, ceil_div(rows, 16), kv->kv_heads, 1, 256, &a);
         return launch(b, K_ATTN_PREFILL_G4, ceil_div(rows, 32), kv->kv_heads, 1, 256, &a);
     }
     // decode reads a layer's K/V through 32-bit buffer ranges

@@ -66,6 +66,7 @@ enum GhKernel : int {
     K_GEMM3_MIXED_R128,
     K_GEMM_REDUCE_SEG,
     K_ATTN_PREFILL_G4,
+    K_ATTN_PREFILL_G4_R16,
     K_GEMM3_Q4K_R128,
     K_GEMM3_Q6K_R128,
     K_GEMM3_Q4K_R96,

@@ -792,3 +792,6 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
 }  // namespace
 
 GH_KERNEL __launch_bounds__(256) void gh_attn_prefill_g4(GhAttnArgs a) { attn_prefill_g4<2>(a); }
+// 16 query rows per workgroup: twice the workgroups, for row counts whose 32-row blocks leave
+// CUs idle
+GH_KERNEL __launch_bounds__(256) void gh_attn_prefill_g4_r16(GhAttnArgs a) { attn_prefill_g4<1>(a); }
