@@ -74,6 +74,7 @@ class GhModelConfig(C.Structure):
 
 
 MODEL_NO_GRAPH = 1
+MODEL_NO_F16_WEIGHTS = 2
 
 
 class GhGgufTensorInfo(C.Structure):

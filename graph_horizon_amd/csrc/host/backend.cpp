@@ -53,6 +53,10 @@ const KernelName kKernels[] = {
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
     {K_FILL_U32, "gh_fill_u32"},
+    {K_GEMM3W_Q4K_R128, "gh_gemm3w_q4k_r128"}, {K_GEMM3W_Q6K_R128, "gh_gemm3w_q6k_r128"},
+    {K_GEMM3W_Q4K_R96, "gh_gemm3w_q4k_r96"},   {K_GEMM3W_Q6K_R96, "gh_gemm3w_q6k_r96"},
+    {K_GEMM3W_MIXED_R128, "gh_gemm3w_mixed_r128"},
+    {K_DEQUANT_F16_Q4K, "gh_dequant_f16_q4k"}, {K_DEQUANT_F16_Q6K, "gh_dequant_f16_q6k"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -683,6 +687,7 @@ int gh_free_buffer(gh_backend* b, gh_buf* buf) {
         return fail(b, GH_E_INVALID, "free_buffer: a view never owns its storage");
     int rc = hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
     if (!rc) rc = hip_check(b, hipFree((void*)buf->addr), "hipFree");
+    if (buf->kind == GH_BUF_WEIGHT) b->w16.erase(buf->addr);  // its FP16 copy no longer applies
     *buf = gh_buf{};
     return rc;
 }
@@ -853,9 +858,10 @@ constexpr GemmTile kGemmTiles[2] = {{128, 64, 0}, {128, 128, 1}};
 // FP32 partials to the workspace and gh_gemm_reduce sums them in split order. `e` adds the
 // SiLU epilogue (in the GEMM or the reduce) or replaces the reduce by gh_gemm_tail (residual
 // add and RMSNorm of each output row).
+// w16: the registered FP16 copy of w that the kernel reads instead of w (0: none)
 static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, uint32_t tt,
                        uint32_t splits, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n,
-                       const GemmEpi* e) {
+                       const GemmEpi* e, uint64_t w16 = 0) {
     // the kernels give split z the units [z per, min(units, (z + 1) per)), per = ceil(units /
     // splits): shrink splits to ceil(units / per) until every split is non-empty
     const uint32_t units = w->cols / 64;
@@ -864,7 +870,7 @@ static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, u
         if (s == splits) break;
         splits = s;
     }
-    GhGemmArgs ga{a->addr, w->addr, out, 0, w->cols, w->rows, n, splits};
+    GhGemmArgs ga{a->addr, w16 ? w16 : w->addr, out, 0, w->cols, w->rows, n, splits};
     const bool tail = e && e->resid;
     if (e && !tail) {
         ga.epi = e->epi;
@@ -926,11 +932,18 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         };
         const bool narrow = rows <= 1024;
         const uint32_t br = narrow || fill(96) > fill(128) ? 96u : 128u;
-        const GhKernel k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96 : K_GEMM3_Q6K_R96)
-                                    : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
+        GhKernel k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96 : K_GEMM3_Q6K_R96) : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
         const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
         const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
-        return gemm_launch(b, k, 512, tr, tt, clamp_splits(std::max<uint32_t>(1, slots / tiles)), out, a, w, n, e);
+        const uint32_t splits = clamp_splits(std::max<uint32_t>(1, slots / tiles));
+        // a registered FP16 copy of w, where each split streams enough units to hide the
+        // copy's start: the same tiles with the weights copied, not dequantized
+        const auto copy = b->w16.find(w->addr);
+        const uint64_t w16 =
+            copy != b->w16.end() && ceil_div(units, splits) >= kGemmCopyMinUnits ? copy->second : 0;
+        if (w16)
+            k = br == 96 ? (q4 ? K_GEMM3W_Q4K_R96 : K_GEMM3W_Q6K_R96) : (q4 ? K_GEMM3W_Q4K_R128 : K_GEMM3W_Q6K_R128);
+        return gemm_launch(b, k, 512, tr, tt, splits, out, a, w, n, e, w16);
     }
     const GemmTile tile = rows >= 4096 ? kGemmTiles[1] : kGemmTiles[0];
     const GhKernel k = (GhKernel)((q4 ? K_GEMM_Q4K_T128_R64 : K_GEMM_Q6K_T128_R64) + tile.index);
@@ -1004,6 +1017,12 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
         if (s == splits) break;
         splits = s;
     }
+    // FP16 copies registered for every matrix, and splits long enough to hide their start:
+    // the launch copies the weights instead of dequantizing them
+    bool copies = ceil_div(units, splits) >= kGemmCopyMinUnits;
+    for (uint32_t i = 0; i < nseg; ++i) copies = copies && b->w16.count(segs[i].w->addr);
+    if (copies)
+        for (uint32_t i = 0; i < nseg; ++i) ga.seg[i].w = b->w16.at(segs[i].w->addr);
     ga.x = a->addr;
     ga.in_dim = in_dim;
     ga.rows = total;
@@ -1024,7 +1043,7 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
         if (rc) return rc;
         ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
     }
-    int rc = launch(b, K_GEMM3_MIXED_R128, tiles, tt, splits, 512, &ga);
+    int rc = launch(b, copies ? K_GEMM3W_MIXED_R128 : K_GEMM3_MIXED_R128, tiles, tt, splits, 512, &ga);
     if (rc) return rc;
     if (splits > 1) {
         const uint64_t npairs = (uint64_t)n * total / 2;
@@ -1036,6 +1055,18 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
             rc = op_rope(b, *rope, segs[i].out, segs[i].w->rows / head_dim, head_dim, base, n,
                          segs[i].role == GH_GEMM_ROLE_ROPE_QUERY ? GH_ROPE_QUERY : GH_ROPE_KEY, nullptr);
     return rc;
+}
+
+int op_dequant_f16(gh_backend* b, const gh_buf* w, uint64_t out16) {
+    if (!is_weight(w)) return fail(b, GH_E_UNSUPPORTED, "dequant f16: weight must be Q4_K or Q6_K");
+    GhGemmArgs ga{};
+    ga.w = w->addr;
+    ga.out = out16;
+    ga.in_dim = w->cols;
+    ga.rows = w->rows;
+    const uint64_t threads = (uint64_t)w->rows * (w->cols / 64) * 2;
+    return launch(b, w->format == GH_FMT_Q4_K ? K_DEQUANT_F16_Q4K : K_DEQUANT_F16_Q6K, ceil_div(threads, 256), 1, 1,
+                  256, &ga);
 }
 
 bool gemm_rope_applies(uint32_t n, uint32_t out_dim, uint32_t head_dim, const GhRopeTable& rope) {

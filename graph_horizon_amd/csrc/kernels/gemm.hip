@@ -293,7 +293,13 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
 
 // Tile (bx, by) and split bz of one matrix (a.w, a.rows, a.out); lds3 holds GH_GEMM3_LDS(BR)
 // halves; partials go to columns pc .. of rows ps long.
-template <uint32_t FMT, int BR>
+// F16W: a.w is the matrix already dequantized (gh_dequant_f16: row r's unit u is the 64 FP16
+// weights store_w would write, at a.w + (r · units + u) · 128 bytes). The producer waves then
+// copy each unit's rows into the stage with LDS DMA, no dequantization: a stage row is 128
+// bytes with chunk c at slot c ^ sw(r), the activations' layout, and the consumers read B
+// fragments as they read A. Same FP16 values, same MFMA order: the same bits as the Q4_K /
+// Q6_K form.
+template <uint32_t FMT, int BR, bool F16W = false>
 __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
     constexpr int WT = 64, TI = WT / 32, TJ = BR / 32;
@@ -307,6 +313,46 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
     auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };
 
+    if (F16W && wave >= 4) {
+        // ---- producers, FP16 weights: kD DMA loads of 8 rows x 128 bytes per wave and unit ----
+        // Issued from inline assembly (outside the compiler's wait counting): the wave waits for
+        // them itself. The unit of interval kk goes into stage (kk + 2) % 3, whose previous unit
+        // was read before the barrier that ended interval kk - 1, and must have landed by the
+        // barrier that ends interval kk + 1: each interval waits for all but its own kD loads.
+        constexpr int kD = BR / 32;
+        static_assert(kD == 3 || kD == 4, "F16W producers: 96 or 128 rows");
+        const uint32_t pw = wave - 4;
+        uint64_t src[kD];
+#pragma unroll
+        for (int i = 0; i < kD; ++i) {
+            const uint32_t rr = 8 * (pw * kD + i) + (lane >> 3), c = (lane & 7u) ^ ((rr >> 1) & 7u);
+            src[i] = a.w + ((uint64_t)min(r0 + rr, a.rows - 1) * units) * 128 + c * 16;
+        }
+        auto issue = [&](uint32_t u, uint32_t st) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < kD; ++i) {
+                const uint32_t dst =
+                    (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(wstage(st) + (pw * kD + i) * 512);
+                asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src[i] + (uint64_t)u * 128),
+                             "{m0}"(__builtin_amdgcn_readfirstlane(dst))
+                             : "memory");
+            }
+        };
+        issue(u0, 0);
+        issue(uc(u0 + 1), 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (uint32_t kk = 0; kk < u1 - u0; ++kk) {
+            issue(uc(u0 + kk + kS - 1), (kk + kS - 1) % kS);
+            if constexpr (kD == 3)
+                asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            __syncthreads();
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) loads have landed
+        return;
+    }
     if (wave >= 4) {
         // ---- producers ----
         const uint32_t pt = threadIdx.x - 256;
@@ -387,7 +433,14 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
                 af[i] = *(const h8*)(xb + r * 64 + c * 8);
             }
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
+            for (int j = 0; j < TJ; ++j) {
+                if constexpr (F16W) {
+                    const uint32_t r = 32 * j + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
+                    bf[j] = *(const h8*)(wb + r * 64 + c * 8);
+                } else {
+                    bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
+                }
+            }
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -424,6 +477,33 @@ GH_GEMM3(gh_gemm3_q4k_r128, kQ4K, 128)
 GH_GEMM3(gh_gemm3_q6k_r128, kQ6K, 128)
 GH_GEMM3(gh_gemm3_q4k_r96, kQ4K, 96)
 GH_GEMM3(gh_gemm3_q6k_r96, kQ6K, 96)
+// the same tiles over FP16 weights from gh_dequant_f16 (a.w), copied into LDS by DMA
+#define GH_GEMM3W(NAME, FMT, BR)                                                                   \
+    GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
+        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(BR)];                   \
+        gemm3_body<FMT, BR, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);          \
+    }
+GH_GEMM3W(gh_gemm3w_q4k_r128, kQ4K, 128)
+GH_GEMM3W(gh_gemm3w_q6k_r128, kQ6K, 128)
+GH_GEMM3W(gh_gemm3w_q4k_r96, kQ4K, 96)
+GH_GEMM3W(gh_gemm3w_q6k_r96, kQ6K, 96)
+
+// A Q4_K / Q6_K matrix [rows][in_dim] dequantized to FP16 in the GEMM's unit order (the layout
+// gemm3_body<F16W> reads): thread t handles half p = t % 2 of unit u of row r, t / 2 = r · units
+// + u, with load_w and store_w (one row per "tile"), so each value is the one the dequantizing
+// producers stage. a.w: device layout, a.out: FP16 [rows][units][64].
+template <uint32_t FMT>
+__device__ __forceinline__ void dequant_f16(const GhGemmArgs& a) {
+    const uint32_t units = a.in_dim / 64;
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x, ru = t >> 1;
+    if (ru >= (uint64_t)a.rows * units) return;
+    const uint32_t p = (uint32_t)(t & 1u), r = (uint32_t)(ru / units), u = (uint32_t)(ru % units);
+    WStage ws;
+    load_w<FMT, 1>(a, r, u, ws, p);
+    store_w<FMT, 1>(u, ws, (_Float16*)(uintptr_t)a.out + ru * 64, p);
+}
+GH_KERNEL __launch_bounds__(256) void gh_dequant_f16_q4k(GhGemmArgs a) { dequant_f16<kQ4K>(a); }
+GH_KERNEL __launch_bounds__(256) void gh_dequant_f16_q6k(GhGemmArgs a) { dequant_f16<kQ6K>(a); }
 
 // Several matrices of one input in one launch (the prefill's Q, K and V projections): row tile
 // blockIdx.x belongs to the matrix whose tiles start at or below it, and runs that matrix's
@@ -443,6 +523,23 @@ GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128(GhGemmArgs a) {
         gemm3_body<kQ4K, 128>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
     else
         gemm3_body<kQ6K, 128>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+}
+
+// The multi-matrix launch over FP16 weights (each segment's w from gh_dequant_f16).
+GH_KERNEL __launch_bounds__(512) void gh_gemm3w_mixed_r128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(128)];
+    uint32_t s = 0;
+    for (uint32_t i = 1; i < a.nseg; ++i)
+        if (blockIdx.x >= a.seg[i].tile0) s = i;
+    GhGemmArgs m = a;
+    m.w = a.seg[s].w;
+    m.rows = a.seg[s].rows;
+    m.out = a.seg[s].out;
+    const uint32_t bx = blockIdx.x - a.seg[s].tile0;
+    if (a.seg[s].fmt == kQ4K)
+        gemm3_body<kQ4K, 128, true>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+    else
+        gemm3_body<kQ6K, 128, true>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
 }
 
 // Sum split-K partials in split order, round to FP16: out[i] = f16(Σ_s part[s][i]).

@@ -90,3 +90,33 @@ def test_full_width_prefill_driver_matches_op_by_op(hip, name):
         assert err.max() <= 2e-3 * np.abs(b).max(), (role, float(err.max()), float(np.abs(b).max()))
         assert np.mean(err > 0) < 1e-2, (role, float(np.mean(err > 0)))  # isolated FP16 flips (0.2 %)
     gm.close()
+
+
+@pytest.mark.parametrize("n", [1024, 2048])
+@pytest.mark.parametrize("name", ["8b", "14b"])
+def test_prefill_fp16_weight_copies_are_bit_identical(hip, name, n):
+    """The FP16 copies of the layer matrices (made before the first prefill with chunks of 1024
+    rows or more) hold the values the dequantizing GEMM producers stage, and the GEMMs run the
+    same MFMAs over them: the prefill leaves the same logits, residual row and K/V cache bits as
+    with GH_MODEL_NO_F16_WEIGHTS. The GEMMs take the copies where each K split streams 48 units
+    or more: at 1024 rows the mixed Q/K/V launch, the 96-row gate/up and the Q6_K down, at 2048
+    rows also the 128-row Q4_K tiles (gate/up, O)."""
+    from graph_horizon_amd import _ffi as F
+
+    shape = dataclasses.replace(synth.SHAPES[name], name=f"{name}-1", block_count=1)
+    seed, ctx = 17, max(320, n)
+    tensors = list(synth.model_tensors(shape, seed))
+    toks = [int(t) for t in np.random.default_rng(seed).integers(0, shape.vocab_size, n)]
+    outs = []
+    for flags in (0, F.MODEL_NO_F16_WEIGHTS):
+        gm = HipModel(hip, synth.model_config(shape, ctx, prefill_rows=max(512, n), flags=flags))
+        for layer, tid, fmt, data in tensors:
+            gm.load_tensor(layer, tid, fmt, data)
+        gm.prefill(toks, 0)
+        kv = gm.kv()
+        m = shape.block_count * ctx * shape.kv_head_count * shape.head_dim
+        outs.append((gm.read_logits().view(np.uint32), gm.read_x().view(np.uint32),
+                     hip.download(kv.k, np.uint16, m), hip.download(kv.v, np.uint16, m)))
+        gm.close()
+    for got, want, what in zip(outs[0], outs[1], ("logits", "x", "k", "v")):
+        assert np.array_equal(got, want), what
