@@ -12,8 +12,9 @@ Also reported on the same line:
   roofline      the metric's GEMV: Q4_K 4096x4096 with x ~ N(0,1), launched back to
                 back over the model's 68 distinct Q and O weights (642 MB, beyond the 256 MB
                 MALL), timed with HIP events on the backend stream;
-  config        the 12288x4096 gate/up-shape GEMV, the C3 prefill GEMMs, the C4 attention cases
-                and the C5 14B-shaped decoder (512-token prefill, greedy decode);
+  config        the 12288x4096 gate/up-shape GEMV, the C3 prefill GEMMs, a 2048-token prefill
+                (one chunk of the policy's size, over the FP16 weight copies), the C4 attention
+                cases and the C5 14B-shaped decoder (512-token prefill, greedy decode);
   cpu_baseline  the CPU oracle (a C++ restatement of the reference's AVX2 CPU kernels) on all
                 host cores: greedy decode steps of the same 8B model, resumed from the GPU's
                 512-token KV cache, for a bounded time; plus the C1 GEMV and C4 decode attention.
@@ -249,6 +250,7 @@ def main():
     }
     result["config"]["prefill_gemm_c3"] = prefill_gemm(hip, model, shape, 512)
     model.close()
+    result["config"]["prefill_2048"] = prefill_long(hip, shape, tensors, 2048)
     result["config"]["attention_c4"] = c4_attention(hip)
     if not args.no_c5:
         result["config"]["decoder_c5"] = c5_decoder(hip, HipModel, args.prompt)
@@ -412,6 +414,25 @@ def gemm_probe(shape, n=512):
             hip.free_buffer(b)
     log(f"bench: gemm probe: 32 x {n}x{d}->{ffn} Q4_K, 32 x {n}x{ffn}->{d} Q6_K")
     hip.close()
+
+
+def prefill_long(hip, shape, tensors, n):
+    """A long prompt through the prefill policy's 2048-row chunks: the same 8B-shaped weights in
+    a model of n positions, one n-token chunk. Its first prefill (untimed) also makes the FP16
+    copies of the layer matrices that chunks of 1024 rows or more use; the second is timed."""
+    model = HipModel(hip, synth.model_config(shape, n, prefill_rows=n))
+    for layer, tid, fmt, data in tensors:
+        model.load_tensor(layer, tid, fmt, data)
+    prompt = np.random.default_rng(11).integers(0, shape.vocab_size, n).astype(np.uint32)
+    model.prefill(prompt, 0)
+    hip.synchronize()
+    hip.timer_start()
+    model.prefill(prompt, 0)
+    ms = hip.timer_stop()
+    model.close()
+    log(f"bench: prefill {n} tokens (one chunk, FP16 weight copies) in {ms:.2f} ms ({n / (ms / 1e3):.0f} tok/s)")
+    return {"tokens": n, "chunk_rows": n, "ms": round(ms, 3), "tok_s": round(n / (ms / 1e3), 1),
+            "fp16_weight_copies": True}
 
 
 def prefill_gemm(hip, model, shape, n):
