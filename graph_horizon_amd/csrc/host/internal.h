@@ -75,13 +75,13 @@ enum GhKernel : int {
     K_TOPK_PARTIAL,
     K_TOPK_FINAL,
     K_FILL_U32,
-    K_GEMM3W_Q4K_R128,
-    K_GEMM3W_Q6K_R128,
     K_GEMM3W_Q4K_R96,
     K_GEMM3W_Q6K_R96,
-    K_GEMM3W_MIXED_R128,
     K_DEQUANT_F16_Q4K,
     K_DEQUANT_F16_Q6K,
+    K_GEMM4W_Q4K_R128,
+    K_GEMM4W_Q6K_R128,
+    K_GEMM4W_MIXED_R128,
     K_COUNT
 };
 
@@ -122,8 +122,7 @@ struct gh_backend {
     uint32_t attn_splits = 0;  // gh_set_attention_splits: 0 = attention_splits' policy
     void* noalloc_scratch = nullptr;  // this device's copy of the no-allocation scratch array
     // FP16 copies of weights (gh_dequant_f16 layout), by the weight's device address: the
-    // warp-specialized GEMMs read a registered copy instead of dequantizing (same values)
-    // when each K split streams at least kGemmCopyMinUnits units.
+    // warp-specialized GEMMs read a registered copy instead of dequantizing (same values).
     // Registered and dropped by their owner (a model); gh_free_buffer of a weight drops its entry.
     std::unordered_map<uint64_t, uint64_t> w16;
     uint64_t gen = 0;  // bumped whenever the workspace or rope table moves (captured graphs hold them)
@@ -179,11 +178,6 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
 // w (Q4_K / Q6_K) dequantized to FP16 at out16 (rows x cols x 2 bytes) in the layout the GEMMs
 // read registered copies in: row r, unit u (64 weights) at out16 + (r · cols / 64 + u) · 128.
 int op_dequant_f16(gh_backend* b, const gh_buf* w, uint64_t out16);
-// Splits of fewer 64-weight units run faster dequantizing: the copy's first units arrive
-// later than the raw blocks' (measured on the 8B prefill at 512 tokens: O with 16 units per
-// split 37.2 -> 44.7 us, Q/K/V with 32 57.0 -> 64.1 us, down with 48 89.8 -> 87.3 us; at 2048
-// tokens, 64 or more, all faster: gate/up 295.6 -> 272.6 us, down 292.6 -> 249.1 us).
-constexpr uint32_t kGemmCopyMinUnits = 48;
 int op_embed_rows(gh_backend* b, const gh_buf* x, const gh_buf* w, const void* tokens, uint32_t rows,
                   uint32_t embd);
 int op_embed(gh_backend* b, const gh_buf* x, const gh_buf* w, uint32_t token, uint32_t embd,

@@ -56,11 +56,9 @@ int alloc(gh_model* m, uint64_t bytes, gh_buf* out) {
     return rc;
 }
 
-// Prefill chunks of this many rows or more make and use the FP16 copies. Measured on the 8B
-// shape: 2048-row chunks 43.8 -> 39.5 ms per 2048 tokens with the copies (14B: 82.0 -> 79.6);
-// a 512-row chunk 13.5 -> 13.8 ms (the copies' four-fold weight stream leaves less of the MALL
-// to the activations and partials the other kernels read than the GEMMs save).
-constexpr uint32_t kGemmCopyRows = 1024;
+// Prefill chunks of this many rows or more (those that run the warp-specialized GEMMs) make
+// and use the FP16 copies.
+constexpr uint32_t kGemmCopyRows = 256;
 
 // Register the copies for this prefill call, or withdraw them (shorter chunks dequantize).
 void set_w16(gh_model* m, bool on) {

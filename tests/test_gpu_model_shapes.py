@@ -92,15 +92,16 @@ def test_full_width_prefill_driver_matches_op_by_op(hip, name):
     gm.close()
 
 
-@pytest.mark.parametrize("n", [1024, 2048])
+@pytest.mark.parametrize("n", [300, 2048])
 @pytest.mark.parametrize("name", ["8b", "14b"])
 def test_prefill_fp16_weight_copies_are_bit_identical(hip, name, n):
-    """The FP16 copies of the layer matrices (made before the first prefill with chunks of 1024
-    rows or more) hold the values the dequantizing GEMM producers stage, and the GEMMs run the
-    same MFMAs over them: the prefill leaves the same logits, residual row and K/V cache bits as
-    with GH_MODEL_NO_F16_WEIGHTS. The GEMMs take the copies where each K split streams 48 units
-    or more: at 1024 rows the mixed Q/K/V launch, the 96-row gate/up and the Q6_K down, at 2048
-    rows also the 128-row Q4_K tiles (gate/up, O)."""
+    """The FP16 copies of the layer matrices (made before the first prefill with chunks of 256
+    rows or more) hold the values the dequantizing GEMM producers stage, and the all-waves-MFMA
+    kernels that read them sum in the same k order: the prefill leaves the same logits, residual
+    row and K/V cache bits as with GH_MODEL_NO_F16_WEIGHTS. 300 rows run the mixed Q/K/V launch,
+    O and the Q6_K down with split K (2, 4 and 4 splits), 2048 rows every GEMM unsplit. (The
+    96-row copying tiles of outputs up to 1024 rows run in the tiny shape's prefill, bit for bit
+    against the op-by-op recording.)"""
     from graph_horizon_amd import _ffi as F
 
     shape = dataclasses.replace(synth.SHAPES[name], name=f"{name}-1", block_count=1)
