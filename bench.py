@@ -248,7 +248,7 @@ def main():
         },
         "roofline": roofline,
     }
-    result["config"]["prefill_gemm_c3"] = prefill_gemm(hip, model, shape, 512)
+    result["config"]["prefill_gemm_c3"] = prefill_gemm(hip, model, shape, tensors, 512)
     model.close()
     result["config"]["prefill_2048"] = prefill_long(hip, HipModel, shape, tensors, 2048)
     result["config"]["attention_c4"] = c4_attention(hip)
@@ -437,9 +437,12 @@ def prefill_long(hip, HipModel, shape, tensors, n):
             "fp16_weight_copies": True}
 
 
-def prefill_gemm(hip, model, shape, n):
+def prefill_gemm(hip, model, shape, tensors, n):
     """the n-token prefill GEMMs (gate/up Q4_K d->FFN, down Q6_K FFN->d) on
-    the matrix cores, over 8 distinct layers' weights, timed with HIP events."""
+    the matrix cores, over 8 distinct layers' weights, timed with HIP events. Two forms with the
+    same output bits: the model's own weights, whose FP16 copies its prefill made and its GEMMs
+    read (the prefill's path), and the same weights loaded again without copies, which the
+    GEMMs dequantize tile by tile ("dequantizing")."""
     import ctypes as C
 
     from graph_horizon_amd import _ffi as F
@@ -449,10 +452,11 @@ def prefill_gemm(hip, model, shape, n):
     a_d = hip.from_host(synth_f16(rng, n * d))
     a_f = hip.from_host(synth_f16(rng, n * ffn))
     y = hip.alloc_buffer(n * max(d, ffn) * 2)
-    out = {}
-    for name, tid, ind, outd, a in (("gate_up_q4k", F.T_FFN_GATE, d, ffn, a_d),
-                                    ("down_q6k", F.T_FFN_DOWN, ffn, d, a_f)):
-        ws = [model_weight(model, li, tid) for li in range(min(8, shape.block_count))]
+    layers = min(8, shape.block_count)
+    host = {(layer, tid): (fmt, data) for layer, tid, fmt, data in tensors
+            if layer < layers and tid in (F.T_FFN_GATE, F.T_FFN_DOWN)}
+
+    def timed(name, ws, ind, outd, a):
         enc = hip.begin()
         hip.lib.gh_matmul_batched(hip.h, enc, C.byref(y), C.byref(a), C.byref(ws[0]), ind, outd, n)
         hip.submit()
@@ -465,9 +469,18 @@ def prefill_gemm(hip, model, shape, n):
         ms = hip.timer_stop() / (reps * len(ws))
         hip.submit()
         tflops = 2.0 * n * ind * outd / (ms * 1e-3) / 1e12
-        out[name] = {"shape": f"{n}x{ind}->{outd}", "avg_us": round(ms * 1e3, 2),
-                     "tflops": round(tflops, 1), "frac_f16_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
         log(f"bench: prefill GEMM {name} {n}x{ind}->{outd}: {ms * 1e3:.1f} us, {tflops:.0f} TFLOP/s")
+        return {"shape": f"{n}x{ind}->{outd}", "avg_us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
+                "frac_f16_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+
+    out = {"weights": "the model's, over the FP16 copies its prefill reads", "dequantizing": {}}
+    for name, tid, ind, outd, a in (("gate_up_q4k", F.T_FFN_GATE, d, ffn, a_d),
+                                    ("down_q6k", F.T_FFN_DOWN, ffn, d, a_f)):
+        out[name] = timed(name, [model_weight(model, li, tid) for li in range(layers)], ind, outd, a)
+        ws = [hip.load_weight(*host[(li, tid)], ind, outd) for li in range(layers)]
+        out["dequantizing"][name] = timed(name + " (dequantizing)", ws, ind, outd, a)
+        for w in ws:
+            hip.free_buffer(w)
     for b in (a_d, a_f, y):
         hip.free_buffer(b)
     return out
