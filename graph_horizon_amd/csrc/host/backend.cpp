@@ -53,10 +53,10 @@ const KernelName kKernels[] = {
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
     {K_FILL_U32, "gh_fill_u32"},
-    {K_GEMM3W_Q4K_R96, "gh_gemm3w_q4k_r96"},   {K_GEMM3W_Q6K_R96, "gh_gemm3w_q6k_r96"},
     {K_DEQUANT_F16_Q4K, "gh_dequant_f16_q4k"}, {K_DEQUANT_F16_Q6K, "gh_dequant_f16_q6k"},
     {K_GEMM4W_Q4K_R128, "gh_gemm4w_q4k_r128"}, {K_GEMM4W_Q6K_R128, "gh_gemm4w_q6k_r128"},
     {K_GEMM4W_MIXED_R128, "gh_gemm4w_mixed_r128"},
+    {K_GEMM4W_Q4K_R96, "gh_gemm4w_q4k_r96"},   {K_GEMM4W_Q6K_R96, "gh_gemm4w_q6k_r96"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -934,12 +934,10 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         // a registered FP16 copy of w: the same sums with the weights copied, not dequantized
         const auto copy = b->w16.find(w->addr);
         const uint64_t w16 = copy == b->w16.end() ? 0 : copy->second;
-        // with a copy, the all-waves-MFMA kernel's 128-row tiles (8B prefill at 512 tokens: 12.0
-        // against 12.7 ms with the 96-row copying tiles that fill the CUs' last wave better)
-        const uint32_t br = narrow || (!w16 && fill(96) > fill(128)) ? 96u : 128u;
+        const uint32_t br = narrow || fill(96) > fill(128) ? 96u : 128u;
         GhKernel k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96 : K_GEMM3_Q6K_R96) : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
         if (w16)
-            k = br == 96 ? (q4 ? K_GEMM3W_Q4K_R96 : K_GEMM3W_Q6K_R96) : (q4 ? K_GEMM4W_Q4K_R128 : K_GEMM4W_Q6K_R128);
+            k = br == 96 ? (q4 ? K_GEMM4W_Q4K_R96 : K_GEMM4W_Q6K_R96) : (q4 ? K_GEMM4W_Q4K_R128 : K_GEMM4W_Q6K_R128);
         const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
         const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
         const uint32_t splits = clamp_splits(std::max<uint32_t>(1, slots / tiles));

@@ -75,13 +75,13 @@ enum GhKernel : int {
     K_TOPK_PARTIAL,
     K_TOPK_FINAL,
     K_FILL_U32,
-    K_GEMM3W_Q4K_R96,
-    K_GEMM3W_Q6K_R96,
     K_DEQUANT_F16_Q4K,
     K_DEQUANT_F16_Q6K,
     K_GEMM4W_Q4K_R128,
     K_GEMM4W_Q6K_R128,
     K_GEMM4W_MIXED_R128,
+    K_GEMM4W_Q4K_R96,
+    K_GEMM4W_Q6K_R96,
     K_COUNT
 };
 

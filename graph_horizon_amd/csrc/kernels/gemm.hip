@@ -293,13 +293,7 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
 
 // Tile (bx, by) and split bz of one matrix (a.w, a.rows, a.out); lds3 holds GH_GEMM3_LDS(BR)
 // halves; partials go to columns pc .. of rows ps long.
-// F16W: a.w is the matrix already dequantized (gh_dequant_f16: row r's unit u is the 64 FP16
-// weights store_w would write, at a.w + (r · units + u) · 128 bytes). The producer waves then
-// copy each unit's rows into the stage with LDS DMA, no dequantization: a stage row is 128
-// bytes with chunk c at slot c ^ sw(r), the activations' layout, and the consumers read B
-// fragments as they read A. Same FP16 values, same MFMA order: the same bits as the Q4_K /
-// Q6_K form.
-template <uint32_t FMT, int BR, bool F16W = false>
+template <uint32_t FMT, int BR>
 __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
     constexpr int WT = 64, TI = WT / 32, TJ = BR / 32;
@@ -313,46 +307,6 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
     auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };
 
-    if (F16W && wave >= 4) {
-        // ---- producers, FP16 weights: kD DMA loads of 8 rows x 128 bytes per wave and unit ----
-        // Issued from inline assembly (outside the compiler's wait counting): the wave waits for
-        // them itself. The unit of interval kk goes into stage (kk + 2) % 3, whose previous unit
-        // was read before the barrier that ended interval kk - 1, and must have landed by the
-        // barrier that ends interval kk + 1: each interval waits for all but its own kD loads.
-        constexpr int kD = BR / 32;
-        static_assert(kD == 3 || kD == 4, "F16W producers: 96 or 128 rows");
-        const uint32_t pw = wave - 4;
-        uint64_t src[kD];
-#pragma unroll
-        for (int i = 0; i < kD; ++i) {
-            const uint32_t rr = 8 * (pw * kD + i) + (lane >> 3), c = (lane & 7u) ^ ((rr >> 1) & 7u);
-            src[i] = a.w + ((uint64_t)min(r0 + rr, a.rows - 1) * units) * 128 + c * 16;
-        }
-        auto issue = [&](uint32_t u, uint32_t st) __attribute__((always_inline)) {
-#pragma unroll
-            for (int i = 0; i < kD; ++i) {
-                const uint32_t dst =
-                    (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(wstage(st) + (pw * kD + i) * 512);
-                asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src[i] + (uint64_t)u * 128),
-                             "{m0}"(__builtin_amdgcn_readfirstlane(dst))
-                             : "memory");
-            }
-        };
-        issue(u0, 0);
-        issue(uc(u0 + 1), 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        for (uint32_t kk = 0; kk < u1 - u0; ++kk) {
-            issue(uc(u0 + kk + kS - 1), (kk + kS - 1) % kS);
-            if constexpr (kD == 3)
-                asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-            else
-                asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-            __syncthreads();
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) loads have landed
-        return;
-    }
     if (wave >= 4) {
         // ---- producers ----
         const uint32_t pt = threadIdx.x - 256;
@@ -433,14 +387,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
                 af[i] = *(const h8*)(xb + r * 64 + c * 8);
             }
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                if constexpr (F16W) {
-                    const uint32_t r = 32 * j + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
-                    bf[j] = *(const h8*)(wb + r * 64 + c * 8);
-                } else {
-                    bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
-                }
-            }
+            for (int j = 0; j < TJ; ++j) bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -477,53 +424,51 @@ GH_GEMM3(gh_gemm3_q4k_r128, kQ4K, 128)
 GH_GEMM3(gh_gemm3_q6k_r128, kQ6K, 128)
 GH_GEMM3(gh_gemm3_q4k_r96, kQ4K, 96)
 GH_GEMM3(gh_gemm3_q6k_r96, kQ6K, 96)
-// the same tiles over FP16 weights from gh_dequant_f16 (a.w), copied into LDS by DMA (the
-// host takes these for outputs of up to 1024 rows, gemm4_body's 128-row tiles otherwise)
-#define GH_GEMM3W(NAME, FMT, BR)                                                                   \
-    GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
-        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(BR)];                   \
-        gemm3_body<FMT, BR, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);          \
-    }
-GH_GEMM3W(gh_gemm3w_q4k_r96, kQ4K, 96)
-GH_GEMM3W(gh_gemm3w_q6k_r96, kQ6K, 96)
 
 // Over FP16 weight copies, every wave of the workgroup runs the matrix cores: 512 threads own
-// 256 tokens x 128 rows, wave w the 64 tokens of group w / 2 against rows 64 (w % 2) .. + 64
-// (2 x 2 tiles of v_mfma_f32_32x32x16_f16), two waves per SIMD, so that one wave's LDS reads
-// and waits overlap the other's matrix work. Each unit's activation lines and weight rows go
-// into a 3-stage LDS ring by LDS DMA that every wave shares in (4 activation and 2 weight
-// loads of 1 KiB per wave and unit, from inline assembly; both operands in 128-byte rows with
-// chunk c of row r at slot c ^ (r / 2) % 8). The unit of iteration u goes out two iterations
-// ahead into the stage read during u - 1; each iteration waits for all but its own loads
-// (vmcnt(6)) before the barrier. The k order of every output's sum is the one gemm3_body
+// 256 tokens x BR rows, two waves per SIMD, so that one wave's LDS reads and waits overlap the
+// other's matrix work. BR = 128: wave w takes the 64 tokens of group w / 2 against rows
+// 64 (w % 2) .. + 64 (2 x 2 tiles of v_mfma_f32_32x32x16_f16); BR = 96: the 32 tokens of
+// group w against all 96 rows (1 x 3 tiles), which makes 256 workgroups of a 12288-row output
+// at 512 tokens instead of 192. Each unit's activation lines and weight rows go into a
+// 3-stage LDS ring by LDS DMA that every wave shares in (activation rows 32 w .. + 32 and
+// weight row blocks w, w + 8 of 8 rows, 1 KiB loads from inline assembly; both operands in
+// 128-byte rows with chunk c of row r at slot c ^ (r / 2) % 8). The unit of iteration u goes
+// out two iterations ahead into the stage read during u - 1; each iteration waits for all but
+// its own loads before the barrier. The k order of every output's sum is the one gemm3_body
 // uses: the same bits.
-#define GH_GEMM4_LDS (3 * (256 + 128) * 64)
-template <uint32_t FMT>
+#define GH_GEMM4_LDS(BR) (3 * (256 + (BR)) * 64)
+template <uint32_t FMT, int BR>
 __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
-    constexpr uint32_t kStage = (256 + 128) * 64;  // halves: A (256 token rows), then B (128 rows)
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, g = wave >> 1, hr = wave & 1u;
-    const uint32_t r0 = bx * 128;
+    static_assert(BR == 128 || BR == 96, "all-waves-MFMA tiles: 128 or 96 rows");
+    constexpr uint32_t WTOK = BR == 128 ? 64 : 32, WROW = BR == 128 ? 64 : 96;
+    constexpr uint32_t NR = BR / WROW, TI = WTOK / 32, TJ = WROW / 32, NB = BR / 8;
+    constexpr uint32_t kStage = (256 + BR) * 64;  // halves: A (256 token rows), then B (BR rows)
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, g = wave / NR, hr = wave % NR;
+    const uint32_t r0 = bx * BR;
     const uint32_t units = a.in_dim / 64;
     const uint32_t per = (units + a.splits - 1) / a.splits;
     const uint32_t u0 = bz * per, u1 = min(units, u0 + per);
     if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
     auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };
     const uint32_t fm = lane & 31u, fg = lane >> 5;
-    // this wave's loads: activation rows 64 g + 32 hr + 8 i + lane / 8 (i < 4), weight rows
-    // 16 w + 8 i + lane / 8 (i < 2); lane l fetches chunk (l % 8) ^ sw(row) of its row
+    // this wave's loads: activation rows 32 w + 8 i + lane / 8 (i < 4), weight rows
+    // 8 d + lane / 8 of blocks d = w, w + 8 (< NB); lane l fetches chunk (l % 8) ^ sw(row)
     const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
-    uint64_t xa[4], wa[2];
+    constexpr uint32_t kB = (NB + 7) / 8;  // weight blocks of wave 0 (waves >= NB - 8 have one fewer)
+    const bool two = NB >= 16 || wave + 8 < NB;  // compile-time true for 128 rows
+    uint64_t xa[4], wa[kB];
     uint32_t xc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t r = 64 * g + 32 * hr + 8 * i + (lane >> 3);
+        const uint32_t r = 32 * wave + 8 * i + (lane >> 3);
         xc[i] = (lane & 7u) ^ ((r >> 1) & 7u);
         xa[i] = (uint64_t)(uintptr_t)(x + (uint64_t)min(by * 256 + r, a.n - 1) * a.in_dim);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t r = 16 * wave + 8 * i + (lane >> 3), c = (lane & 7u) ^ ((r >> 1) & 7u);
+    for (uint32_t i = 0; i < kB; ++i) {
+        const uint32_t r = 8 * (wave + 8 * i) + (lane >> 3), c = (lane & 7u) ^ ((r >> 1) & 7u);
         wa[i] = a.w + ((uint64_t)min(r0 + r, a.rows - 1) * units) * 128 + c * 16;
     }
     auto stage = [&](uint32_t st) __attribute__((always_inline)) { return lds + st * kStage; };
@@ -531,26 +476,27 @@ __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, u
         _Float16* sa = stage(st);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(
-                sa + (64 * g + 32 * hr + 8 * i) * 64);
+            const uint32_t dst =
+                (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(sa + (32 * wave + 8 * i) * 64);
             asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(xa[i] + 2ull * chunk_k<FMT>(u, xc[i])),
                          "{m0}"(__builtin_amdgcn_readfirstlane(dst))
                          : "memory");
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (uint32_t i = 0; i < kB; ++i) {
+            if (i == 1 && !two) break;  // wave-uniform
             const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(
-                sa + (256 + 16 * wave + 8 * i) * 64);
+                sa + (256 + 8 * (wave + 8 * i)) * 64);
             asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(wa[i] + (uint64_t)u * 128),
                          "{m0}"(__builtin_amdgcn_readfirstlane(dst))
                          : "memory");
         }
     };
-    f16v acc[2][2];
+    f16v acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (uint32_t i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f16v{};
+        for (uint32_t j = 0; j < TJ; ++j) acc[i][j] = f16v{};
     issue(u0, 0);
     issue(uc(u0 + 1), 1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -558,41 +504,50 @@ __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, u
     for (uint32_t u = u0; u < u1; ++u) {
         const uint32_t k = u - u0;
         issue(uc(u + 2), (k + 2) % 3);
-        const _Float16* xb = stage(k % 3) + (64 * g) * 64;
-        const _Float16* wb = stage(k % 3) + (256 + 64 * hr) * 64;
+        const _Float16* xb = stage(k % 3) + (WTOK * g) * 64;
+        const _Float16* wb = stage(k % 3) + 256 * 64;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            h8 af[2], bf[2];
+            h8 af[TI], bf[TJ];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (uint32_t i = 0; i < TI; ++i) {
                 const uint32_t r = 32 * i + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
                 af[i] = *(const h8*)(xb + r * 64 + c * 8);
-                const uint32_t rw = 64 * hr + 32 * i + fm, cw = (2 * ks + fg) ^ ((rw >> 1) & 7u);
-                bf[i] = *(const h8*)(wb - (64 * hr) * 64 + rw * 64 + cw * 8);
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (uint32_t j = 0; j < TJ; ++j) {
+                const uint32_t r = WROW * hr + 32 * j + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
+                bf[j] = *(const h8*)(wb + r * 64 + c * 8);
+            }
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+            for (uint32_t i = 0; i < TI; ++i)
+#pragma unroll
+                for (uint32_t j = 0; j < TJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // unit u + 1 has landed
+        // unit u + 1 has landed: all but this iteration's own loads (4 + 1 or 2)
+        if (kB == 1 || two)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + kB) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + kB - 1) : "memory");
         __syncthreads();
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) loads have landed
-    gemm_write<2, 2, true>(a, acc, by * 256 + 64 * g, r0 + 64 * hr, fm, fg, bz, ps, pc);
+    gemm_write<TI, TJ, true>(a, acc, by * 256 + WTOK * g, r0 + WROW * hr, fm, fg, bz, ps, pc);
 }
-#define GH_GEMM4W(NAME, FMT)                                                                       \
+#define GH_GEMM4W(NAME, FMT, BR)                                                                   \
     GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
-        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM4_LDS];                       \
-        gemm4_body<FMT>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);                    \
+        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM4_LDS(BR)];                   \
+        gemm4_body<FMT, BR>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);                \
     }
-GH_GEMM4W(gh_gemm4w_q4k_r128, kQ4K)
-GH_GEMM4W(gh_gemm4w_q6k_r128, kQ6K)
+GH_GEMM4W(gh_gemm4w_q4k_r128, kQ4K, 128)
+GH_GEMM4W(gh_gemm4w_q6k_r128, kQ6K, 128)
+GH_GEMM4W(gh_gemm4w_q4k_r96, kQ4K, 96)
+GH_GEMM4W(gh_gemm4w_q6k_r96, kQ6K, 96)
 
-// A Q4_K / Q6_K matrix [rows][in_dim] dequantized to FP16 in the GEMM's unit order (the layout
-// gemm3_body<F16W> reads): thread t handles half p = t % 2 of unit u of row r, t / 2 = r · units
-// + u, with load_w and store_w (one row per "tile"), so each value is the one the dequantizing
+// A Q4_K / Q6_K matrix [rows][in_dim] dequantized to FP16 in the GEMM's unit order, the layout
+// gemm4_body reads: thread t handles half p = t % 2 of unit u of row r, t / 2 = r · units + u,
+// with load_w and store_w (one row per "tile"), so each value is the one the dequantizing
 // producers stage. a.w: device layout, a.out: FP16 [rows][units][64].
 template <uint32_t FMT>
 __device__ __forceinline__ void dequant_f16(const GhGemmArgs& a) {
@@ -629,7 +584,7 @@ GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128(GhGemmArgs a) {
 
 // The multi-matrix launch over FP16 weights with every wave on the matrix cores (gemm4_body).
 GH_KERNEL __launch_bounds__(512) void gh_gemm4w_mixed_r128(GhGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM4_LDS];
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM4_LDS(128)];
     uint32_t s = 0;
     for (uint32_t i = 1; i < a.nseg; ++i)
         if (blockIdx.x >= a.seg[i].tile0) s = i;
@@ -639,9 +594,9 @@ GH_KERNEL __launch_bounds__(512) void gh_gemm4w_mixed_r128(GhGemmArgs a) {
     m.out = a.seg[s].out;
     const uint32_t bx = blockIdx.x - a.seg[s].tile0;
     if (a.seg[s].fmt == kQ4K)
-        gemm4_body<kQ4K>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+        gemm4_body<kQ4K, 128>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
     else
-        gemm4_body<kQ6K>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+        gemm4_body<kQ6K, 128>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
 }
 
 // Sum split-K partials in split order, round to FP16: out[i] = f16(Σ_s part[s][i]).

@@ -98,10 +98,9 @@ def test_prefill_fp16_weight_copies_are_bit_identical(hip, name, n):
     """The FP16 copies of the layer matrices (made before the first prefill with chunks of 256
     rows or more) hold the values the dequantizing GEMM producers stage, and the all-waves-MFMA
     kernels that read them sum in the same k order: the prefill leaves the same logits, residual
-    row and K/V cache bits as with GH_MODEL_NO_F16_WEIGHTS. 300 rows run the mixed Q/K/V launch,
-    O and the Q6_K down with split K (2, 4 and 4 splits), 2048 rows every GEMM unsplit. (The
-    96-row copying tiles of outputs up to 1024 rows run in the tiny shape's prefill, bit for bit
-    against the op-by-op recording.)"""
+    row and K/V cache bits as with GH_MODEL_NO_F16_WEIGHTS. 300 rows run gate/up in 96-row
+    tiles and the mixed Q/K/V launch, O and the Q6_K down in 128-row tiles with split K (2, 4
+    and 4 splits); 2048 rows run every GEMM in 128-row tiles, unsplit."""
     from graph_horizon_amd import _ffi as F
 
     shape = dataclasses.replace(synth.SHAPES[name], name=f"{name}-1", block_count=1)
