@@ -690,72 +690,78 @@ GH_KERNEL __launch_bounds__(256) void gh_gemm_tail(GhGemmArgs a) {
     const uint64_t total = (uint64_t)a.n * d, row0 = (uint64_t)t * d;
     GH_GLOBAL float4* x = gh_gpw<float4>(a.aux) + row0 / 4;
     __shared__ float red[4];
-    float4 v[2][4];
-    float ss = 0.0f;
-    // every load of a group of four splits is requested before any is summed (clamped chunk
-    // and split indices: no branch around the loads)
-    float4 s[2][4], xv[2][4];
+    __shared__ float4 ys[2048];  // the updated residual row (rows <= 8192)
+    // Pass 1, coalesced: thread t takes the float4s t + 256 j (a wave's loads cover whole
+    // lines), 1024 per round. Every load of a round and a group of four splits is requested
+    // before any is summed (clamped indices, no branch around the loads); the splits are summed
+    // in order, the sum rounded to FP16, added into the residual, and the new row kept in LDS.
+    for (uint32_t j0 = 0; j0 < n4; j0 += 1024) {  // launch-uniform: one round up to 4096 rows
+        float4 s[4], xv[4];
 #pragma unroll
-    for (uint32_t it = 0; it < 2; ++it)
-#pragma unroll
-        for (uint32_t q = 0; q < 4; ++q) {
-            s[it][q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            xv[it][q] = x[min(4 * (threadIdx.x + 256 * it) + q, n4 - 1)];
+        for (uint32_t j = 0; j < 4; ++j) {
+            s[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            xv[j] = x[min(j0 + threadIdx.x + 256 * j, n4 - 1)];
         }
-    if (a.splits > 1) {
-        for (uint32_t k0 = 0; k0 < a.splits; k0 += 4) {
-            float4 p[4][2][4];
+        if (a.splits > 1) {
+            for (uint32_t k0 = 0; k0 < a.splits; k0 += 4) {
+                float4 p[4][4];
 #pragma unroll
-            for (uint32_t kk = 0; kk < 4; ++kk)
+                for (uint32_t kk = 0; kk < 4; ++kk)
 #pragma unroll
-                for (uint32_t it = 0; it < 2; ++it)
-#pragma unroll
-                    for (uint32_t q = 0; q < 4; ++q) {
-                        const uint32_t k = min(k0 + kk, a.splits - 1), c = min(4 * (threadIdx.x + 256 * it) + q, n4 - 1);
-                        p[kk][it][q] = gh_gp<float4>(a.part)[(k * total + row0) / 4 + c];
+                    for (uint32_t j = 0; j < 4; ++j) {
+                        const uint32_t k = min(k0 + kk, a.splits - 1), c = min(j0 + threadIdx.x + 256 * j, n4 - 1);
+                        p[kk][j] = gh_gp<float4>(a.part)[(k * total + row0) / 4 + c];
                     }
 #pragma unroll
-            for (uint32_t kk = 0; kk < 4; ++kk)
-                if (k0 + kk < a.splits)
+                for (uint32_t kk = 0; kk < 4; ++kk)
+                    if (k0 + kk < a.splits)
 #pragma unroll
-                    for (uint32_t it = 0; it < 2; ++it)
-#pragma unroll
-                        for (uint32_t q = 0; q < 4; ++q) {
-                            s[it][q].x += p[kk][it][q].x;
-                            s[it][q].y += p[kk][it][q].y;
-                            s[it][q].z += p[kk][it][q].z;
-                            s[it][q].w += p[kk][it][q].w;
+                        for (uint32_t j = 0; j < 4; ++j) {
+                            s[j].x += p[kk][j].x;
+                            s[j].y += p[kk][j].y;
+                            s[j].z += p[kk][j].z;
+                            s[j].w += p[kk][j].w;
                         }
-        }
-    } else {
-#pragma unroll
-        for (uint32_t it = 0; it < 2; ++it)
-#pragma unroll
-            for (uint32_t q = 0; q < 4; ++q) {
-                const uint2 o = gh_gp<uint2>(a.out)[row0 / 4 + min(4 * (threadIdx.x + 256 * it) + q, n4 - 1)];
-                s[it][q] = make_float4(gh_h2f(o.x & 0xFFFFu), gh_h2f(o.x >> 16), gh_h2f(o.y & 0xFFFFu), gh_h2f(o.y >> 16));
             }
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                const uint2 o = gh_gp<uint2>(a.out)[row0 / 4 + min(j0 + threadIdx.x + 256 * j, n4 - 1)];
+                s[j] = make_float4(gh_h2f(o.x & 0xFFFFu), gh_h2f(o.x >> 16), gh_h2f(o.y & 0xFFFFu), gh_h2f(o.y >> 16));
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t c = j0 + threadIdx.x + 256 * j;
+            if (c >= n4) continue;
+            // one split: s already holds the FP16 output; several: round their sum to FP16
+            const float4 h = a.splits > 1 ? make_float4(gh_h2f(gh_f2h(s[j].x)), gh_h2f(gh_f2h(s[j].y)),
+                                                        gh_h2f(gh_f2h(s[j].z)), gh_h2f(gh_f2h(s[j].w)))
+                                          : s[j];
+            float4 y = xv[j];
+            y.x = y.x + h.x;
+            y.y = y.y + h.y;
+            y.z = y.z + h.z;
+            y.w = y.w + h.w;
+            x[c] = y;
+            ys[c] = y;
+        }
     }
+    if (!a.norm) return;  // launch-uniform
+    __syncthreads();
+    // Pass 2: thread t takes the 16-value items t, t + 256 of the row back from LDS, in
+    // gh_rms_inverse_256's order, for the sum of squares and the normalized FP16 values.
+    float4 v[2][4];
+    float ss = 0.0f;
 #pragma unroll
     for (uint32_t it = 0; it < 2; ++it)
 #pragma unroll
         for (uint32_t q = 0; q < 4; ++q) {
             const uint32_t c = 4 * (threadIdx.x + 256 * it) + q;
             if (c >= n4) continue;
-            // one split: s already holds the FP16 output; several: round their sum to FP16
-            const float4 h = a.splits > 1 ? make_float4(gh_h2f(gh_f2h(s[it][q].x)), gh_h2f(gh_f2h(s[it][q].y)),
-                                                        gh_h2f(gh_f2h(s[it][q].z)), gh_h2f(gh_f2h(s[it][q].w)))
-                                          : s[it][q];
-            float4 y = xv[it][q];
-            y.x = y.x + h.x;
-            y.y = y.y + h.y;
-            y.z = y.z + h.z;
-            y.w = y.w + h.w;
-            x[c] = y;
-            v[it][q] = y;
-            ss = gh_rms_add(ss, y);
+            v[it][q] = ys[c];
+            ss = gh_rms_add(ss, v[it][q]);
         }
-    if (!a.norm) return;  // launch-uniform
     const float inverse = gh_rms_finish_256(ss, d, a.eps, red);
     const GH_GLOBAL uint2* w = gh_gp<uint2>(a.norm);
     GH_GLOBAL uint2* out = gh_gpw<uint2>(a.normed) + row0 / 4;
