@@ -120,3 +120,41 @@ def test_prefill_fp16_weight_copies_are_bit_identical(hip, name, n):
         gm.close()
     for got, want, what in zip(outs[0], outs[1], ("logits", "x", "k", "v")):
         assert np.array_equal(got, want), what
+
+
+def test_prefill_fp16_weight_copies_follow_reloaded_weights(hip):
+    """The FP16 copies are a cache of the layer matrices: reloading a matrix after a prefill
+    made them (gh_model_load_tensor) drops every copy, and the next prefill dequantizes the new
+    weights again. A model that prefilled with one set of weights, then had block 0's Q, gate
+    and down matrices replaced, prefills the same prompt bit for bit like a fresh model built
+    with the new weights."""
+    from graph_horizon_amd import _ffi as F
+
+    shape = synth.SHAPES["small"]
+    ctx, n = 320, 300
+    old = list(synth.model_tensors(shape, 23))
+    new = list(synth.model_tensors(shape, 24))
+    swap = {(0, F.T_ATTN_Q), (0, F.T_FFN_GATE), (0, F.T_FFN_DOWN)}
+    mixed = [nt if (nt[0], nt[1]) in swap else ot for ot, nt in zip(old, new)]
+    toks = [int(t) for t in np.random.default_rng(5).integers(0, shape.vocab_size, n)]
+
+    gm = HipModel(hip, synth.model_config(shape, ctx, prefill_rows=512))
+    for layer, tid, fmt, data in old:
+        gm.load_tensor(layer, tid, fmt, data)
+    gm.prefill(toks, 0)
+    before = gm.read_logits().view(np.uint32).copy()
+    for layer, tid, fmt, data in mixed:
+        if (layer, tid) in swap:
+            gm.load_tensor(layer, tid, fmt, data)
+    gm.prefill(toks, 0)
+    got = (gm.read_logits().view(np.uint32).copy(), gm.read_x().view(np.uint32).copy())
+    gm.close()
+
+    ref = HipModel(hip, synth.model_config(shape, ctx, prefill_rows=512))
+    for layer, tid, fmt, data in mixed:
+        ref.load_tensor(layer, tid, fmt, data)
+    ref.prefill(toks, 0)
+    want = (ref.read_logits().view(np.uint32), ref.read_x().view(np.uint32))
+    ref.close()
+    assert not np.array_equal(before, want[0])  # the swap changes the result
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
