@@ -57,6 +57,8 @@ const KernelName kKernels[] = {
     {K_GEMM4W_Q4K_R128, "gh_gemm4w_q4k_r128"}, {K_GEMM4W_Q6K_R128, "gh_gemm4w_q6k_r128"},
     {K_GEMM4W_MIXED_R128, "gh_gemm4w_mixed_r128"},
     {K_GEMM4W_Q4K_R96, "gh_gemm4w_q4k_r96"},   {K_GEMM4W_Q6K_R96, "gh_gemm4w_q6k_r96"},
+    {K_GEMM3_Q4K_R128_T128, "gh_gemm3_q4k_r128_t128"}, {K_GEMM3_Q6K_R128_T128, "gh_gemm3_q6k_r128_t128"},
+    {K_GEMM3_Q4K_R96_T128, "gh_gemm3_q4k_r96_t128"},   {K_GEMM3_Q6K_R96_T128, "gh_gemm3_q6k_r96_t128"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -847,6 +849,9 @@ namespace gh {
 // batches take the 256-thread tiles of 128 tokens x 64 rows (outputs below 4096 rows) or
 // x 128 rows. Either splits K over the units when the tiles alone would leave CUs idle.
 constexpr uint32_t kGemmMinTokens = 8;
+// From this many tokens the warp-specialized kernels run (128-token tiles below 256 tokens);
+// fewer take gemm_body's 128-token tiles.
+constexpr uint32_t kGemmShortMinTokens = 8;
 constexpr uint32_t kGemmTailMaxRows = 8192;  // gh_gemm_tail: two 16-value items per thread
 
 struct GemmTile {
@@ -918,13 +923,16 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         return std::max<uint32_t>(1, std::min<uint32_t>({s, std::max<uint32_t>(1, units / 8), 16u}));
     };
     const bool q4 = w->format == GH_FMT_Q4_K;
-    if (n >= 256) {
+    if (n >= kGemmShortMinTokens) {
         // Row height (measured at 512 tokens on the 8B and 14B shapes): one workgroup per CU,
         // s = CUs / tiles splits, and the height whose tiles x splits fill the CUs' last wave
         // better — 96 rows for 12288 x 4096 (256 tiles against 192 of 128 rows), 128 rows
         // otherwise. Narrow outputs (<= 1024 rows) take 96 rows with two workgroups per CU
         // and up to 16 splits: their few units per split leave latency for a second to hide.
-        const uint32_t tt = ceil_div(n, 256u), cus = b->cus;
+        // Batches of fewer than 256 tokens take 128-token tiles (no FP16 copies: at these
+        // sizes their four-fold weight stream is the floor).
+        const bool tall = n >= 256;
+        const uint32_t tt = ceil_div(n, tall ? 256u : 128u), cus = b->cus;
         auto fill = [&](uint32_t br) {
             const uint32_t t = ceil_div(rows, br) * tt, s = std::max<uint32_t>(1, cus / t);
             const uint64_t ts = (uint64_t)t * s;
@@ -933,9 +941,12 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         const bool narrow = rows <= 1024;
         // a registered FP16 copy of w: the same sums with the weights copied, not dequantized
         const auto copy = b->w16.find(w->addr);
-        const uint64_t w16 = copy == b->w16.end() ? 0 : copy->second;
+        const uint64_t w16 = copy == b->w16.end() || !tall ? 0 : copy->second;
         const uint32_t br = narrow || fill(96) > fill(128) ? 96u : 128u;
         GhKernel k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96 : K_GEMM3_Q6K_R96) : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
+        if (!tall)
+            k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96_T128 : K_GEMM3_Q6K_R96_T128)
+                         : (q4 ? K_GEMM3_Q4K_R128_T128 : K_GEMM3_Q6K_R128_T128);
         if (w16)
             k = br == 96 ? (q4 ? K_GEMM4W_Q4K_R96 : K_GEMM4W_Q6K_R96) : (q4 ? K_GEMM4W_Q4K_R128 : K_GEMM4W_Q6K_R128);
         const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
@@ -950,10 +961,10 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
                        out, a, w, n, e);
 }
 
-// The SiLU epilogue is compiled into the warp-specialized kernels (n >= 256) only; the tail
-// runs after any GEMM (n >= kGemmMinTokens).
+// The SiLU epilogue is compiled into the warp-specialized kernels (n >= kGemmShortMinTokens)
+// only; the tail runs after any GEMM (n >= kGemmMinTokens).
 bool gemm_epi_applies(uint32_t n, uint32_t out_dim, bool tail) {
-    return tail ? n >= kGemmMinTokens && out_dim % 4 == 0 && out_dim <= kGemmTailMaxRows : n >= 256;
+    return tail ? n >= kGemmMinTokens && out_dim % 4 == 0 && out_dim <= kGemmTailMaxRows : n >= kGemmShortMinTokens;
 }
 
 int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,

@@ -82,6 +82,10 @@ enum GhKernel : int {
     K_GEMM4W_MIXED_R128,
     K_GEMM4W_Q4K_R96,
     K_GEMM4W_Q6K_R96,
+    K_GEMM3_Q4K_R128_T128,
+    K_GEMM3_Q6K_R128_T128,
+    K_GEMM3_Q4K_R96_T128,
+    K_GEMM3_Q6K_R96_T128,
     K_COUNT
 };
 

@@ -281,22 +281,26 @@ __device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
     gemm_write<TI, TJ, false>(a, acc, t0, r0, fm, fg, blockIdx.z, a.rows, 0);
 }
 
-// Warp-specialized variant for long batches: a 512-thread workgroup owns 256 tokens x BR rows.
-// Waves 0-3 (consumers) run the matrix cores exactly as gemm_body's waves do (64 tokens each,
-// A from registers one unit ahead, B from LDS). Waves 4-7 (producers) stream the weight bytes
+// Warp-specialized variant for long batches: a 512-thread workgroup owns 4·WT tokens x BR rows
+// (WT = 64: 256 tokens; WT = 32: 128 tokens, for chunks of fewer than 256 rows, where split K
+// has to spread the units over many workgroups: the producers' kL units in flight keep those
+// short ranges streaming where gemm_body's one unit of lookahead leaves them waiting on
+// memory). Waves 0-3 (consumers) run the matrix cores (WT tokens each, B from LDS). Waves 4-7 (producers) stream the weight bytes
 // kL units ahead of use — kL register sets, selected statically by unrolling the loop kL-fold —
 // and dequantize each unit into a kS-stage LDS ring, kS - 1 units ahead of the consumers. One
 // barrier per unit: in the interval of unit u the consumers read stage (u - u0) % kS while the
 // producers fill unit u + kS - 1 into the stage read during unit u - 1.
 // LDS of gemm3_body: kS = 3 weight stages, then each consumer wave's two activation buffers.
 #define GH_GEMM3_LDS(BR) (3 * (BR) * LDK + 4 * 2 * 64 * 64)
+#define GH_GEMM3_LDS_T(BR, WT) (3 * (BR) * LDK + 4 * 2 * (WT) * 64)
 
 // Tile (bx, by) and split bz of one matrix (a.w, a.rows, a.out); lds3 holds GH_GEMM3_LDS(BR)
 // halves; partials go to columns pc .. of rows ps long.
-template <uint32_t FMT, int BR>
+template <uint32_t FMT, int BR, int WT = 64>
 __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
-    constexpr int WT = 64, TI = WT / 32, TJ = BR / 32;
+    static_assert(WT == 64 || WT == 32, "consumer waves of 64 or 32 tokens");
+    constexpr int TI = WT / 32, TJ = BR / 32, NX = WT / 8;  // NX: activation line loads per unit
     constexpr int kS = 3, kL = 4;
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -346,9 +350,9 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     const uint32_t t0 = by * (4 * WT) + wave * WT;
     const uint32_t fm = lane & 31u, fg = lane >> 5;
     const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
-    uint32_t xrow[8];
+    uint32_t xrow[NX];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xrow[i] = min(t0 + 8 * i + (lane >> 3), a.n - 1) * a.in_dim;
+    for (int i = 0; i < NX; ++i) xrow[i] = min(t0 + 8 * i + (lane >> 3), a.n - 1) * a.in_dim;
     // Activations go straight to LDS (global_load_lds_dwordx4: lane l of a load lands at byte
     // 16 l of its 1 KiB destination). Load i covers rows 8 i .. 8 i + 7 of the wave's 64; lane
     // l fetches chunk (l % 8) ^ sw(r) of row r = 8 i + l / 8, so chunk c of row r sits at slot
@@ -359,7 +363,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     _Float16* xw = lds3 + kS * BR * LDK + wave * (2 * WT * 64);
     auto load_rows = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NX; ++i) {
             const uint32_t r = 8 * i + (lane >> 3), c = (lane & 7u) ^ ((r >> 1) & 7u);
             __builtin_amdgcn_global_load_lds((const GH_GLOBAL void*)(x + xrow[i] + chunk_k<FMT>(u, c)),
                                              (__attribute__((address_space(3))) void*)(xw + b * (WT * 64) + i * 512),
@@ -424,6 +428,16 @@ GH_GEMM3(gh_gemm3_q4k_r128, kQ4K, 128)
 GH_GEMM3(gh_gemm3_q6k_r128, kQ6K, 128)
 GH_GEMM3(gh_gemm3_q4k_r96, kQ4K, 96)
 GH_GEMM3(gh_gemm3_q6k_r96, kQ6K, 96)
+// 128-token tiles (consumer waves of 32 tokens)
+#define GH_GEMM3T(NAME, FMT, BR)                                                                   \
+    GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
+        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_T(BR, 32)];             \
+        gemm3_body<FMT, BR, 32>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);            \
+    }
+GH_GEMM3T(gh_gemm3_q4k_r128_t128, kQ4K, 128)
+GH_GEMM3T(gh_gemm3_q6k_r128_t128, kQ6K, 128)
+GH_GEMM3T(gh_gemm3_q4k_r96_t128, kQ4K, 96)
+GH_GEMM3T(gh_gemm3_q6k_r96_t128, kQ6K, 96)
 
 // Over FP16 weight copies, every wave of the workgroup runs the matrix cores: 512 threads own
 // 256 tokens x BR rows, two waves per SIMD, so that one wave's LDS reads and waits overlap the
