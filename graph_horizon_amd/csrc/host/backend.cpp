@@ -43,8 +43,6 @@ const KernelName kKernels[] = {
     {K_ATTN_G2, "gh_attn_g2"},             {K_ATTN_MFMA_G4, "gh_attn_mfma_g4"},
     {K_ATTN_MFMA_G8, "gh_attn_mfma_g8"},
 
-    {K_GEMM_Q4K_T128_R64, "gh_gemm_q4k_t128_r64"},   {K_GEMM_Q4K_T128_R128, "gh_gemm_q4k_t128_r128"},
-    {K_GEMM_Q6K_T128_R64, "gh_gemm_q6k_t128_r64"},   {K_GEMM_Q6K_T128_R128, "gh_gemm_q6k_t128_r128"},
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},
     {K_GEMM_REDUCE_ROPE, "gh_gemm_reduce_rope"}, {K_GEMM3_MIXED_R128, "gh_gemm3_mixed_r128"},
     {K_GEMM_REDUCE_SEG, "gh_gemm_reduce_seg"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
@@ -844,20 +842,11 @@ int gh_embed(gh_backend* b, gh_encoder* enc, const gh_buf* x, const gh_buf* w, u
 
 namespace gh {
 
-// Matrix-core GEMM for n >= kGemmMinTokens. Batches of 256 tokens or more take the
-// warp-specialized kernels (256 tokens x 128 or 96 rows per 512-thread workgroup); shorter
-// batches take the 256-thread tiles of 128 tokens x 64 rows (outputs below 4096 rows) or
-// x 128 rows. Either splits K over the units when the tiles alone would leave CUs idle.
+// Matrix-core GEMM for n >= kGemmMinTokens: the warp-specialized kernels (512-thread
+// workgroups of 256 tokens, or 128 below 256 tokens, x 128 or 96 rows), over FP16 weight
+// copies where registered; K splits over the units when the tiles alone would leave CUs idle.
 constexpr uint32_t kGemmMinTokens = 8;
-// From this many tokens the warp-specialized kernels run (128-token tiles below 256 tokens);
-// fewer take gemm_body's 128-token tiles.
-constexpr uint32_t kGemmShortMinTokens = 8;
 constexpr uint32_t kGemmTailMaxRows = 8192;  // gh_gemm_tail: two 16-value items per thread
-
-struct GemmTile {
-    uint32_t tokens, rows, index;
-};
-constexpr GemmTile kGemmTiles[2] = {{128, 64, 0}, {128, 128, 1}};
 
 // One GEMM launch over tr x tt tiles and `splits` K ranges; with splits > 1 the kernel writes
 // FP32 partials to the workspace and gh_gemm_reduce sums them in split order. `e` adds the
@@ -875,7 +864,14 @@ static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, u
         if (s == splits) break;
         splits = s;
     }
-    GhGemmArgs ga{a->addr, w16 ? w16 : w->addr, out, 0, w->cols, w->rows, n, splits};
+    GhGemmArgs ga{};
+    ga.x = a->addr;
+    ga.w = w16 ? w16 : w->addr;
+    ga.out = out;
+    ga.in_dim = w->cols;
+    ga.rows = w->rows;
+    ga.n = n;
+    ga.splits = splits;
     const bool tail = e && e->resid;
     if (e && !tail) {
         ga.epi = e->epi;
@@ -923,48 +919,40 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         return std::max<uint32_t>(1, std::min<uint32_t>({s, std::max<uint32_t>(1, units / 8), 16u}));
     };
     const bool q4 = w->format == GH_FMT_Q4_K;
-    if (n >= kGemmShortMinTokens) {
-        // Row height (measured at 512 tokens on the 8B and 14B shapes): one workgroup per CU,
-        // s = CUs / tiles splits, and the height whose tiles x splits fill the CUs' last wave
-        // better — 96 rows for 12288 x 4096 (256 tiles against 192 of 128 rows), 128 rows
-        // otherwise. Narrow outputs (<= 1024 rows) take 96 rows with two workgroups per CU
-        // and up to 16 splits: their few units per split leave latency for a second to hide.
-        // Batches of fewer than 256 tokens take 128-token tiles (no FP16 copies: at these
-        // sizes their four-fold weight stream is the floor).
-        const bool tall = n >= 256;
-        const uint32_t tt = ceil_div(n, tall ? 256u : 128u), cus = b->cus;
-        auto fill = [&](uint32_t br) {
-            const uint32_t t = ceil_div(rows, br) * tt, s = std::max<uint32_t>(1, cus / t);
-            const uint64_t ts = (uint64_t)t * s;
-            return (double)ts / ((double)cus * (double)ceil_div(ts, cus));
-        };
-        const bool narrow = rows <= 1024;
-        // a registered FP16 copy of w: the same sums with the weights copied, not dequantized
-        const auto copy = b->w16.find(w->addr);
-        const uint64_t w16 = copy == b->w16.end() || !tall ? 0 : copy->second;
-        const uint32_t br = narrow || fill(96) > fill(128) ? 96u : 128u;
-        GhKernel k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96 : K_GEMM3_Q6K_R96) : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
-        if (!tall)
-            k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96_T128 : K_GEMM3_Q6K_R96_T128)
-                         : (q4 ? K_GEMM3_Q4K_R128_T128 : K_GEMM3_Q6K_R128_T128);
-        if (w16)
-            k = br == 96 ? (q4 ? K_GEMM4W_Q4K_R96 : K_GEMM4W_Q6K_R96) : (q4 ? K_GEMM4W_Q4K_R128 : K_GEMM4W_Q6K_R128);
-        const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
-        const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
-        const uint32_t splits = clamp_splits(std::max<uint32_t>(1, slots / tiles));
-        return gemm_launch(b, k, 512, tr, tt, splits, out, a, w, n, e, w16);
-    }
-    const GemmTile tile = rows >= 4096 ? kGemmTiles[1] : kGemmTiles[0];
-    const GhKernel k = (GhKernel)((q4 ? K_GEMM_Q4K_T128_R64 : K_GEMM_Q6K_T128_R64) + tile.index);
-    const uint32_t tr = ceil_div(rows, tile.rows), tt = ceil_div(n, tile.tokens), tiles = tr * tt;
-    return gemm_launch(b, k, 256, tr, tt, clamp_splits(std::max<uint32_t>(1, resident_wgs(b, k, 256, 0) / tiles)),
-                       out, a, w, n, e);
+    // Row height (measured at 512 tokens on the 8B and 14B shapes): one workgroup per CU,
+    // s = CUs / tiles splits, and the height whose tiles x splits fill the CUs' last wave
+    // better — 96 rows for 12288 x 4096 (256 tiles against 192 of 128 rows), 128 rows
+    // otherwise. Narrow outputs (<= 1024 rows) take 96 rows with two workgroups per CU
+    // and up to 16 splits: their few units per split leave latency for a second to hide.
+    // Batches of fewer than 256 tokens take 128-token tiles (no FP16 copies: at these
+    // sizes their four-fold weight stream is the floor).
+    const bool tall = n >= 256;
+    const uint32_t tt = ceil_div(n, tall ? 256u : 128u), cus = b->cus;
+    auto fill = [&](uint32_t br) {
+        const uint32_t t = ceil_div(rows, br) * tt, s = std::max<uint32_t>(1, cus / t);
+        const uint64_t ts = (uint64_t)t * s;
+        return (double)ts / ((double)cus * (double)ceil_div(ts, cus));
+    };
+    const bool narrow = rows <= 1024;
+    // a registered FP16 copy of w: the same sums with the weights copied, not dequantized
+    const auto copy = b->w16.find(w->addr);
+    const uint64_t w16 = copy == b->w16.end() || !tall ? 0 : copy->second;
+    const uint32_t br = narrow || fill(96) > fill(128) ? 96u : 128u;
+    GhKernel k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96 : K_GEMM3_Q6K_R96) : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
+    if (!tall)
+        k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96_T128 : K_GEMM3_Q6K_R96_T128)
+                     : (q4 ? K_GEMM3_Q4K_R128_T128 : K_GEMM3_Q6K_R128_T128);
+    if (w16)
+        k = br == 96 ? (q4 ? K_GEMM4W_Q4K_R96 : K_GEMM4W_Q6K_R96) : (q4 ? K_GEMM4W_Q4K_R128 : K_GEMM4W_Q6K_R128);
+    const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
+    const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
+    const uint32_t splits = clamp_splits(std::max<uint32_t>(1, slots / tiles));
+    return gemm_launch(b, k, 512, tr, tt, splits, out, a, w, n, e, w16);
 }
 
-// The SiLU epilogue is compiled into the warp-specialized kernels (n >= kGemmShortMinTokens)
-// only; the tail runs after any GEMM (n >= kGemmMinTokens).
+// The SiLU epilogue and the tail apply to every GEMM (n >= kGemmMinTokens).
 bool gemm_epi_applies(uint32_t n, uint32_t out_dim, bool tail) {
-    return tail ? n >= kGemmMinTokens && out_dim % 4 == 0 && out_dim <= kGemmTailMaxRows : n >= kGemmShortMinTokens;
+    return n >= kGemmMinTokens && (!tail || (out_dim % 4 == 0 && out_dim <= kGemmTailMaxRows));
 }
 
 int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,

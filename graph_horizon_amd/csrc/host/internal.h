@@ -57,10 +57,6 @@ enum GhKernel : int {
     K_ATTN_MFMA_G4,
     K_ATTN_MFMA_G8,
     // prefill GEMM tile variants (tokens x rows per workgroup), Q4_K then Q6_K
-    K_GEMM_Q4K_T128_R64,
-    K_GEMM_Q4K_T128_R128,
-    K_GEMM_Q6K_T128_R64,
-    K_GEMM_Q6K_T128_R128,
     K_GEMM_REDUCE,
     K_GEMM_TAIL,
     K_GEMM_REDUCE_ROPE,

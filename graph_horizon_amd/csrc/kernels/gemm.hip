@@ -206,86 +206,10 @@ __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc
     }
 }
 
-// Tiling: 4 waves stacked along tokens; wave w owns tokens t0 + WT·w .. + WT, all BR rows of
-// the workgroup, as (WT/32) x (BR/32) tiles of v_mfma_f32_32x32x16_f16 (A = activations
-// straight from global memory into registers, B = weights from the LDS tile).
-template <uint32_t FMT, int WT, int BR>
-__device__ __forceinline__ void gemm_body(const GhGemmArgs& a) {
-    constexpr int TI = WT / 32, TJ = BR / 32;
-    __shared__ __attribute__((aligned(16))) _Float16 wbuf[2][BR * LDK];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t r0 = blockIdx.x * BR, t0 = blockIdx.y * (4 * WT) + wave * WT;
-    const uint32_t units = a.in_dim / 64;
-    const uint32_t per = (units + a.splits - 1) / a.splits;
-    const uint32_t u0 = blockIdx.z * per, u1 = min(units, u0 + per);
-    const uint32_t fm = lane & 31u, fg = lane >> 5;  // fragment row, k half
-    const bool wload = threadIdx.x < 2 * BR;
-
-    // A fragments of a unit: [i][sub-step ks of 16]: tokens t0 + 32 i + fm, LDS-order k chunk
-    // 2 ks + fg (8 halves)
-    const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
-    uint32_t trow[TI];
-#pragma unroll
-    for (int i = 0; i < TI; ++i) trow[i] = min(t0 + 32 * i + fm, a.n - 1) * a.in_dim;
-    auto load_x = [&](uint32_t u, h8 (&xf)[TI][4]) {
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                xf[i][ks] = *(const GH_GLOBAL h8*)(x + trow[i] + chunk_k<FMT>(u, 2 * ks + fg));
-    };
-
-    f16v acc[TI][TJ];
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = f16v{};
-
-    if (u0 < u1) {
-        WStage ws;
-        h8 xf[TI][4], xn[TI][4];
-        if (wload) load_w<FMT, BR>(a, r0, u0, ws);
-        load_x(u0, xf);
-        if (wload) store_w<FMT, BR>(u0, ws, wbuf[0]);
-        __syncthreads();
-        for (uint32_t u = u0; u < u1; ++u) {
-            const uint32_t cur = (u - u0) & 1u;
-            const bool more = u + 1 < u1;
-            if (more) {
-                if (wload) load_w<FMT, BR>(a, r0, u + 1, ws);
-                load_x(u + 1, xn);
-            }
-            const _Float16* wb = wbuf[cur];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                h8 bf[TJ];
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
-#pragma unroll
-                for (int i = 0; i < TI; ++i)
-#pragma unroll
-                    for (int j = 0; j < TJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[i][ks], bf[j], acc[i][j], 0, 0, 0);
-            }
-            if (more && wload) store_w<FMT, BR>(u + 1, ws, wbuf[cur ^ 1u]);
-            __syncthreads();
-            if (more) {
-#pragma unroll
-                for (int i = 0; i < TI; ++i)
-#pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) xf[i][ks] = xn[i][ks];
-            }
-        }
-    }
-
-    gemm_write<TI, TJ, false>(a, acc, t0, r0, fm, fg, blockIdx.z, a.rows, 0);
-}
-
 // Warp-specialized variant for long batches: a 512-thread workgroup owns 4·WT tokens x BR rows
 // (WT = 64: 256 tokens; WT = 32: 128 tokens, for chunks of fewer than 256 rows, where split K
 // has to spread the units over many workgroups: the producers' kL units in flight keep those
-// short ranges streaming where gemm_body's one unit of lookahead leaves them waiting on
-// memory). Waves 0-3 (consumers) run the matrix cores (WT tokens each, B from LDS). Waves 4-7 (producers) stream the weight bytes
+// short ranges streaming, where a tile with one unit of lookahead waited on memory). Waves 0-3 (consumers) run the matrix cores (WT tokens each, B from LDS). Waves 4-7 (producers) stream the weight bytes
 // kL units ahead of use — kL register sets, selected statically by unrolling the loop kL-fold —
 // and dequantize each unit into a kS-stage LDS ring, kS - 1 units ahead of the consumers. One
 // barrier per unit: in the interval of unit u the consumers read stage (u - u0) % kS while the
@@ -413,11 +337,6 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
 }  // namespace
 
 // Tile variants: 128 tokens per workgroup (4 waves x 32) x 64 or 128 weight rows.
-#define GH_GEMM(SUF, WT, BR)                                                                       \
-    GH_KERNEL __launch_bounds__(256) void gh_gemm_q4k_##SUF(GhGemmArgs a) { gemm_body<kQ4K, WT, BR>(a); } \
-    GH_KERNEL __launch_bounds__(256) void gh_gemm_q6k_##SUF(GhGemmArgs a) { gemm_body<kQ6K, WT, BR>(a); }
-GH_GEMM(t128_r64, 32, 64)
-GH_GEMM(t128_r128, 32, 128)
 // warp-specialized 256-token tiles (512 threads)
 #define GH_GEMM3(NAME, FMT, BR)                                                                    \
     GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
