@@ -57,6 +57,7 @@ const KernelName kKernels[] = {
     {K_GEMM4W_Q4K_R96, "gh_gemm4w_q4k_r96"},   {K_GEMM4W_Q6K_R96, "gh_gemm4w_q6k_r96"},
     {K_GEMM3_Q4K_R128_T128, "gh_gemm3_q4k_r128_t128"}, {K_GEMM3_Q6K_R128_T128, "gh_gemm3_q6k_r128_t128"},
     {K_GEMM3_Q4K_R96_T128, "gh_gemm3_q4k_r96_t128"},   {K_GEMM3_Q6K_R96_T128, "gh_gemm3_q6k_r96_t128"},
+    {K_GEMM3_MIXED_R128_T128, "gh_gemm3_mixed_r128_t128"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -981,12 +982,12 @@ int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_bu
     return op_gemm(b, out->addr, a, w, n, &e);
 }
 
-bool gemm_multi_applies(uint32_t n) { return n >= 256; }
+bool gemm_multi_applies(uint32_t n) { return n >= kGemmMinTokens; }
 
 int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint32_t nseg, uint32_t n,
                   const GhRopeTable* rope, uint32_t base, uint32_t head_dim) {
     constexpr uint32_t BR = 128;
-    if (nseg == 0 || nseg > 3 || !gemm_multi_applies(n)) return fail(b, GH_E_UNSUPPORTED, "gemm multi: 1..3 matrices, n >= 256");
+    if (nseg == 0 || nseg > 3 || !gemm_multi_applies(n)) return fail(b, GH_E_UNSUPPORTED, "gemm multi: 1..3 matrices, n >= 8");
     const uint32_t in_dim = segs[0].w->cols;
     GhGemmArgs ga{};
     uint32_t tiles = 0, total = 0;
@@ -1006,7 +1007,8 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
         total += w->rows;
     }
     if (!fits(a, (uint64_t)n * in_dim * 2)) return fail(b, GH_E_RANGE, "gemm multi: input too small");
-    const uint32_t tt = ceil_div(n, 256u), units = in_dim / 64;
+    const bool tall = n >= 256;  // 256-token tiles; 128 below (no FP16 copies there)
+    const uint32_t tt = ceil_div(n, tall ? 256u : 128u), units = in_dim / 64;
     // splits: the CUs over the tiles, at most 16 and at least 8 units per split, none empty
     uint32_t splits = std::max<uint32_t>(1, std::min<uint32_t>({b->cus / (tiles * tt), std::max<uint32_t>(1, units / 8), 16u}));
     for (;;) {
@@ -1016,7 +1018,7 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
     }
     // FP16 copies registered for every matrix: the launch copies the weights instead of
     // dequantizing them
-    bool copies = true;
+    bool copies = tall;
     for (uint32_t i = 0; i < nseg; ++i) copies = copies && b->w16.count(segs[i].w->addr);
     if (copies)
         for (uint32_t i = 0; i < nseg; ++i) ga.seg[i].w = b->w16.at(segs[i].w->addr);
@@ -1040,7 +1042,8 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
         if (rc) return rc;
         ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
     }
-    int rc = launch(b, copies ? K_GEMM4W_MIXED_R128 : K_GEMM3_MIXED_R128, tiles, tt, splits, 512, &ga);
+    const GhKernel k = copies ? K_GEMM4W_MIXED_R128 : tall ? K_GEMM3_MIXED_R128 : K_GEMM3_MIXED_R128_T128;
+    int rc = launch(b, k, tiles, tt, splits, 512, &ga);
     if (rc) return rc;
     if (splits > 1) {
         const uint64_t npairs = (uint64_t)n * total / 2;

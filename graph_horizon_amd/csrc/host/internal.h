@@ -82,6 +82,7 @@ enum GhKernel : int {
     K_GEMM3_Q6K_R128_T128,
     K_GEMM3_Q4K_R96_T128,
     K_GEMM3_Q6K_R96_T128,
+    K_GEMM3_MIXED_R128_T128,
     K_COUNT
 };
 
@@ -221,7 +222,7 @@ int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_bu
                   uint32_t out_dim, uint32_t n, const gh_buf* gate, const gh_buf* resid,
                   const gh_buf* norm = nullptr, const gh_buf* normed = nullptr, float eps = 0.0f);
 bool gemm_rope_applies(uint32_t n, uint32_t out_dim, uint32_t head_dim, const GhRopeTable& rope);
-// Several projections of one FP16 input (n >= 256 tokens) in one warp-specialized launch (row
+// Several projections of one FP16 input (n >= 8 tokens) in one warp-specialized launch (row
 // tiles of 128, each in its matrix's format) and one split reduce that writes each matrix's
 // FP16 output and applies its RoPE role (GH_GEMM_ROLE_*; rows of head_dim, positions base + t)
 // — the values of separate gh_matmul_batched launches and op_rope.

@@ -499,8 +499,8 @@ GH_KERNEL __launch_bounds__(256) void gh_dequant_f16_q6k(GhGemmArgs a) { dequant
 // blockIdx.x belongs to the matrix whose tiles start at or below it, and runs that matrix's
 // format (Q4_K or Q6_K) over the shared LDS block; a.rows is the total row count, the
 // partials' row length.
-GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128(GhGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(128)];
+template <int WT>
+__device__ __forceinline__ void gemm3_mixed(const GhGemmArgs& a, _Float16* lds) {
     uint32_t s = 0;
     for (uint32_t i = 1; i < a.nseg; ++i)
         if (blockIdx.x >= a.seg[i].tile0) s = i;
@@ -510,9 +510,18 @@ GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128(GhGemmArgs a) {
     m.out = a.seg[s].out;
     const uint32_t bx = blockIdx.x - a.seg[s].tile0;
     if (a.seg[s].fmt == kQ4K)
-        gemm3_body<kQ4K, 128>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+        gemm3_body<kQ4K, 128, WT>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
     else
-        gemm3_body<kQ6K, 128>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+        gemm3_body<kQ6K, 128, WT>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+}
+GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(128)];
+    gemm3_mixed<64>(a, lds);
+}
+// 128-token tiles, for batches of fewer than 256 tokens
+GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128_t128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_T(128, 32)];
+    gemm3_mixed<32>(a, lds);
 }
 
 // The multi-matrix launch over FP16 weights with every wave on the matrix cores (gemm4_body).
