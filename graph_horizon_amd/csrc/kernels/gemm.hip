@@ -366,10 +366,11 @@ GH_GEMM3T(gh_gemm3_q6k_r96_t128, kQ6K, 96)
 // at 512 tokens instead of 192. Each unit's activation lines and weight rows go into a
 // 3-stage LDS ring by LDS DMA that every wave shares in (activation rows 32 w .. + 32 and
 // weight row blocks w, w + 8 of 8 rows, 1 KiB loads from inline assembly; both operands in
-// 128-byte rows with chunk c of row r at slot c ^ (r / 2) % 8). The unit of iteration u goes
-// out two iterations ahead into the stage read during u - 1; each iteration waits for all but
-// its own loads before the barrier. The k order of every output's sum is the one gemm3_body
-// uses: the same bits.
+// 128-byte rows with chunk c of row r at slot c ^ (r / 2) % 8). Each wave holds one unit's
+// fragments in registers and reads the next unit's into a second set while the matrix cores
+// work on the first, so no k-step waits on an LDS read. After the barrier of iteration u
+// (unit u + 1 landed, every wave's reads of unit u done) unit u + 3 goes into unit u's stage.
+// The k order of every output's sum is the one gemm3_body uses: the same bits.
 #define GH_GEMM4_LDS(BR) (3 * (256 + (BR)) * 64)
 template <uint32_t FMT, int BR>
 __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, uint32_t bx, uint32_t by,
@@ -430,41 +431,76 @@ __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, u
     for (uint32_t i = 0; i < TI; ++i)
 #pragma unroll
         for (uint32_t j = 0; j < TJ; ++j) acc[i][j] = f16v{};
-    issue(u0, 0);
-    issue(uc(u0 + 1), 1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (uint32_t u = u0; u < u1; ++u) {
-        const uint32_t k = u - u0;
-        issue(uc(u + 2), (k + 2) % 3);
-        const _Float16* xb = stage(k % 3) + (WTOK * g) * 64;
-        const _Float16* wb = stage(k % 3) + 256 * 64;
+    // one unit's fragments: 4 k-steps x (TI activation + TJ weight) 8-half lane slices
+    struct Frags {
+        h8 a[4][TI], b[4][TJ];
+    };
+    auto read = [&](uint32_t st, Frags& f) __attribute__((always_inline)) {
+        const _Float16* xb = stage(st) + (WTOK * g) * 64;
+        const _Float16* wb = stage(st) + 256 * 64;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            h8 af[TI], bf[TJ];
 #pragma unroll
             for (uint32_t i = 0; i < TI; ++i) {
                 const uint32_t r = 32 * i + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
-                af[i] = *(const h8*)(xb + r * 64 + c * 8);
+                f.a[ks][i] = *(const h8*)(xb + r * 64 + c * 8);
             }
 #pragma unroll
             for (uint32_t j = 0; j < TJ; ++j) {
                 const uint32_t r = WROW * hr + 32 * j + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
-                bf[j] = *(const h8*)(wb + r * 64 + c * 8);
+                f.b[ks][j] = *(const h8*)(wb + r * 64 + c * 8);
             }
+        }
+    };
+    auto mma = [&](const Frags& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (uint32_t i = 0; i < TI; ++i)
 #pragma unroll
                 for (uint32_t j = 0; j < TJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[ks][i], f.b[ks][j], acc[i][j], 0, 0, 0);
+    };
+    // all but this wave's last n issues have landed
+    auto wait_but = [&](int n) __attribute__((always_inline)) {
+        if (kB == 1 || two) {
+            if (n == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (4 + kB)) : "memory");
+            else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + kB) : "memory");
+        } else {
+            if (n == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (4 + kB - 1)) : "memory");
+            else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + kB - 1) : "memory");
         }
-        // unit u + 1 has landed: all but this iteration's own loads (4 + 1 or 2)
-        if (kB == 1 || two)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + kB) : "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + kB - 1) : "memory");
+    };
+    // iteration k (unit u): unit u + 1 has landed -> barrier (every wave's reads of unit u are
+    // done, so its stage k % 3 takes unit u + 3) -> the next unit's fragments are read while
+    // this unit's matrix work runs from registers
+    auto step = [&](uint32_t u, Frags& cur, Frags& nxt) __attribute__((always_inline)) {
+        const uint32_t k = u - u0;
+        wait_but(1);
         __syncthreads();
+        issue(uc(u + 3), k % 3);
+        read((k + 1) % 3, nxt);
+        mma(cur);
+        // one fragment read between consecutive matrix instructions
+#pragma unroll
+        for (uint32_t q = 0; q < 4 * (TI + TJ); ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        }
+    };
+    issue(u0, 0);
+    issue(uc(u0 + 1), 1);
+    issue(uc(u0 + 2), 2);
+    wait_but(2);
+    __syncthreads();
+    Frags f0, f1;
+    read(0, f0);
+    uint32_t u = u0;
+    for (; u + 1 < u1; u += 2) {
+        step(u, f0, f1);
+        step(u + 1, f1, f0);
     }
+    if (u < u1) step(u, f0, f1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) loads have landed
     gemm_write<TI, TJ, true>(a, acc, by * 256 + WTOK * g, r0 + WROW * hr, fm, fg, bz, ps, pc);
 }
