@@ -925,19 +925,18 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
     // better — 96 rows for 12288 x 4096 (256 tiles against 192 of 128 rows), 128 rows
     // otherwise. Narrow outputs (<= 1024 rows) take 96 rows with two workgroups per CU
     // and up to 16 splits: their few units per split leave latency for a second to hide.
-    // Batches of fewer than 256 tokens take 128-token tiles (no FP16 copies: at these
-    // sizes their four-fold weight stream is the floor).
-    const bool tall = n >= 256;
+    // Batches of 128 tokens or fewer take 128-token tiles (kGemmTallTokens).
+    const bool tall = n >= kGemmTallTokens;
     const uint32_t tt = ceil_div(n, tall ? 256u : 128u), cus = b->cus;
+    // a registered FP16 copy of w: the same sums with the weights copied, not dequantized
+    const auto copy = b->w16.find(w->addr);
+    const uint64_t w16 = copy == b->w16.end() || !tall ? 0 : copy->second;
     auto fill = [&](uint32_t br) {
         const uint32_t t = ceil_div(rows, br) * tt, s = std::max<uint32_t>(1, cus / t);
         const uint64_t ts = (uint64_t)t * s;
         return (double)ts / ((double)cus * (double)ceil_div(ts, cus));
     };
     const bool narrow = rows <= 1024;
-    // a registered FP16 copy of w: the same sums with the weights copied, not dequantized
-    const auto copy = b->w16.find(w->addr);
-    const uint64_t w16 = copy == b->w16.end() || !tall ? 0 : copy->second;
     const uint32_t br = narrow || fill(96) > fill(128) ? 96u : 128u;
     GhKernel k = br == 96 ? (q4 ? K_GEMM3_Q4K_R96 : K_GEMM3_Q6K_R96) : (q4 ? K_GEMM3_Q4K_R128 : K_GEMM3_Q6K_R128);
     if (!tall)
@@ -1007,7 +1006,11 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
         total += w->rows;
     }
     if (!fits(a, (uint64_t)n * in_dim * 2)) return fail(b, GH_E_RANGE, "gemm multi: input too small");
-    const bool tall = n >= 256;  // 256-token tiles; 128 below (no FP16 copies there)
+    // 256-token tiles above 128 tokens, 128-token tiles below (kGemmTallTokens); FP16 copies
+    // registered for every matrix: the launch copies the weights instead of dequantizing them
+    const bool tall = n >= kGemmTallTokens;
+    bool copies = tall;
+    for (uint32_t i = 0; i < nseg; ++i) copies = copies && b->w16.count(segs[i].w->addr);
     const uint32_t tt = ceil_div(n, tall ? 256u : 128u), units = in_dim / 64;
     // splits: the CUs over the tiles, at most 16 and at least 8 units per split, none empty
     uint32_t splits = std::max<uint32_t>(1, std::min<uint32_t>({b->cus / (tiles * tt), std::max<uint32_t>(1, units / 8), 16u}));
@@ -1016,10 +1019,6 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
         if (s == splits) break;
         splits = s;
     }
-    // FP16 copies registered for every matrix: the launch copies the weights instead of
-    // dequantizing them
-    bool copies = tall;
-    for (uint32_t i = 0; i < nseg; ++i) copies = copies && b->w16.count(segs[i].w->addr);
     if (copies)
         for (uint32_t i = 0; i < nseg; ++i) ga.seg[i].w = b->w16.at(segs[i].w->addr);
     ga.x = a->addr;

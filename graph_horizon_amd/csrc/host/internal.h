@@ -222,6 +222,11 @@ int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_bu
                   uint32_t out_dim, uint32_t n, const gh_buf* gate, const gh_buf* resid,
                   const gh_buf* norm = nullptr, const gh_buf* normed = nullptr, float eps = 0.0f);
 bool gemm_rope_applies(uint32_t n, uint32_t out_dim, uint32_t head_dim, const GhRopeTable& rope);
+// Batches of more than 128 tokens run the GEMMs in 256-token tiles, over a registered FP16 copy
+// of the weights (b->w16) where there is one; 128 tokens or fewer fit the 128-token tiles of
+// the dequantizing kernels exactly, where a copy's four-fold weight stream costs more. Both
+// forms of a batch size share one tile and split plan, so they give the same bits.
+constexpr uint32_t kGemmTallTokens = 129;
 // Several projections of one FP16 input (n >= 8 tokens) in one warp-specialized launch (row
 // tiles of 128, each in its matrix's format) and one split reduce that writes each matrix's
 // FP16 output and applies its RoPE role (GH_GEMM_ROLE_*; rows of head_dim, positions base + t)

@@ -43,7 +43,7 @@ struct gh_model {
     uint32_t last_rows = 0;  // rows of the most recent pass (for read_x)
     bool last_prefill = false;
     // FP16 copies of the layer matrices for the prefill GEMMs (registered in b->w16), made
-    // before the first prefill chunk of kGemmCopyRows rows or more; empty until then (and
+    // before the first prefill chunk of more than 128 rows (kGemmTallTokens); empty until then (and
     // left unregistered during shorter chunks, whose GEMMs dequantize)
     std::vector<std::pair<uint64_t, gh_buf>> w16;  // (weight address, copy)
 };
@@ -55,10 +55,6 @@ int alloc(gh_model* m, uint64_t bytes, gh_buf* out) {
     if (!rc) m->owned.push_back(*out);
     return rc;
 }
-
-// Prefill chunks of this many rows or more (those that run the warp-specialized GEMMs) make
-// and use the FP16 copies.
-constexpr uint32_t kGemmCopyRows = 256;
 
 // Register the copies for this prefill call, or withdraw them (shorter chunks dequantize).
 void set_w16(gh_model* m, bool on) {
@@ -518,7 +514,7 @@ int gh_model_prefill(gh_model* m, const uint32_t* tokens, uint32_t n, uint32_t b
     // the chunk's embedding rows in one launch from the token ids on the device (the values
     // of embed per row, encode.rs:16-106, without a launch per token)
     int urc = gh_upload(m->b, &m->prompt, 0, tokens, (uint64_t)n * 4);
-    const bool copies = std::min(cap, n) >= kGemmCopyRows;
+    const bool copies = std::min(cap, n) >= kGemmTallTokens;
     if (!urc && copies) urc = ensure_w16(m);
     if (urc) return urc;
     set_w16(m, copies);

@@ -241,7 +241,7 @@ typedef struct gh_model_config {
  * for tools that cannot trace kernels inside graphs. */
 #define GH_MODEL_NO_GRAPH 1u
 /* gh_model_prefill keeps no FP16 copy of the layer matrices. By default the first prefill
- * call with chunks of 256 rows or more dequantizes each Q/K/V/O/gate/up/down matrix once
+ * call with chunks of more than 128 rows dequantizes each Q/K/V/O/gate/up/down matrix once
  * into an FP16 copy (2 bytes per weight: 14.8 GB for the 8B shape), which the GEMMs of such
  * chunks then copy into LDS instead of dequantizing every tile; the results are the same
  * bits either way. Without the memory for the copy, the prefill dequantizes as with this

@@ -92,15 +92,16 @@ def test_full_width_prefill_driver_matches_op_by_op(hip, name):
     gm.close()
 
 
-@pytest.mark.parametrize("n", [300, 2048])
+@pytest.mark.parametrize("n", [160, 300, 2048])
 @pytest.mark.parametrize("name", ["8b", "14b"])
 def test_prefill_fp16_weight_copies_are_bit_identical(hip, name, n):
-    """The FP16 copies of the layer matrices (made before the first prefill with chunks of 256
-    rows or more) hold the values the dequantizing GEMM producers stage, and the all-waves-MFMA
-    kernels that read them sum in the same k order: the prefill leaves the same logits, residual
-    row and K/V cache bits as with GH_MODEL_NO_F16_WEIGHTS. 300 rows run gate/up in 96-row
-    tiles and the mixed Q/K/V launch, O and the Q6_K down in 128-row tiles with split K (2, 4
-    and 4 splits); 2048 rows run every GEMM in 128-row tiles, unsplit."""
+    """The FP16 copies of the layer matrices (made before the first prefill with chunks of more
+    than 128 rows) hold the values the dequantizing GEMM producers stage, and the all-waves-MFMA
+    kernels that read them sum in the same k order over the same tiles and splits: the prefill
+    leaves the same logits, residual row and K/V cache bits as with GH_MODEL_NO_F16_WEIGHTS.
+    160 rows fill one 256-token tile (the rest clamped to the last row); 300 rows run gate/up
+    in 96-row tiles and the mixed Q/K/V launch, O and the Q6_K down in 128-row tiles with split
+    K (2, 4 and 4 splits); 2048 rows run every GEMM in 128-row tiles, unsplit."""
     from graph_horizon_amd import _ffi as F
 
     shape = dataclasses.replace(synth.SHAPES[name], name=f"{name}-1", block_count=1)
