@@ -47,10 +47,12 @@ def test_full_width_blocks_decode_matches_oracle(hip, name):
     om.close()
 
 
+@pytest.mark.parametrize("n", [100, 300])
 @pytest.mark.parametrize("name", ["8b", "14b"])
-def test_full_width_prefill_driver_matches_op_by_op(hip, name):
+def test_full_width_prefill_driver_matches_op_by_op(hip, name, n):
     """The driver's fused prefill at the real widths, 300 rows in one chunk (a partial second
-    256-token tile) — Q/K/V in one mixed-format GEMM with its RoPE split reduce writing K/V into
+    256-token tile, over the FP16 weight copies) or 100 rows (one partial 128-token tile of the
+    dequantizing kernels, no copies) — Q/K/V in one mixed-format GEMM with its RoPE split reduce writing K/V into
     the cache, the O and down projections' split sums folded into the residual and the
     RMSNorm, SiLU in the up GEMM, 16-row attention blocks — against every trait op recorded
     separately over the C ABI (prefill::record_batch): logits, the last row's residual and the
@@ -61,7 +63,7 @@ def test_full_width_prefill_driver_matches_op_by_op(hip, name):
     from graph_over_abi import AbiGraph
 
     shape = dataclasses.replace(synth.SHAPES[name], name=f"{name}-1", block_count=1)
-    seed, ctx, n = 91, 320, 300
+    seed, ctx = 91, 320
     tensors = list(synth.model_tensors(shape, seed))
     ref = AbiGraph(hip, shape, seed, ctx, tensors=tensors)
     gm = HipModel(hip, synth.model_config(shape, ctx, prefill_rows=512))
