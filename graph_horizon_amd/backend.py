@@ -214,6 +214,13 @@ class HipBackend:
     def synchronize(self):
         self._ok(self.lib.gh_synchronize(self.h), "synchronize")
 
+    def scratch_info(self):
+        """(workspace bytes, attention-merge counter slots, generation) of the backend."""
+        ws, cs, gen = C.c_uint64(), C.c_uint64(), C.c_uint64()
+        self._ok(self.lib.gh_scratch_info(self.h, C.byref(ws), C.byref(cs), C.byref(gen)),
+                 "scratch_info")
+        return ws.value, cs.value, gen.value
+
     def set_attention_splits(self, splits: int):
         """Decode attention workgroups per (row, kv head); 0 = the backend's policy."""
         self._ok(self.lib.gh_set_attention_splits(self.h, splits), "set_attention_splits")

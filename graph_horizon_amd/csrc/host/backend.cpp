@@ -44,7 +44,7 @@ const KernelName kKernels[] = {
     {K_ATTN_MFMA_G8, "gh_attn_mfma_g8"},
 
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},
-    {K_GEMM_REDUCE_ROPE, "gh_gemm_reduce_rope"}, {K_GEMM3_MIXED_R128, "gh_gemm3_mixed_r128"},
+    {K_GEMM3_MIXED_R128, "gh_gemm3_mixed_r128"},
     {K_GEMM_REDUCE_SEG, "gh_gemm_reduce_seg"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
     {K_ATTN_PREFILL_G4_R16, "gh_attn_prefill_g4_r16"},
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
@@ -697,11 +697,14 @@ int gh_view(gh_backend* b, const gh_buf* buf, uint64_t off, uint64_t len, gh_buf
     if (!b || !buf || !out) return GH_E_INVALID;
     if (buf->kind == GH_BUF_WEIGHT) return fail(b, GH_E_INVALID, "view of a packed weight");
     if (off > buf->bytes || len > buf->bytes - off) return fail(b, GH_E_RANGE, "view beyond buffer");
+    if (off % kMinViewAlignment) return fail(b, GH_E_INVALID, "view offset not 16-byte aligned");
     *out = gh_buf{buf->addr + off, len, buf->format, GH_BUF_VIEW, 0, 0};
     return GH_OK;
 }
 
-uint64_t gh_min_buffer_offset_alignment(const gh_backend*) { return 4; }
+// The kernels read activation rows with 16-byte vector loads and LDS DMA, so views start on
+// 16-byte boundaries (every Mistral row stride is a multiple of 512 bytes).
+uint64_t gh_min_buffer_offset_alignment(const gh_backend*) { return kMinViewAlignment; }
 
 int gh_upload(gh_backend* b, const gh_buf* dst, uint64_t off, const void* src, uint64_t len) {
     if (!b || !dst || (!src && len)) return GH_E_INVALID;
@@ -824,7 +827,8 @@ int gh_kv_write(gh_backend* b, gh_encoder* enc, const gh_kv* kv, const gh_buf* k
     if (kv->scheme != GH_KV_F16) return latch(enc, fail(b, GH_E_UNSUPPORTED, "kv_write: only the f16 scheme"));
     const uint64_t kb = (uint64_t)vectors * kv->head_dim * 2, vb = (uint64_t)vectors * kv->value_dim * 2;
     if (!fits(k, kb) || !fits(v, vb) || k_payload_offset % 2 || v_payload_offset % 2 ||
-        k_payload_offset + kb > kv->k.bytes || v_payload_offset + vb > kv->v.bytes)
+        k_payload_offset > kv->k.bytes || kb > kv->k.bytes - k_payload_offset ||
+        v_payload_offset > kv->v.bytes || vb > kv->v.bytes - v_payload_offset)
         return latch(enc, fail(b, GH_E_RANGE, "kv_write: beyond cache"));
     return latch(enc, op_kv_write(b, kv, k, v, k_payload_offset / 2, v_payload_offset / 2, vectors, nullptr));
 }
@@ -884,22 +888,6 @@ static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, u
         ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
     }
     int rc = launch(b, k, tr, tt, splits, block, &ga);
-    if (!rc && e && e->rope) {
-        if (splits == 1) {
-            gh_buf o{};
-            o.addr = out;
-            o.bytes = (uint64_t)n * w->rows * 2;
-            return op_rope(b, *e->rope, &o, w->rows / e->head_dim, e->head_dim, e->rope_base, n, e->rope_role, nullptr);
-        }
-        ga.table = (uint64_t)e->rope->table;
-        ga.post = e->rope_role == GH_ROPE_QUERY ? (uint64_t)e->rope->post : 0;
-        ga.base = e->rope_base;
-        ga.head_dim = e->head_dim;
-        ga.pairs = e->rope->yarn.rope_dim / 2;
-        const uint64_t npairs = (uint64_t)n * w->rows / 2;
-        return launch(b, K_GEMM_REDUCE_ROPE, (uint32_t)std::min<uint64_t>(ceil_div(npairs, (uint64_t)256), 4096), 1,
-                      1, 256, &ga);
-    }
     if (!rc && tail) {
         ga.aux = e->resid;
         ga.norm = e->norm;
@@ -1071,23 +1059,6 @@ int op_dequant_f16(gh_backend* b, const gh_buf* w, uint64_t out16) {
 bool gemm_rope_applies(uint32_t n, uint32_t out_dim, uint32_t head_dim, const GhRopeTable& rope) {
     return n >= kGemmMinTokens && head_dim && head_dim % 2 == 0 && out_dim % head_dim == 0 && rope.table &&
            rope.yarn.rope_dim <= head_dim;
-}
-
-int op_matmul_rope(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,
-                   uint32_t out_dim, uint32_t n, const GhRopeTable& rope, uint32_t role, uint32_t base,
-                   uint32_t head_dim) {
-    if (!gemm_rope_applies(n, out_dim, head_dim, rope) || (uint64_t)base + n > rope.positions)
-        return fail(b, GH_E_UNSUPPORTED, "matmul rope: GEMM path, whole heads, positions in the table");
-    if (!is_weight(w)) return fail(b, GH_E_UNSUPPORTED, "matmul: weight must be Q4_K or Q6_K");
-    if (w->cols != in_dim || w->rows != out_dim) return fail(b, GH_E_INVALID, "matmul: weight shape mismatch");
-    if (!fits(a, (uint64_t)n * in_dim * 2) || !fits(out, (uint64_t)n * out_dim * 2))
-        return fail(b, GH_E_RANGE, "matmul: buffer too small");
-    GemmEpi e;
-    e.rope = &rope;
-    e.rope_role = role;
-    e.rope_base = base;
-    e.head_dim = head_dim;
-    return op_gemm(b, out->addr, a, w, n, &e);
 }
 
 }  // namespace gh
@@ -1314,6 +1285,15 @@ int gh_set_attention_splits(gh_backend* b, uint32_t splits) {
     if (splits > 32) return fail(b, GH_E_INVALID, "attention splits: at most 32");
     b->attn_splits = splits;
     ++b->gen;  // recorded graphs hold the old grid
+    return GH_OK;
+}
+
+int gh_scratch_info(const gh_backend* b, uint64_t* workspace_bytes, uint64_t* counter_slots,
+                    uint64_t* generation) {
+    if (!b) return GH_E_INVALID;
+    if (workspace_bytes) *workspace_bytes = b->ws_bytes;
+    if (counter_slots) *counter_slots = b->counter_slots;
+    if (generation) *generation = b->gen;
     return GH_OK;
 }
 

@@ -59,7 +59,6 @@ enum GhKernel : int {
     // prefill GEMM tile variants (tokens x rows per workgroup), Q4_K then Q6_K
     K_GEMM_REDUCE,
     K_GEMM_TAIL,
-    K_GEMM_REDUCE_ROPE,
     K_GEMM3_MIXED_R128,
     K_GEMM_REDUCE_SEG,
     K_ATTN_PREFILL_G4,
@@ -195,6 +194,8 @@ struct GemvSeg {
 // norm: x is the FP32 residual and rmsnorm_x(norm, eps) is applied while staging it
 // (in_dim <= kFusedNormMaxDim).
 constexpr uint32_t kFusedNormMaxDim = 5120;
+// gh_view offsets and gh_min_buffer_offset_alignment: rows are read with 16-byte loads
+constexpr uint64_t kMinViewAlignment = 16;
 // rope: the table the RoPE epilogues read (required when a segment has one).
 int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, uint32_t n,
             uint32_t base, const void* pos_ptr, uint32_t head_dim, const gh_buf* up,
@@ -210,8 +211,6 @@ struct GemmEpi {
     uint64_t aux = 0;
     uint64_t resid = 0, norm = 0, normed = 0;
     float eps = 0.0f;
-    const GhRopeTable* rope = nullptr;
-    uint32_t rope_role = 0, rope_base = 0, head_dim = 0;
 };
 int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n,
             const GemmEpi* e = nullptr);
@@ -241,9 +240,6 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
                   const GhRopeTable* rope, uint32_t base, uint32_t head_dim);
 // gh_matmul_batched then op_rope(role, positions base + t) on its output, the rotation folded
 // into the split reduce when the GEMM splits K (n >= 8 tokens, out_dim a multiple of head_dim).
-int op_matmul_rope(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,
-                   uint32_t out_dim, uint32_t n, const GhRopeTable& rope, uint32_t role, uint32_t base,
-                   uint32_t head_dim);
 size_t attention_workspace(uint32_t rows, uint32_t q_heads, uint32_t splits);
 uint32_t attention_splits(const gh_backend* b, uint32_t max_len, uint32_t kv_heads, uint32_t rows);
 int ensure_counters(gh_backend* b, size_t slots);

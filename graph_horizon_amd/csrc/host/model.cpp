@@ -46,6 +46,9 @@ struct gh_model {
     // before the first prefill chunk of more than 128 rows (kGemmTallTokens); empty until then (and
     // left unregistered during shorter chunks, whose GEMMs dequantize)
     std::vector<std::pair<uint64_t, gh_buf>> w16;  // (weight address, copy)
+    // the copies did not fit (or crowded out a prefill's workspace): the prefill dequantizes
+    // from then on, until the weights are reloaded
+    bool w16_failed = false;
 };
 
 namespace {
@@ -74,20 +77,44 @@ void free_w16(gh_model* m) {
     m->w16.clear();
 }
 
+constexpr uint32_t kCopiedTensors[] = {GH_T_ATTN_Q, GH_T_ATTN_K, GH_T_ATTN_V, GH_T_ATTN_OUTPUT,
+                                       GH_T_FFN_GATE, GH_T_FFN_UP, GH_T_FFN_DOWN};
+
+// Device memory a prefill chunk of `rows` rows may still claim after the copies are made: the
+// GEMMs' split-K partials (at most one FP32 value per output and split, 32 splits bounded by
+// the CU count) and the attention partials, with 1 GiB beside them for the rest.
+uint64_t prefill_headroom(const gh_model* m, uint32_t rows) {
+    const gh_model_config& c = m->cfg;
+    const uint64_t widest = std::max<uint64_t>(c.feed_forward_length, (uint64_t)c.head_count * c.key_length);
+    const uint64_t split_k = (uint64_t)rows * widest * 4 * 8;
+    return split_k + ((uint64_t)256 << 20) + ((uint64_t)1 << 30);
+}
+
 // Dequantize every layer matrix once into an FP16 copy and register it, so that the prefill
 // GEMMs copy weight tiles into LDS instead of dequantizing them per tile (the same FP16 values:
 // identical results). 2 bytes per weight: 14.8 GB for the 8B shape, 24 GB for the 14B one, of
-// 288 GB. Without the memory the prefill keeps dequantizing (nothing is registered).
+// 288 GB. The copies are made only when the device has room for them and for a prefill chunk's
+// workspace beside them; otherwise (or when an allocation fails) the model records the failure
+// and its prefills keep dequantizing (nothing is registered) without trying again.
 int ensure_w16(gh_model* m) {
-    if ((m->cfg.flags & GH_MODEL_NO_F16_WEIGHTS) || !m->w16.empty()) return GH_OK;
+    if ((m->cfg.flags & GH_MODEL_NO_F16_WEIGHTS) || m->w16_failed || !m->w16.empty()) return GH_OK;
+    uint64_t need = prefill_headroom(m, m->cfg.prefill_rows);
     for (auto& l : m->layers)
-        for (uint32_t t : {GH_T_ATTN_Q, GH_T_ATTN_K, GH_T_ATTN_V, GH_T_ATTN_OUTPUT, GH_T_FFN_GATE, GH_T_FFN_UP,
-                           GH_T_FFN_DOWN}) {
+        for (uint32_t t : kCopiedTensors) need += (uint64_t)l[t].rows * l[t].cols * 2;
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess || free_b < need) {
+        (void)hipGetLastError();
+        m->w16_failed = true;
+        return GH_OK;
+    }
+    for (auto& l : m->layers)
+        for (uint32_t t : kCopiedTensors) {
             const gh_buf& w = l[t];
             gh_buf copy{};
             if (gh_alloc_buffer(m->b, (uint64_t)w.rows * w.cols * 2, &copy) != GH_OK) {
                 free_w16(m);
                 m->b->err.clear();
+                m->w16_failed = true;
                 return GH_OK;
             }
             int rc = op_dequant_f16(m->b, &w, copy.addr);
@@ -208,15 +235,6 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
         gh_buf kd{}, vd{};
         if (!rc) rc = gh_view(b, &m->kv.k, koff * 2, (uint64_t)rows * kw * 2, &kd);
         if (!rc) rc = gh_view(b, &m->kv.v, voff * 2, (uint64_t)rows * vw * 2, &vd);
-        // rope_yarn_batched (prefill/layer.rs:79-89) on the Q and K projections, folded into
-        // their split reduces
-        auto project_rope = [&](const gh_buf* out, const gh_buf* wt, uint32_t od, uint32_t role) {
-            if (gemm_rope_applies(rows, od, c.key_length, m->rope))
-                return op_matmul_rope(b, out, &s.normed, wt, d, od, rows, m->rope, role, base, c.key_length);
-            int r = gh_matmul_batched(b, enc, out, &s.normed, wt, d, od, rows);
-            if (!r) r = op_rope(b, m->rope, out, od / c.key_length, c.key_length, base, rows, role, nullptr);
-            return r;
-        };
         if (gemm_multi_applies(rows)) {
             // the three projections in one launch and one split reduce
             const GemmSegSpec qkv[3] = {{&w[GH_T_ATTN_Q], &s.q, GH_GEMM_ROLE_ROPE_QUERY},
@@ -224,9 +242,13 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
                                         {&w[GH_T_ATTN_V], &vd, GH_GEMM_ROLE_PLAIN}};
             if (!rc) rc = op_gemm_multi(b, &s.normed, qkv, 3, rows, &m->rope, base, c.key_length);
         } else {
-            if (!rc) rc = project_rope(&s.q, &w[GH_T_ATTN_Q], qw, GH_ROPE_QUERY);
-            if (!rc) rc = project_rope(&kd, &w[GH_T_ATTN_K], kw, GH_ROPE_KEY);
+            // chunks of fewer than 8 rows (the GEMV): rope_yarn_batched (prefill/layer.rs:79-89)
+            // on the Q rows and, in place, on the K cache rows
+            if (!rc) rc = gh_matmul_batched(b, enc, &s.q, &s.normed, &w[GH_T_ATTN_Q], d, qw, rows);
+            if (!rc) rc = gh_matmul_batched(b, enc, &kd, &s.normed, &w[GH_T_ATTN_K], d, kw, rows);
             if (!rc) rc = gh_matmul_batched(b, enc, &vd, &s.normed, &w[GH_T_ATTN_V], d, vw, rows);
+            if (!rc) rc = op_rope(b, m->rope, &s.q, c.head_count, c.key_length, base, rows, GH_ROPE_QUERY, nullptr);
+            if (!rc) rc = op_rope(b, m->rope, &kd, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, nullptr);
         }
     } else {
         if (!rc) rc = gh_matmul_batched(b, enc, &s.q, &s.normed, &w[GH_T_ATTN_Q], d, qw, rows);
@@ -339,6 +361,13 @@ int run_steps(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps) {
         m->step_graph = nullptr;
     }
     if (!m->step) {
+        // size the attention partials and merge counters for the split count in force now
+        // (gh_set_attention_splits may have raised it since gh_model_create): nothing may grow
+        // while the capture records
+        const uint32_t splits = attention_splits(b, m->kv.context, m->cfg.kv_head_count, 1);
+        rc = ensure_workspace(b, attention_workspace(1, m->cfg.head_count, splits));
+        if (!rc) rc = ensure_counters(b, m->cfg.kv_head_count);
+        if (rc) return rc;
         gh_encoder* enc = nullptr;
         rc = gh_begin(b, &enc);
         if (rc) return rc;
@@ -364,6 +393,37 @@ int run_steps(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps) {
     m->last_rows = 1;
     m->last_prefill = false;
     return rc;
+}
+
+// The chunks of one gh_model_prefill call (prefill::prefill, encode.rs:16-106) over the
+// prompt ids already on the device: embed, the layers, and the tail on the last chunk's last
+// row.
+int prefill_chunks(gh_model* m, uint32_t n, uint32_t base) {
+    const gh_model_config& c = m->cfg;
+    const uint32_t cap = c.prefill_rows;
+    const uint64_t d = c.embedding_length;
+    for (uint32_t off = 0; off < n; off += cap) {
+        const uint32_t rows = std::min(cap, n - off);
+        gh_encoder* enc = nullptr;
+        int rc = gh_begin(m->b, &enc);
+        if (rc) return rc;
+        rc = latch_rc(enc, op_embed_rows(m->b, &m->pre.x, &m->token_embd, (const void*)(m->prompt.addr + (uint64_t)off * 4),
+                                         rows, c.embedding_length));
+        bool normed = false;
+        for (uint32_t li = 0; li < c.block_count && !rc; ++li)
+            rc = layer(m, enc, m->pre, li, base + off, rows, nullptr, &normed);
+        if (!rc && off + rows == n) {  // the tail belongs to the last chunk's last row
+            gh_buf xr, nr;
+            rc = gh_view(m->b, &m->pre.x, (rows - 1) * d * 4, d * 4, &xr);
+            if (!rc) rc = gh_view(m->b, &m->pre.normed, (rows - 1) * d * 2, d * 2, &nr);
+            if (!rc) rc = tail(m, enc, &xr, &nr);
+        }
+        int rs = gh_submit(m->b, enc);
+        if (rc || rs) return rc ? rc : rs;
+        m->last_rows = rows;
+        m->last_prefill = true;
+    }
+    return GH_OK;
 }
 
 }  // namespace
@@ -472,6 +532,7 @@ int gh_model_load_tensor(gh_model* m, uint32_t layer_index, uint32_t tensor, uin
     if (norm != (format == GH_FMT_F32 || format == GH_FMT_F16))
         return fail(m->b, GH_E_UNSUPPORTED, "model: norms are F32/F16, matrices Q4_K/Q6_K");
     free_w16(m);  // made again from the new weights by the next long prefill
+    m->w16_failed = false;
     if (slot->addr) gh_free_buffer(m->b, slot);
     if (m->step) {
         (void)hipGraphExecDestroy(m->step);
@@ -510,7 +571,6 @@ int gh_model_prefill(gh_model* m, const uint32_t* tokens, uint32_t n, uint32_t b
     for (uint32_t i = 0; i < n; ++i)
         if (tokens[i] >= c.vocab_size) return fail(m->b, GH_E_RANGE, "model: token beyond vocabulary");
     const uint32_t cap = c.prefill_rows;
-    const uint64_t d = c.embedding_length;
     // the chunk's embedding rows in one launch from the token ids on the device (the values
     // of embed per row, encode.rs:16-106, without a launch per token)
     int urc = gh_upload(m->b, &m->prompt, 0, tokens, (uint64_t)n * 4);
@@ -518,28 +578,16 @@ int gh_model_prefill(gh_model* m, const uint32_t* tokens, uint32_t n, uint32_t b
     if (!urc && copies) urc = ensure_w16(m);
     if (urc) return urc;
     set_w16(m, copies);
-    for (uint32_t off = 0; off < n; off += cap) {
-        const uint32_t rows = std::min(cap, n - off);
-        gh_encoder* enc = nullptr;
-        int rc = gh_begin(m->b, &enc);
-        if (rc) return rc;
-        rc = latch_rc(enc, op_embed_rows(m->b, &m->pre.x, &m->token_embd, (const void*)(m->prompt.addr + (uint64_t)off * 4),
-                                         rows, c.embedding_length));
-        bool normed = false;
-        for (uint32_t li = 0; li < c.block_count && !rc; ++li)
-            rc = layer(m, enc, m->pre, li, base + off, rows, nullptr, &normed);
-        if (!rc && off + rows == n) {  // the tail belongs to the last chunk's last row
-            gh_buf xr, nr;
-            rc = gh_view(m->b, &m->pre.x, (rows - 1) * d * 4, d * 4, &xr);
-            if (!rc) rc = gh_view(m->b, &m->pre.normed, (rows - 1) * d * 2, d * 2, &nr);
-            if (!rc) rc = tail(m, enc, &xr, &nr);
-        }
-        int rs = gh_submit(m->b, enc);
-        if (rc || rs) return rc ? rc : rs;
-        m->last_rows = rows;
-        m->last_prefill = true;
+    int rc = prefill_chunks(m, n, base);
+    if (rc == GH_E_OOM && copies && !m->w16.empty()) {
+        // the copies crowded out this prefill's workspace: drop them for good and run the
+        // prompt again dequantizing (every chunk rewrites the same cache rows)
+        free_w16(m);
+        m->w16_failed = true;
+        m->b->err.clear();
+        rc = prefill_chunks(m, n, base);
     }
-    return GH_OK;
+    return rc;
 }
 
 int gh_model_read_logits(gh_model* m, float* dst) {

@@ -589,41 +589,11 @@ GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce(GhGemmArgs a) {
     }
 }
 
-// Split-K sum with RoPE (rope_yarn, rope.rs:14-39) for a query or key projection: one thread per
-// adjacent output pair (2p, 2p + 1) of a head; each value's partials are summed in split order
-// and rounded to FP16 (gh_gemm_reduce), then rotated and post-scaled exactly as gh_rope does
-// (pairs at or past rope_dim / 2 are stored unrotated). Token t sits at position base + t.
-GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce_rope(GhGemmArgs a) {
-#pragma clang fp contract(off)
-    const uint64_t total = (uint64_t)a.n * a.rows, npairs = total / 2;
-    const uint64_t groups = min((npairs + 255) / 256, (uint64_t)4096);
-    for (uint64_t k = (uint64_t)blockIdx.x * 256 + threadIdx.x; k < npairs; k += groups * 256) {
-        const uint64_t i = 2 * k;
-        float s0 = 0.0f, s1 = 0.0f;
-        for (uint32_t z = 0; z < a.splits; ++z) {
-            const float2 p = gh_gp<float2>(a.part)[(z * total + i) / 2];
-            s0 += p.x;
-            s1 += p.y;
-        }
-        const uint32_t t = (uint32_t)(i / a.rows), col = (uint32_t)(i % a.rows);
-        const uint32_t pair = (col % a.head_dim) / 2;
-        uint32_t h0 = gh_f2h(s0), h1 = gh_f2h(s1);
-        if (pair < a.pairs) {
-            const uint32_t pos = a.base + t;
-            const float2 cs = gh_gp<float2>(a.table)[(uint64_t)pos * a.pairs + pair];
-            const float scale = a.post ? gh_gp<float>(a.post)[pos] : 1.0f;
-            const float x0 = gh_h2f(h0), x1 = gh_h2f(h1);
-            h0 = gh_f2h((x0 * cs.x - x1 * cs.y) * scale);
-            h1 = gh_f2h((x0 * cs.y + x1 * cs.x) * scale);
-        }
-        gh_gpw<uint32_t>(a.out)[k] = h0 | (h1 << 16);
-    }
-}
-
 // Split-K sum of a multi-matrix launch (partials [splits][n][Σ rows]): one thread per adjacent
 // column pair, summed in split order and rounded to FP16 as gh_gemm_reduce does, then, for a
-// matrix with a RoPE role, rotated as gh_gemm_reduce_rope does; written to the matrix's own
-// output [n][rows].
+// matrix with a RoPE role, rotated and post-scaled exactly as gh_rope does (rope_yarn,
+// rope.rs:14-39; pairs at or past rope_dim / 2 stored unrotated, the post-scale on the query
+// role only); written to the matrix's own output [n][rows]. Token t sits at position base + t.
 GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce_seg(GhGemmArgs a) {
 #pragma clang fp contract(off)
     const uint64_t total = (uint64_t)a.n * a.rows, npairs = total / 2;

@@ -118,9 +118,9 @@ struct GhGemmArgs {
     uint64_t normed;  // gh_gemm_tail: FP16 normalized rows [n][rows]
     uint32_t epi;     // GH_GEMM_EPI_*
     float eps;        // gh_gemm_tail
-    uint64_t table;   // gh_gemm_reduce_rope: float2 (cos, sin) [positions][pairs]
-    uint64_t post;    // gh_gemm_reduce_rope: f32 post-scale [positions] (0: 1.0, keys)
-    uint32_t base;    // gh_gemm_reduce_rope: position of token 0
+    uint64_t table;   // gh_gemm_reduce_seg: float2 (cos, sin) [positions][pairs]
+    uint64_t post;    // gh_gemm_reduce_seg: f32 query post-scale [positions]
+    uint32_t base;    // gh_gemm_reduce_seg: position of token 0
     uint32_t head_dim;
     uint32_t pairs;   // rope_dim / 2 (pairs rotated per head)
     uint32_t nseg;    // > 0: gh_gemm3_mixed_* / gh_gemm_reduce_seg over seg[] (rows = Σ rows)

@@ -106,10 +106,11 @@ const char* gh_last_error(const gh_backend* b);
 int gh_alloc_buffer(gh_backend* b, uint64_t bytes, gh_buf* out);
 /* free_buffer, contract.rs:30 (views are rejected with GH_E_INVALID, contract.rs:38-40) */
 int gh_free_buffer(gh_backend* b, gh_buf* buf);
-/* view, contract.rs:48: alias of [offset, offset+len) of `buf`, no allocation, no copy */
+/* view, contract.rs:48: alias of [offset, offset+len) of `buf`, no allocation, no copy;
+ * offset_bytes must be a multiple of gh_min_buffer_offset_alignment (GH_E_INVALID otherwise) */
 int gh_view(gh_backend* b, const gh_buf* buf, uint64_t offset_bytes, uint64_t len_bytes,
             gh_buf* out);
-/* min_buffer_offset_alignment, contract.rs:56 */
+/* min_buffer_offset_alignment, contract.rs:56: 16 (rows are read with 16-byte loads) */
 uint64_t gh_min_buffer_offset_alignment(const gh_backend* b);
 /* host<->device copies (the CPU backend's buffer read/write; vulkan/mem/buffers.rs staging);
  * synchronous with respect to the backend stream */
@@ -210,6 +211,13 @@ int gh_synchronize(gh_backend* b);
  * chunk); 0 restores the backend's policy (about two workgroups per CU). At most 32. Graphs
  * recorded before the call are re-recorded on their next use. */
 int gh_set_attention_splits(gh_backend* b, uint32_t splits);
+
+/* The backend's growable device scratch (no counterpart in the reference: a diagnostic for
+ * tests): workspace bytes (split-K and attention partials, argmax partials), attention-merge
+ * counter slots, and a generation number bumped whenever either is reallocated or a recorded
+ * graph must be re-recorded. Any argument may be NULL. */
+int gh_scratch_info(const gh_backend* b, uint64_t* workspace_bytes, uint64_t* counter_slots,
+                    uint64_t* generation);
 
 /* =====================================================================================
  * Graph driver: a C++ restatement of the caller side of the boundary — MistralGraph's pinned

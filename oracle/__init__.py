@@ -33,6 +33,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgh_oracle.so")
 
 FMT_F32, FMT_F16, FMT_Q4_K, FMT_Q6_K = 0, 1, 12, 14
+PLANT_NONE, PLANT_POST_SCALE_ON_K, PLANT_NO_POST_SCALE_ON_Q = 0, 1, 2
 LAYER_TENSORS = 9
 
 
@@ -102,6 +103,7 @@ _SIG = {
     "gho_model_set_trace": (None, [P, I32]),
     "gho_model_load_kv": (I32, [P, P, P, U32, U32]),
     "gho_model_trace": (C.c_char_p, [P]),
+    "gho_model_set_plant": (I32, [P, I32]),
 }
 
 _lib = None
@@ -272,6 +274,10 @@ class Model:
 
     def set_trace(self, on: bool):
         lib().gho_model_set_trace(self.h, 1 if on else 0)
+
+    def set_plant(self, plant: int):
+        """Plant a known mistake (PLANT_*) to show that a parity check fails on it."""
+        assert lib().gho_model_set_plant(self.h, plant) == 0
 
     def trace(self) -> list:
         return lib().gho_model_trace(self.h).decode().split("\n")[:-1]

@@ -169,6 +169,11 @@ int gho_model_load_kv(gho_model* m, const uint16_t* k, const uint16_t* v, uint32
  * op, the tensor's name (l<i>.q, output_norm, logits:output, ...) when the op takes one */
 void gho_model_set_trace(gho_model* m, int on);
 const char* gho_model_trace(gho_model* m); /* newline-separated, valid until the next call */
+/* A planted mistake for tests that show a parity check can fail (never set otherwise):
+ * GHO_PLANT_NONE, or the YaRN post-scale (rope.rs:91-100) applied to K as well as Q, or
+ * dropped from Q. Only the per-row RoPE roles of layer_rows change. */
+enum { GHO_PLANT_NONE = 0, GHO_PLANT_POST_SCALE_ON_K = 1, GHO_PLANT_NO_POST_SCALE_ON_Q = 2 };
+int gho_model_set_plant(gho_model* m, int plant);
 
 #ifdef __cplusplus
 }

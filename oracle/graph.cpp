@@ -26,6 +26,7 @@ struct gho_model {
     std::vector<std::string> trace;
     std::map<const void*, std::string> names;
     std::string joined;
+    int plant = GHO_PLANT_NONE;  // a planted mistake (tests of the checks' power only)
 };
 
 namespace {
@@ -73,9 +74,13 @@ void layer_rows(gho_model* m, size_t li, size_t base, size_t rows, std::vector<f
     // rope_yarn_batched default (contract.rs:187-246): per row, Q then K at base + row.
     rec(m, rows == 1 ? "rope_q" : "rope_batched");
     if (rows == 1) rec(m, "rope_k");
+    // the role only selects the post-scale (rope.rs:84-100), so a planted role swap is
+    // exactly a post-scale mistake
+    const int q_role = m->plant == GHO_PLANT_NO_POST_SCALE_ON_Q ? 1 : 0;
+    const int k_role = m->plant == GHO_PLANT_POST_SCALE_ON_K ? 0 : 1;
     for (size_t r = 0; r < rows; ++r) {
-        gho_rope_yarn(q.data() + r * qw, c.head_count, c.key_length, base + r, &c.yarn, 0);
-        gho_rope_yarn(k.data() + r * kw, c.kv_head_count, c.key_length, base + r, &c.yarn, 1);
+        gho_rope_yarn(q.data() + r * qw, c.head_count, c.key_length, base + r, &c.yarn, q_role);
+        gho_rope_yarn(k.data() + r * kw, c.kv_head_count, c.key_length, base + r, &c.yarn, k_role);
     }
     rec(m, "kv_write");
     kv_append(m, li, base, k.data(), v.data(), rows);
@@ -215,6 +220,12 @@ int gho_model_load_kv(gho_model* m, const uint16_t* k, const uint16_t* v, uint32
 void gho_model_set_trace(gho_model* m, int on) {
     m->tracing = on != 0;
     m->trace.clear();
+}
+
+int gho_model_set_plant(gho_model* m, int plant) {
+    if (plant < GHO_PLANT_NONE || plant > GHO_PLANT_NO_POST_SCALE_ON_Q) return -1;
+    m->plant = plant;
+    return 0;
 }
 
 const char* gho_model_trace(gho_model* m) {

@@ -6,13 +6,15 @@ with a 512-token random-id prompt and 256 greedy decode steps through the replay
 The CPU oracle cannot prefill 512 tokens through 40 blocks within a test (about 12 s per
 block), so it resumes from the device's prefilled KV cache: seeded with the device's K/V of
 positions < p, it recomputes position p through all 40 blocks itself — the prompt's last row
-(its logits and its K/V entries against the device prefill's) and 16 decode steps
-teacher-forced on the device's greedy tokens (>= 99 % top-1 agreement, near-ties excepted).
+(its logits and its K/V entries against the device prefill's) and 64 decode steps
+teacher-forced on the device's greedy tokens (>= 99 % top-1 agreement; near ties, counted and
+printed, excepted).
 """
 import numpy as np
 import pytest
 
 import oracle as O
+from agreement import assert_agreement
 from graph_horizon_amd import HipModel, synth
 from graph_horizon_amd import _ffi as F
 from test_oracle import oracle_model
@@ -20,6 +22,7 @@ from test_oracle import oracle_model
 pytestmark = pytest.mark.gpu
 
 PROMPT, STEPS, CTX = 512, 256, 1024
+ORACLE_STEPS = 64
 
 
 def _close(got, want, what, rel=2e-2):
@@ -74,22 +77,19 @@ def test_c5_14b_prompt_512_greedy_256(hip):
     om.load_kv(k_dev, v_dev, CTX, PROMPT - 1)
     om.token(prompt[-1], PROMPT - 1)
     _close(prefill_logits, om.logits(), "prompt's last row vs oracle")
-    assert int(np.argmax(om.logits())) == first or \
-        np.sort(om.logits())[-1] - np.sort(om.logits())[-2] < 1e-3 * max(abs(om.logits().max()), 1.0)
+    ora = [om.logits()]
     # the row's K and V in every layer (K after RoPE), within the FP16 model tolerance
     kv_row = shape.kv_head_count * shape.head_dim
     for role, dev in ((0, k_dev), (1, v_dev)):
         ora = O.f32(om.kv(role)).reshape(shape.block_count, CTX, kv_row)[:, PROMPT - 1]
         got = O.f32(dev).reshape(shape.block_count, CTX, kv_row)[:, PROMPT - 1]
         _close(got, ora, f"KV role {role} at position {PROMPT - 1}")
-    # 16 decode steps teacher-forced on the device's tokens
-    agree, tok, steps = 0, first, 16
-    for i in range(steps):
+    # 64 decode steps teacher-forced on the device's tokens
+    tok = first
+    for i in range(ORACLE_STEPS):
         om.token(tok, PROMPT + i)
-        lg = om.logits()
-        s = np.sort(lg)
-        if int(toks[i]) == int(np.argmax(lg)) or s[-1] - s[-2] < 1e-3 * max(abs(s[-1]), 1.0):
-            agree += 1
+        ora.append(om.logits())
         tok = int(toks[i])
-    assert agree >= 0.99 * steps, agree
     om.close()
+    assert_agreement([first] + [int(t) for t in toks[:ORACLE_STEPS]], ora,
+                     f"C5 14B, prompt row and {ORACLE_STEPS} greedy steps")

@@ -14,6 +14,7 @@ import pytest
 import oracle as O
 from graph_horizon_amd import GhError, Yarn, synth
 from graph_horizon_amd import _ffi as F
+from agreement import assert_agreement
 
 pytestmark = pytest.mark.gpu
 
@@ -282,8 +283,26 @@ def test_kv_write_bytes(hip):
     assert np.array_equal(gk, wk) and np.array_equal(gv, wv)
     with pytest.raises(GhError):  # past the end of the cache
         hip.kv_write(kv, kb, vb, kc.nbytes - 2, 0, rows * kvh)
+    with pytest.raises(GhError):  # an offset whose sum with the length wraps around 2^64
+        hip.kv_write(kv, kb, vb, 2**64 - 2, 0, rows * kvh)
+    with pytest.raises(GhError):
+        hip.kv_write(kv, kb, vb, 0, 2**64 - 1024, rows * kvh)
     for b in (kb, vb, kv.k, kv.v):
         hip.free_buffer(b)
+
+
+def test_view_alignment(hip):
+    """min_buffer_offset_alignment (contract.rs:56) is 16, and views at other offsets are
+    rejected (the kernels read rows with 16-byte loads)."""
+    assert hip.min_buffer_offset_alignment() == 16
+    b = hip.alloc_buffer(4096)
+    assert hip.view(b, 32, 64).addr == b.addr + 32
+    for off in (2, 4, 8, 24):
+        with pytest.raises(GhError):
+            hip.view(b, off, 64)
+    with pytest.raises(GhError):
+        hip.view(b, 4096 - 16, 32)  # beyond the buffer
+    hip.free_buffer(b)
 
 
 # ---------------------------------------------------------------- attention
@@ -395,13 +414,15 @@ def _models(hip, shape_name, seed, kv_context, prefill_rows=64):
 def test_model_decode_tokens_match_oracle(hip):
     gm, om = _models(hip, "tiny", 31, 128)
     toks = [1, 500, 2047, 33, 900, 12, 7, 1999]
+    dev, ora = [], []
     for p, t in enumerate(toks):
         gm.token(t, p)
         om.token(t, p)
         got, want = gm.read_logits(), om.logits()
         assert np.allclose(got, want, rtol=2e-2, atol=2e-2), p
-        assert gm.read_argmax() == int(np.argmax(want)) or \
-            np.sort(want)[-1] - np.sort(want)[-2] < 1e-2
+        dev.append(gm.read_argmax())
+        ora.append(want)
+    assert_agreement(dev, ora, "tiny decode", min_frac=1.0)
     gm.close()
     om.close()
 
@@ -447,16 +468,12 @@ def test_greedy_decode_graph_replay_teacher_forced(hip):
     first = int(np.argmax(om.logits()))
     steps = 64
     toks = gm.decode_greedy(first, len(prompt), steps)
-    agree = 0
-    tok = first
+    tok, ora = first, []
     for i in range(steps):
         om.token(tok, len(prompt) + i)
-        l = om.logits()
-        s = np.sort(l)
-        if int(toks[i]) == int(np.argmax(l)) or s[-1] - s[-2] < 1e-3:
-            agree += 1
+        ora.append(om.logits())
         tok = int(toks[i])
-    assert agree >= 0.99 * steps, agree
+    assert_agreement(toks, ora, "tiny 64-step greedy")
     # replaying the graph from the same state reproduces the host-driven path
     gm.prefill(prompt, 0)
     again = gm.decode_greedy(first, len(prompt), 8)

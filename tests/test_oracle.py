@@ -593,3 +593,33 @@ def test_graph_closed_form_one_layer(ora, variant, tied):
             bad = CF.logits(ts, variant, token, plant=plant)
             assert CF.error(bad, want) > 5 * CF.TOL, (plant, CF.error(bad, want))
     om.close()
+
+
+# ---------------------------------------------------------------- long context (YaRN post-scale)
+@pytest.mark.parametrize("scenario", __import__("yarn_long").SCENARIOS,
+                         ids=lambda s: f"n{s[0]}-base{s[1]}")
+def test_long_context_checks_catch_post_scale_mistakes(ora, scenario):
+    """The long-context GPU parity test compares logits within yarn_long.LOGIT_TOL of the
+    oracle across position 16384. Planted in the oracle, a post-scale applied to K as well, or
+    dropped from Q (rope.rs:91-100), moves the teacher-forced logits of each scenario by more
+    than three times that bar, and the first mistake also scales block 0's cached K rows of
+    positions >= 16384 (whose input is the embedding alone) by the post-scale itself,
+    1 + 0.1 ln 2, while leaving every row below 16384 untouched."""
+    import yarn_long as Y
+
+    shape = synth.SHAPES["tiny"]
+    ts = Y.tensors(shape)
+    n, base, steps = scenario
+    first, logits, kc, _, fed = Y.oracle_run(shape, ts, scenario)
+    for plant in (O.PLANT_POST_SCALE_ON_K, O.PLANT_NO_POST_SCALE_ON_Q):
+        pf, pl, pk, _, _ = Y.oracle_run(shape, ts, scenario, forced=fed, plant=plant)
+        err = max(Y.logit_err(a, b) for a, b in zip([pf] + pl, [first] + logits))
+        assert err > 3 * Y.LOGIT_TOL, (plant, err)
+        if plant == O.PLANT_POST_SCALE_ON_K:
+            kvw = shape.kv_head_count * shape.head_dim
+            a = O.f32(pk).reshape(shape.block_count, Y.CTX, kvw)
+            b = O.f32(kc).reshape(shape.block_count, Y.CTX, kvw)
+            last = base + n + steps
+            assert np.array_equal(a[:, :16384], b[:, :16384])
+            ratio = np.abs(a[0, 16384:last]).sum() / np.abs(b[0, 16384:last]).sum()
+            assert abs(ratio - (1 + 0.1 * math.log(2))) < 2e-3, ratio

@@ -68,3 +68,32 @@ def test_noalloc_rejects_launches_beyond_its_scratch(hip):
         hip.set_attention_splits(0)
     for b in (qb, kv.k, kv.v):
         hip.free_buffer(b)
+
+
+def test_noalloc_grows_no_backend_scratch():
+    """The entry point's whole scratch is its fixed array: on a fresh backend (no attention
+    has run, so it holds no merge counters yet) two no-allocation calls at 32 splits leave the
+    backend's workspace, counter slots and generation exactly as they were. The allocating
+    entry point then creates the counters, so the check does see an allocation when one
+    happens."""
+    from graph_horizon_amd import HipBackend
+
+    rng = np.random.default_rng(9)
+    with HipBackend(0) as fresh:
+        fresh.set_attention_splits(32)
+        before = fresh.scratch_info()
+        assert before[1] == 0, before
+        outs = []
+        for q_heads, kv_heads, ctx, pos in ((32, 8, 4096, 4095), (8, 8, 512, 100)):
+            kv = _kv(fresh, 1, ctx, kv_heads, rng)
+            qb = fresh.from_host(O.f16(rng.standard_normal(q_heads * 128).astype(np.float32)))
+            outs.append((kv, qb, q_heads, pos,
+                         _decode(fresh, "gh_attention_decode_noalloc", kv, q_heads, pos, 0, qb)))
+        assert fresh.scratch_info() == before
+        for kv, qb, q_heads, pos, got in outs:
+            want = _decode(fresh, "gh_attention_decode", kv, q_heads, pos, 0, qb)
+            assert np.array_equal(got, want)
+        assert fresh.scratch_info()[1] > 0
+        for kv, qb, *_ in outs:
+            for b in (qb, kv.k, kv.v):
+                fresh.free_buffer(b)
