@@ -81,9 +81,9 @@ def test_c5_14b_prompt_512_greedy_256(hip):
     # the row's K and V in every layer (K after RoPE), within the FP16 model tolerance
     kv_row = shape.kv_head_count * shape.head_dim
     for role, dev in ((0, k_dev), (1, v_dev)):
-        ora = O.f32(om.kv(role)).reshape(shape.block_count, CTX, kv_row)[:, PROMPT - 1]
+        want = O.f32(om.kv(role)).reshape(shape.block_count, CTX, kv_row)[:, PROMPT - 1]
         got = O.f32(dev).reshape(shape.block_count, CTX, kv_row)[:, PROMPT - 1]
-        _close(got, ora, f"KV role {role} at position {PROMPT - 1}")
+        _close(got, want, f"KV role {role} at position {PROMPT - 1}")
     # 64 decode steps teacher-forced on the device's tokens
     tok = first
     for i in range(ORACLE_STEPS):

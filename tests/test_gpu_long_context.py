@@ -46,9 +46,14 @@ def _cache(hip, kv, shape, ctx):
 def _kv_close(got, want, lo, hi, what):
     g = O.f32(got[:, lo:hi]).astype(np.float64)
     w = O.f32(want.reshape(got.shape)[:, lo:hi]).astype(np.float64)
+    # the projections sum in another order than the oracle's AVX2 loops, so many values round
+    # to a neighbouring FP16 (a third of the K values of the tiny model's small-scale Q/K
+    # weights, whose sums cancel heavily); a post-scale on K would move every row past 16384
+    # by 7 %, tens of times both bounds
     err = np.abs(g - w)
-    assert err.max() <= 4e-3 * max(np.abs(w).max(), 1.0), (what, float(err.max()))
-    assert np.mean(err > 0) < 2e-2, (what, float(np.mean(err > 0)))
+    scale = max(np.abs(w).max(), 1.0)
+    assert err.max() <= 4e-3 * scale, (what, float(err.max()), scale)
+    assert err.mean() <= 5e-4 * scale, (what, float(err.mean()), scale)
 
 
 @pytest.mark.parametrize("scenario", Y.SCENARIOS, ids=lambda s: f"n{s[0]}-base{s[1]}")

@@ -27,7 +27,7 @@ CTX = 16512
 QK_DIV = 8.0
 K_STD, V_STD = 1.5, 4.0
 SEED = 61
-LOGIT_TOL = 1e-2  # max |diff| of the logits, relative to the largest |logit| (at least 1)
+LOGIT_TOL = 1.5e-2  # max |diff| of the logits, relative to the largest |logit| (at least 1)
 
 # (prefill rows, base position, decode steps after it): the prefill crosses 16384 with a
 # 128-token-tile chunk (40 rows) and with a 256-token-tile chunk over the FP16 weight copies
