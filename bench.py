@@ -41,6 +41,11 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 # the same counter's reading for a 256 MiB device-to-device copy (profiles/q4k_gemv_c1_4096x4096.txt).
 # Re-measure whenever the kernel changes.
 ROOFLINE_TRAFFIC_BYTES = 9596715
+# Mean traced duration of the same kernel under `rocprofv3 --kernel-trace --stats -- python3
+# bench.py --roofline-only` (profiles/q4k_gemv_c1_4096x4096.txt); the tracer's timestamps add
+# 0.2-0.6 us per dispatch against the untraced back-to-back period that `achieved` uses
+# (profiles/stream_probe_floor_9mb_94mb.txt). Re-measure whenever the kernel changes.
+ROOFLINE_TRACED_US = 4.667
 
 
 def log(*a):
@@ -69,8 +74,10 @@ def cpu_model():
 
 def cpu_baseline(shape, tensors, kv, kv_context, prompt_len, first, seconds):
     """The oracle on every core of the affinity set: greedy decode steps of the bench's 8B model
-    resumed from the GPU's KV cache of the prompt (positions < prompt_len), for about `seconds`;
-    then the C1 GEMV over distinct Q/O weights and C4 decode attention at ctx 4096 / 32768."""
+    resumed from the GPU's KV cache of the prompt (positions < prompt_len), for about `seconds`
+    (the oracle's own cache has room for 1024 steps past the prompt); then the C1 GEMV over
+    distinct Q/O weights and C4 decode attention at ctx 4096 / 32768. Every figure is the
+    median of the timed calls."""
     import oracle as O
     from graph_horizon_amd import synth
     from graph_horizon_amd import _ffi as F
@@ -83,16 +90,19 @@ def cpu_baseline(shape, tensors, kv, kv_context, prompt_len, first, seconds):
     cfg = O.ModelCfg(shape.block_count, max(kv_context, 32768), shape.embedding_length,
                      shape.feed_forward_length, shape.head_count, shape.kv_head_count,
                      shape.head_dim, shape.head_dim, shape.vocab_size, 1e-5, O.Yarn(**y))
-    om = O.Model(cfg, table, kv_context)
+    cpu_ctx = prompt_len + 1024
+    om = O.Model(cfg, table, cpu_ctx)
     om.load_kv(kv[0], kv[1], kv_context, prompt_len)
-    tok, pos, steps = first, prompt_len, 0
+    tok, pos, times = first, prompt_len, []
     t0 = time.perf_counter()
-    while (steps < 4 or time.perf_counter() - t0 < seconds) and pos < kv_context:
+    while (len(times) < 4 or time.perf_counter() - t0 < seconds) and pos < cpu_ctx:
+        ts = time.perf_counter()
         om.token(tok, pos)
         tok = int(np.argmax(om.logits()))
+        times.append(time.perf_counter() - ts)
         pos += 1
-        steps += 1
-    dt = (time.perf_counter() - t0) / steps
+    steps = len(times)
+    dt = float(np.median(times))
     om.close()
     _, per_token = weight_bytes(shape)
     # C1: Q4_K 4096x4096 GEMV over the model's distinct Q and O weights (FP32 out, logits)
@@ -101,11 +111,12 @@ def cpu_baseline(shape, tensors, kv, kv_context, prompt_len, first, seconds):
           if layer != F.NO_LAYER and tid in (F.T_ATTN_Q, F.T_ATTN_OUTPUT)]
     rng = np.random.default_rng(3)
     x16 = O.f16(rng.standard_normal(d).astype(np.float32))
-    n, t1 = 0, time.perf_counter()
-    while n < len(ws) or time.perf_counter() - t1 < 2.0:
-        O.logits(F.FMT_Q4_K, x16, ws[n % len(ws)], d, d)
-        n += 1
-    c1_s = (time.perf_counter() - t1) / n
+    c1_times, t1 = [], time.perf_counter()
+    while len(c1_times) < len(ws) or time.perf_counter() - t1 < 2.0:
+        ts = time.perf_counter()
+        O.logits(F.FMT_Q4_K, x16, ws[len(c1_times) % len(ws)], d, d)
+        c1_times.append(time.perf_counter() - ts)
+    c1_s = float(np.median(c1_times))
     c1_bytes = d * (d // 256) * 144 + d * 2 + d * 4
     # C4: decode attention, 32 q / 8 kv heads x 128, f16 KV N(0,1), pos = ctx - 1
     attn = {}
@@ -113,24 +124,25 @@ def cpu_baseline(shape, tensors, kv, kv_context, prompt_len, first, seconds):
         kc = O.f16(rng.standard_normal(ctx * 8 * 128).astype(np.float32))
         vc = O.f16(rng.standard_normal(ctx * 8 * 128).astype(np.float32))
         q = O.f16(rng.standard_normal(32 * 128).astype(np.float32))
-        n, t2 = 0, time.perf_counter()
-        while n < 3 or time.perf_counter() - t2 < 1.0:
+        at, t2 = [], time.perf_counter()
+        while len(at) < 3 or time.perf_counter() - t2 < 1.0:
+            ts = time.perf_counter()
             O.attention_decode(q, kc, vc, 128, 8, 32, ctx - 1, 0, ctx)
-            n += 1
-        us = (time.perf_counter() - t2) / n * 1e6
-        attn[f"decode_{ctx}"] = {"avg_us": round(us, 1),
+            at.append(time.perf_counter() - ts)
+        us = float(np.median(at)) * 1e6
+        attn[f"decode_{ctx}"] = {"median_us": round(us, 1), "calls": len(at),
                                  "gbps": round(2 * ctx * 8 * 128 * 2 / (us * 1e-6) / 1e9, 2)}
     model = cpu_model()
     log(f"bench: CPU baseline: {cores} threads ({model}): {1 / dt:.2f} tok/s, C1 "
-        f"{c1_bytes / c1_s / 1e9:.1f} GB/s, attention ctx 4096 {attn['decode_4096']['avg_us']:.0f} us")
+        f"{c1_bytes / c1_s / 1e9:.1f} GB/s, attention ctx 4096 {attn['decode_4096']['median_us']:.0f} us")
     return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
             "sample": f"{steps} greedy decode steps of the bench's 8B-shaped model (34 blocks with "
                       f"attention, output GEMV and argmax) at context {prompt_len}..{pos - 1}, "
-                      f"resumed from the GPU's prompt KV cache: {dt * 1e3:.1f} ms/token "
-                      f"({per_token / dt / 1e9:.1f} GB/s of weights); {cores} threads "
-                      f"(nproc of the affinity set), {model}",
-            "q4k_gemv_c1": {"avg_us": round(c1_s * 1e6, 1), "gbps": round(c1_bytes / c1_s / 1e9, 2),
-                            "launches": n},
+                      f"resumed from the GPU's prompt KV cache, {sum(times):.1f} s in all: median "
+                      f"{dt * 1e3:.1f} ms/token ({per_token / dt / 1e9:.1f} GB/s of weights); "
+                      f"{cores} threads (nproc of the affinity set), {model}",
+            "q4k_gemv_c1": {"median_us": round(c1_s * 1e6, 1), "gbps": round(c1_bytes / c1_s / 1e9, 2),
+                            "calls": len(c1_times)},
             "attention_c4": attn,
             "label": "C++ restatement of the graph_horizon CPU reference (AVX2 kernels)"}
 
@@ -158,6 +170,15 @@ def main():
     ap.add_argument("--attn-probe", action="store_true",
                     help="only the C4 attention cases (bench.py c4_attention), for rocprofv3 "
                          "--pmc passes")
+    ap.add_argument("--floor-probe", action="store_true",
+                    help="only plain streaming reads (gh_stream_probe) of --probe-bytes with "
+                         "--probe-groups workgroups and the C1 GEMV, back to back over distinct "
+                         "memory: the floor of one launch of each size, and (under rocprofv3 "
+                         "--kernel-trace) the tracer's per-dispatch cost")
+    ap.add_argument("--probe-bytes", default="9437184,94371840",
+                    help="comma-separated read sizes for --floor-probe")
+    ap.add_argument("--probe-groups", default="256,512,1024,2048",
+                    help="comma-separated workgroup counts for --floor-probe")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -172,6 +193,10 @@ def main():
         return
     if args.gemm_probe:
         gemm_probe(synth.SHAPES["8b"])
+        return
+    if args.floor_probe:
+        floor_probe([int(v) for v in args.probe_bytes.split(",")],
+                    [int(v) for v in args.probe_groups.split(",")])
         return
     if args.attn_probe:
         hip = HipBackend(0)
@@ -329,11 +354,15 @@ def c1_roofline(hip, model, shape):
             "kernel": f"gh_gemv_q4k_r2_d (Q4_K GEMV {d}x{d}, BASELINE configs[0], x ~ N(0,1); "
                       f"{nbytes} algorithmic B/launch: weights {d * (d // 256) * 144} + x + y)",
             "avg_us": round(period, 3), "single_launch_us": round(single, 3),
+            "traced_avg_us": ROOFLINE_TRACED_US,
+            "traced_frac": round(nbytes / (ROOFLINE_TRACED_US * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
             "launches": 3 * len(ws), "distinct_weights": len(ws),
             "timing": "avg_us: HIP events on the backend stream around back-to-back launches "
                       "(launch gaps included), per launch; single_launch_us: one launch on an "
                       "idle GPU between its own event pair (dispatch ramp and event markers "
-                      "included)"}
+                      "included); traced_avg_us: the kernel trace's mean per-dispatch duration "
+                      "of the same command (profiles/q4k_gemv_c1_4096x4096.txt), which the "
+                      "tracer's timestamps lengthen"}
 
 
 def gemv_gate_shape(hip, model, shape):
@@ -389,6 +418,62 @@ def traffic_probe(shape):
     hip.close()
 
 
+def floor_probe(sizes, groups, launches=240):
+    """Back-to-back plain streaming reads (gh_stream_probe) of each size over distinct offsets
+    of a 1 GiB buffer (so the 256 MB MALL cannot serve them), for each workgroup count, then the
+    C1 GEMV (gh_gemv_q4k_r2_d, 4096x4096) over 64 distinct random weights (604 MB). Prints the
+    HIP-event period per launch of each case (launch gaps included): the untraced figures that
+    a kernel trace of the same command is compared with."""
+    import ctypes as C
+
+    from graph_horizon_amd import HipBackend, synth
+
+    hip = HipBackend(0)
+    lib = hip.lib
+    span = 1 << 30
+    src, sink = hip.alloc_buffer(span), hip.alloc_buffer(4096)
+    out = {"stream": []}
+    for nbytes in sizes:
+        stride = (nbytes + 4095) // 4096 * 4096
+        slots = max(4, (span - nbytes) // stride + 1)
+        for g in groups:
+            enc = hip.begin()
+            for i in range(8):
+                lib.gh_stream_probe(hip.h, enc, C.byref(src), (i % slots) * stride, nbytes, C.byref(sink), g)
+            hip.submit()
+            enc = hip.begin()
+            hip.timer_start()
+            for i in range(launches):
+                rc = lib.gh_stream_probe(hip.h, enc, C.byref(src), (i % slots) * stride, nbytes,
+                                         C.byref(sink), g)
+                assert rc == 0, rc
+            us = hip.timer_stop() * 1e3 / launches
+            hip.submit()
+            gbps = nbytes / (us * 1e-6) / 1e9
+            out["stream"].append({"bytes": nbytes, "workgroups": g, "period_us": round(us, 3),
+                                  "gbps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)})
+            log(f"bench: stream probe {nbytes} B, {g} workgroups: {us:.3f} us per launch back to "
+                f"back ({gbps:.0f} GB/s, {gbps / HBM_PEAK_GBPS:.1%}), {slots} distinct offsets")
+    hip.free_buffer(src)
+    d = 4096
+    rng = np.random.default_rng(5)
+    ws = [hip.load_weight(12, synth.quant_blocks(rng, 12, d, d, 0.02), d, d) for _ in range(64)]
+    x = hip.from_host(synth.f16_bits(rng.standard_normal(d)))
+    y = hip.alloc_buffer(d * 2)
+    period, _ = time_gemv(hip, ws, x, y, d, d, reps=4)
+    nbytes = d * (d // 256) * 144 + d * 2 + d * 2
+    gbps = nbytes / (period * 1e-6) / 1e9
+    out["c1_gemv"] = {"kernel": "gh_gemv_q4k_r2_d", "bytes": nbytes, "period_us": round(period, 3),
+                      "gbps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4),
+                      "launches": 4 * len(ws)}
+    log(f"bench: C1 GEMV 4096x4096 over 64 distinct weights: {period:.3f} us per launch back to "
+        f"back ({gbps:.0f} GB/s, {gbps / HBM_PEAK_GBPS:.1%})")
+    print(json.dumps({"floor_probe": out}), flush=True)
+    for b in ws + [x, y, sink]:
+        hip.free_buffer(b)
+    hip.close()
+
+
 def gemm_probe(shape, n=512):
     """The C3 prefill GEMMs alone: gate/up (Q4_K d -> FFN) then down (Q6_K FFN -> d) over 8
     random weights each, 4 passes, nothing else (for PMC passes)."""
@@ -439,13 +524,14 @@ def prefill_long(hip, HipModel, shape, tensors, n):
 
 def prefill_gemm(hip, model, shape, tensors, n):
     """the n-token prefill GEMMs (gate/up Q4_K d->FFN, down Q6_K FFN->d) on
-    the matrix cores, over 8 distinct layers' weights, timed with HIP events. Two forms with the
-    same output bits: the model's own weights, whose FP16 copies its prefill made and its GEMMs
-    read (the prefill's path), and the same weights loaded again without copies, which the
-    GEMMs dequantize tile by tile ("dequantizing")."""
+    the matrix cores, over 8 distinct layers' weights, timed with HIP events. The top-level
+    figures are the C3 workload itself: Q4_K/Q6_K weights loaded without FP16 copies, which the
+    GEMMs dequantize tile by tile. Beside them, the same GEMMs over the FP16 copies the model's
+    prefill made (same output bits; their HBM cost is stated)."""
     import ctypes as C
 
     from graph_horizon_amd import _ffi as F
+    from graph_horizon_amd import synth
 
     d, ffn = shape.embedding_length, shape.feed_forward_length
     rng = np.random.default_rng(11)
@@ -473,14 +559,23 @@ def prefill_gemm(hip, model, shape, tensors, n):
         return {"shape": f"{n}x{ind}->{outd}", "avg_us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
                 "frac_f16_mfma_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
 
-    out = {"weights": "the model's, over the FP16 copies its prefill reads", "dequantizing": {}}
+    copy_bytes = 2 * sum(i * o for i, o in (synth.tensor_dims(shape, t) for t in synth.LAYER_FORMATS))
+    out = {"weights": f"Q4_K gate/up, Q6_K down of {layers} layers, dequantized tile by tile "
+                      f"(the C3 workload)",
+           "fp16_weight_copies": {
+               "weights": "the same layers' FP16 copies (a prefill of more than 128 rows reads "
+                          "these instead; same output bits)",
+               "hbm_cost_bytes": copy_bytes * shape.block_count,
+               "hbm_cost": f"{copy_bytes * shape.block_count / 1e9:.1f} GB of HBM beside the "
+                           f"{weight_bytes(shape)[1] / 1e9:.1f} GB of Q4_K_M weights"}}
     for name, tid, ind, outd, a in (("gate_up_q4k", F.T_FFN_GATE, d, ffn, a_d),
                                     ("down_q6k", F.T_FFN_DOWN, ffn, d, a_f)):
-        out[name] = timed(name, [model_weight(model, li, tid) for li in range(layers)], ind, outd, a)
         ws = [hip.load_weight(*host[(li, tid)], ind, outd) for li in range(layers)]
-        out["dequantizing"][name] = timed(name + " (dequantizing)", ws, ind, outd, a)
+        out[name] = timed(name + " (dequantizing)", ws, ind, outd, a)
         for w in ws:
             hip.free_buffer(w)
+        out["fp16_weight_copies"][name] = timed(
+            name + " (FP16 copies)", [model_weight(model, li, tid) for li in range(layers)], ind, outd, a)
     for b in (a_d, a_f, y):
         hip.free_buffer(b)
     return out

@@ -50,7 +50,7 @@ const KernelName kKernels[] = {
     {K_GEMM3_Q4K_R128, "gh_gemm3_q4k_r128"},   {K_GEMM3_Q6K_R128, "gh_gemm3_q6k_r128"},
     {K_GEMM3_Q4K_R96, "gh_gemm3_q4k_r96"},     {K_GEMM3_Q6K_R96, "gh_gemm3_q6k_r96"},
     {K_TOPK_PARTIAL, "gh_topk_partial"},       {K_TOPK_FINAL, "gh_topk_final"},
-    {K_FILL_U32, "gh_fill_u32"},
+    {K_FILL_U32, "gh_fill_u32"},           {K_STREAM_PROBE, "gh_stream_probe"},
     {K_DEQUANT_F16_Q4K, "gh_dequant_f16_q4k"}, {K_DEQUANT_F16_Q6K, "gh_dequant_f16_q6k"},
     {K_GEMM4W_Q4K_R128, "gh_gemm4w_q4k_r128"}, {K_GEMM4W_Q6K_R128, "gh_gemm4w_q6k_r128"},
     {K_GEMM4W_MIXED_R128, "gh_gemm4w_mixed_r128"},
@@ -1286,6 +1286,20 @@ int gh_set_attention_splits(gh_backend* b, uint32_t splits) {
     b->attn_splits = splits;
     ++b->gen;  // recorded graphs hold the old grid
     return GH_OK;
+}
+
+int gh_stream_probe(gh_backend* b, gh_encoder* enc, const gh_buf* src, uint64_t offset, uint64_t bytes,
+                    const gh_buf* sink, uint32_t workgroups) {
+    int rc = check_enc(b, enc);
+    if (rc) return rc;
+    if (!src || !sink) return latch(enc, fail(b, GH_E_INVALID, "stream probe: null"));
+    if (offset % 16 || bytes % 16 || bytes == 0 || bytes / 16 > 0xFFFFFFFFull || workgroups == 0 ||
+        workgroups > 65535)
+        return latch(enc, fail(b, GH_E_INVALID, "stream probe: 16-byte multiples, 1..65535 workgroups"));
+    if (offset > src->bytes || bytes > src->bytes - offset || !fits(sink, 4))
+        return latch(enc, fail(b, GH_E_RANGE, "stream probe: beyond buffer"));
+    GhEltArgs e{sink->addr, src->addr + offset, 0, (uint32_t)(bytes / 16), workgroups};
+    return latch(enc, launch(b, K_STREAM_PROBE, workgroups, 1, 1, 256, &e));
 }
 
 int gh_scratch_info(const gh_backend* b, uint64_t* workspace_bytes, uint64_t* counter_slots,

@@ -70,6 +70,7 @@ enum GhKernel : int {
     K_TOPK_PARTIAL,
     K_TOPK_FINAL,
     K_FILL_U32,
+    K_STREAM_PROBE,
     K_DEQUANT_F16_Q4K,
     K_DEQUANT_F16_Q6K,
     K_GEMM4W_Q4K_R128,

@@ -69,6 +69,31 @@ GH_KERNEL __launch_bounds__(256) void gh_fill_u32(GhEltArgs a) {
     if (i < a.n) gh_gpw<uint32_t>(a.out)[i] = a.pad;
 }
 
+// A plain streaming read, for measurement (no counterpart in the reference): the n 16-byte
+// chunks at `a`, read with nontemporal loads (as the decode GEMVs read weights), four in
+// flight per thread; thread i of the pad x 256 threads takes chunks i, i + 256 pad, ... . The
+// chunks are XOR-folded and the fold is stored only if it equals 0xFFFFFFFF, so the loads stay
+// live while the kernel writes (almost) nothing: its duration is what a pure weight stream of
+// that size and launch shape takes on this chip.
+GH_KERNEL __launch_bounds__(256) void gh_stream_probe(GhEltArgs a) {
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    const GH_GLOBAL u4v* src = (const GH_GLOBAL u4v*)a.a;
+    const uint32_t stride = a.pad * 256;
+    uint32_t i = blockIdx.x * 256 + threadIdx.x, acc = 0;
+    for (; i + 3 * stride < a.n; i += 4 * stride) {
+        u4v v[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) v[k] = __builtin_nontemporal_load(src + i + k * stride);
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    for (; i < a.n; i += stride) {
+        const u4v v = __builtin_nontemporal_load(src + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0xFFFFFFFFu) gh_gpw<uint32_t>(a.out)[0] = blockIdx.x;
+}
+
 // kv_write f16 (cpu/kernels/attention/write.rs:50-63): raw FP16 copy of K and V into the
 // caches at element offsets; with pos_ptr the offsets advance by stride * (*pos_ptr).
 GH_KERNEL __launch_bounds__(256) void gh_kv_write(GhKvWriteArgs a) {

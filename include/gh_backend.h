@@ -212,6 +212,14 @@ int gh_synchronize(gh_backend* b);
  * recorded before the call are re-recorded on their next use. */
 int gh_set_attention_splits(gh_backend* b, uint32_t splits);
 
+/* A plain streaming read of [offset, offset + bytes) of `src` by `workgroups` workgroups of
+ * 256 threads (no counterpart in the reference: a measurement kernel). It stands for the
+ * weight stream of a decode GEMV of the same size with no arithmetic, so its duration is the
+ * floor of one launch of that size. `sink` (at least 4 bytes) is almost never written;
+ * offset and bytes are multiples of 16. */
+int gh_stream_probe(gh_backend* b, gh_encoder* enc, const gh_buf* src, uint64_t offset,
+                    uint64_t bytes, const gh_buf* sink, uint32_t workgroups);
+
 /* The backend's growable device scratch (no counterpart in the reference: a diagnostic for
  * tests): workspace bytes (split-K and attention partials, argmax partials), attention-merge
  * counter slots, and a generation number bumped whenever either is reallocated or a recorded
