@@ -133,9 +133,7 @@ def test_decode_every_forced_split_count(hip, qh, kvh):
     """Decode attention with each split count 1..32 forced (gh_set_attention_splits), for each
     GQA group size: the split partials cross workgroups through agent-scope atomics and the
     last workgroup of each (row, kv head) merges them. Positions below, at and across chunk
-    boundaries, and counts above the row's chunk count (the launch then has more workgroups
-    than splits in use, as in a replayed graph's fixed grid). Same bar as the oracle decode
-    test."""
+    boundaries, and counts above the row's chunk count. Same bar as the oracle decode test."""
     rng = np.random.default_rng(321 + qh)
     ctx, layers = 2048, 2
     kc = O.f16(rng.standard_normal(layers * ctx * kvh * 128).astype(np.float32))
@@ -176,3 +174,26 @@ def test_greedy_graph_with_forced_splits_matches_stream(hip):
     finally:
         hip.set_attention_splits(0)
     assert np.array_equal(outs[0], outs[1])
+
+
+def test_graph_replay_ignores_partials_of_earlier_steps(hip):
+    """The replayed decode graph's attention grid is fixed (4 splits at a 256-position
+    context), while the splits in use follow the position. A run that crosses position 64
+    (two splits in use) leaves real partials and merge state behind; replaying the first steps
+    again (one split in use) must give the first run's tokens."""
+    from graph_horizon_amd import HipModel, synth
+
+    shape = synth.SHAPES["tiny"]
+    gm = HipModel(hip, synth.model_config(shape, 256, 64))
+    for layer, tid, fmt, data in synth.model_tensors(shape, 33):
+        gm.load_tensor(layer, tid, fmt, data)
+    prompt = [3, 99, 1500, 42]
+    gm.prefill(prompt, 0)
+    first = gm.read_argmax()
+    short = gm.decode_greedy(first, 4, 8)
+    gm.prefill(prompt, 0)
+    long = gm.decode_greedy(first, 4, 70)
+    gm.prefill(prompt, 0)
+    again = gm.decode_greedy(first, 4, 8)
+    gm.close()
+    assert np.array_equal(long[:8], short) and np.array_equal(again, short)
