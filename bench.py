@@ -175,6 +175,10 @@ def main():
                          "--probe-groups workgroups and the C1 GEMV, back to back over distinct "
                          "memory: the floor of one launch of each size, and (under rocprofv3 "
                          "--kernel-trace) the tracer's per-dispatch cost")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="calibration only: the vendor library's dense FP16 GEMM (torch.matmul, "
+                         "hipBLASLt) at the C3 shapes beside this build's dequantizing GEMMs, "
+                         "same box, same timing")
     ap.add_argument("--probe-bytes", default="9437184,94371840",
                     help="comma-separated read sizes for --floor-probe")
     ap.add_argument("--probe-groups", default="256,512,1024,2048",
@@ -197,6 +201,9 @@ def main():
     if args.floor_probe:
         floor_probe([int(v) for v in args.probe_bytes.split(",")],
                     [int(v) for v in args.probe_groups.split(",")])
+        return
+    if args.vendor_gemm:
+        vendor_gemm(synth.SHAPES["8b"])
         return
     if args.attn_probe:
         hip = HipBackend(0)
@@ -498,6 +505,81 @@ def gemm_probe(shape, n=512):
         for b in ws + [a]:
             hip.free_buffer(b)
     log(f"bench: gemm probe: 32 x {n}x{d}->{ffn} Q4_K, 32 x {n}x{ffn}->{d} Q6_K")
+    hip.close()
+
+
+def vendor_gemm(shape, sizes=(128, 512, 2048), reps=6):
+    """Calibration for the C3 GEMMs: what the vendor library reaches on this chip at the same
+    shapes. torch.matmul over dense FP16 weights (hipBLASLt; FP16 in, FP32 accumulation, FP16
+    out) and this build's GEMMs over Q4_K (gate/up, d -> FFN) and Q6_K (down, FFN -> d) weights
+    that they dequantize tile by tile, each over 8 distinct weights (more bytes than the MALL
+    holds), timed back to back with events on the stream each is launched on. The vendor figure
+    is a ceiling for the arithmetic at these shapes, not the C3 workload (it reads FP16 weights,
+    3.6x the Q4_K bytes)."""
+    import ctypes as C
+
+    import torch
+
+    from graph_horizon_amd import HipBackend, synth
+
+    dev = torch.device("cuda", 0)
+    hip = HipBackend(0)
+    d, ffn = shape.embedding_length, shape.feed_forward_length
+    rng = np.random.default_rng(3)
+    out = {"vendor": [], "own": []}
+    for name, fmt, ind, outd in (("gate_up", 12, d, ffn), ("down", 14, ffn, d)):
+        # operands made on the host and copied over: the calibration runs no torch kernel of its
+        # own on the device, only the library GEMM
+        g = torch.Generator().manual_seed(ind)
+        tw = [(torch.randn(ind, outd, generator=g) * 0.02).half().to(dev) for _ in range(8)]
+        ws = [hip.load_weight(fmt, synth.quant_blocks(rng, fmt, outd, ind, synth.model_d_std(ind)), ind, outd)
+              for _ in range(8)]
+        for n in sizes:
+            fl = 2.0 * n * ind * outd
+            tx = torch.randn(n, ind, generator=g).half().to(dev)
+            for w in tw:
+                torch.matmul(tx, w)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                for w in tw:
+                    torch.matmul(tx, w)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * len(tw))
+            tf = fl / (us * 1e-6) / 1e12
+            out["vendor"].append({"gemm": name, "shape": f"{n}x{ind}->{outd}", "avg_us": round(us, 2),
+                                  "tflops": round(tf, 1), "frac_f16_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+            log(f"bench: vendor FP16 GEMM {name} {n}x{ind}->{outd}: {us:.1f} us, {tf:.0f} TFLOP/s "
+                f"({tf / MFMA_F16_PEAK_TFLOPS:.1%})")
+            del tx
+            a = hip.from_host(synth_f16(rng, n * ind))
+            y = hip.alloc_buffer(n * outd * 2)
+            enc = hip.begin()
+            for w in ws:
+                hip.lib.gh_matmul_batched(hip.h, enc, C.byref(y), C.byref(a), C.byref(w), ind, outd, n)
+            hip.submit()
+            enc = hip.begin()
+            hip.timer_start()
+            for _ in range(reps):
+                for w in ws:
+                    hip.lib.gh_matmul_batched(hip.h, enc, C.byref(y), C.byref(a), C.byref(w), ind, outd, n)
+            us = hip.timer_stop() * 1e3 / (reps * len(ws))
+            hip.submit()
+            tf = fl / (us * 1e-6) / 1e12
+            out["own"].append({"gemm": name, "fmt": "Q4_K" if fmt == 12 else "Q6_K", "shape": f"{n}x{ind}->{outd}",
+                               "avg_us": round(us, 2), "tflops": round(tf, 1),
+                               "frac_f16_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+            log(f"bench: dequantizing GEMM {name} {n}x{ind}->{outd}: {us:.1f} us, {tf:.0f} TFLOP/s "
+                f"({tf / MFMA_F16_PEAK_TFLOPS:.1%})")
+            hip.free_buffer(a)
+            hip.free_buffer(y)
+        for w in ws:
+            hip.free_buffer(w)
+        del tw
+        torch.cuda.empty_cache()
+    print(json.dumps({"vendor_gemm": out}), flush=True)
     hip.close()
 
 

@@ -648,6 +648,10 @@ int gh_create(const gh_config* cfg, gh_backend** out) {
         if (!f) rc = fail(b, GH_E_MODULE, std::string("kernel not found: ") + kn.name);
         b->fn[kn.id] = f;
     }
+    // the lookups in modules that do not hold a kernel leave hipErrorNotFound as the thread's
+    // last error, which another HIP user in the process (a framework that checks
+    // hipGetLastError after its own calls) would take for its own failure
+    (void)hipGetLastError();
     if (!rc) rc = ensure_workspace(b, 0);
     if (!rc) rc = noalloc_init(b);
     if (rc) {

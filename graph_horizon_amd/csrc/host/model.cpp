@@ -92,7 +92,7 @@ uint64_t prefill_headroom(const gh_model* m, uint32_t rows) {
 
 // Dequantize every layer matrix once into an FP16 copy and register it, so that the prefill
 // GEMMs copy weight tiles into LDS instead of dequantizing them per tile (the same FP16 values:
-// identical results). 2 bytes per weight: 14.8 GB for the 8B shape, 24 GB for the 14B one, of
+// identical results). 2 bytes per weight: 13.1 GB for the 8B shape, 24.3 GB for the 14B one, of
 // 288 GB. The copies are made only when the device has room for them and for a prefill chunk's
 // workspace beside them; otherwise (or when an allocation fails) the model records the failure
 // and its prefills keep dequantizing (nothing is registered) without trying again.

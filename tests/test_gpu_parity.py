@@ -305,6 +305,23 @@ def test_view_alignment(hip):
     hip.free_buffer(b)
 
 
+def test_create_leaves_no_hip_error():
+    """gh_create resolves each kernel by trying the modules in turn; the misses must not stay
+    behind as the thread's last HIP error, which another HIP user in the same process (torch
+    checks hipGetLastError after its own calls) would report as its own failure."""
+    import ctypes
+
+    from graph_horizon_amd import HipBackend
+
+    rt = ctypes.CDLL("libamdhip64.so")
+    rt.hipGetLastError()  # whatever came before
+    b = HipBackend(0)
+    try:
+        assert rt.hipGetLastError() == 0
+    finally:
+        b.close()
+
+
 # ---------------------------------------------------------------- attention
 def _attn_case(hip, ctx, layers, seed, qh=32, kvh=8):
     rng = np.random.default_rng(seed)
