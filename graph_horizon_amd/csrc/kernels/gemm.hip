@@ -1,18 +1,24 @@
 // Prefill GEMM on the matrix cores: out[t][r] = Σ_k x[t][k] · w[r][k] for n tokens of FP16
 // activations against Q4_K / Q6_K weights in the device layout (gh_kargs.h).
 //
-// Tiling: a 256-thread workgroup owns 4·WT tokens x BR weight rows; wave w owns WT tokens x BR
-// rows as tiles of v_mfma_f32_32x32x16_f16 (A = activations, M = tokens, loaded from global
-// memory straight into registers; B = weights, N = rows; FP32 accumulators). K advances one
-// 64-weight unit per stage. Each stage the workgroup dequantizes the w tile (BR rows x 64)
-// into LDS as FP16. Q4_K: w = FP16(RNE(the reference's FP32 dequantized weight)), computed as
-// dequant_row does ((d·sc)·q - dmin·mn, cpu/dequant.rs:93-123). Q6_K: (q - 32)·(d·sc) as one
-// fused multiply-add u·da + (-32·da) rounded once to FP16 (the compiler forms v_fma_mix);
-// the reference rounds the same exact product to FP32 first (dequant.rs:274-308), and the two
-// roundings differ by one FP16 ulp when that FP32 value lands exactly on an FP16 tie. The
-// LDS tile is double-buffered; the next unit's weight
-// and activation loads are in flight while the matrix cores run on the current one, and one
-// barrier separates stages.
+// Every GEMM is a 512-thread workgroup over 256 (or 128) tokens x BR weight rows, K advancing
+// one 64-weight unit per stage through a 3-stage LDS ring, one barrier per unit, with
+// v_mfma_f32_32x32x16_f16 tiles (A = activations, M = tokens; B = weights, N = rows; FP32
+// accumulators). Two forms:
+//   gemm3_body (dequantizing; the C3 workload): warp-specialized. Waves 4-7 (producers) keep
+//     the raw weight bytes of 4 units in flight in registers and dequantize each unit into its
+//     LDS stage as FP16, one row per lane; waves 0-3 (consumers) fetch their activation lines
+//     one unit ahead straight into LDS with global_load_lds_dwordx4 and run the MFMA tiles.
+//     Q4_K: w = FP16(RNE(the reference's FP32 dequantized weight)), computed as dequant_row
+//     does ((d·sc)·q - dmin·mn, cpu/dequant.rs:93-123). Q6_K: (q - 32)·(d·sc) as one fused
+//     multiply-add u·da + (-32·da) rounded once to FP16 (v_fma_mix); the reference rounds the
+//     same exact product to FP32 first (dequant.rs:274-308), and the two roundings differ by
+//     one FP16 ulp when that FP32 value lands exactly on an FP16 tie.
+//   gemm4_body (over FP16 weight copies made by dequant_f16, the same values): every wave runs
+//     the matrix cores; activation lines and weight rows both arrive by LDS DMA, and the k
+//     order of every sum is gemm3_body's, so the bits are the same.
+// A multi-matrix launch (gemm3_mixed, the prefill's Q/K/V) runs each row tile in its matrix's
+// format over the shared LDS block.
 //
 // A Q6_K unit's 64 weights are not contiguous in k (16 from each quarter of a 128-weight half
 // block); x is staged in the same permuted order, which leaves every dot product unchanged.
@@ -24,7 +30,9 @@
 // FP16 values are exact in FP32; accumulation is FP32.
 //
 // Split-K (grid.z > 1): each split covers a contiguous range of units and writes FP32
-// partials [split][n][rows]; gh_gemm_reduce sums them in split order and rounds to FP16.
+// partials [split][n][rows]; gh_gemm_reduce sums them in split order and rounds to FP16
+// (gh_gemm_reduce_seg and gh_gemm_tail fold the prefill driver's RoPE, K/V-cache writes,
+// residual add and RMSNorm into that sum).
 #include "gh_common.h"
 
 namespace {
