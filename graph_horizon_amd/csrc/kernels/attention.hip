@@ -526,41 +526,30 @@ typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPK = 64;          // key positions per tile
-// LDS pitches, chosen so that every 16-byte fragment read is free of bank conflicts on gfx950
-// (ds_read_b128 serves 32 lanes per pass over 128 four-byte banks): 16 key rows x 2 chunks or
-// 16 dim rows x 2 chunks per pass land on 32 distinct bank quads.
-constexpr int kKP = 128 + 16;    // K tile pitch (FP16): [64 keys][128 dims], 288 B
-constexpr int kVP = kPK + 16;    // V^T tile pitch (FP16): [128 dims][64 keys, slot order], 160 B
-
-// V^T keeps keys in MFMA k-slot order: within each group of 32 keys, key 16h + 4f + i sits at
-// slot 8f + 4h + i, so lane group f's eight slots (keys 4f .. 4f+3 and 16+4f .. 16+4f+3, the
-// keys its P values belong to) are one contiguous 16-byte run.
-__device__ __forceinline__ uint32_t vt_slot(uint32_t key) {
-    return (key & ~31u) + 8 * ((key >> 2) & 3u) + 4 * ((key >> 4) & 1u) + (key & 3u);
-}
+// K and V tiles share one layout, [64 keys][128 dims] at a 288-byte pitch, chosen from the
+// gfx950 bank model (128 four-byte banks): a K fragment read (ds_read_b128, 32 lanes per pass:
+// 16 key rows x 2 chunks) and a V transposing read (ds_read_b64_tr_b16, 64 lanes: 16 key rows
+// x 32 bytes) each land on distinct banks, since 72·r mod 128 differs for 16 consecutive rows r.
+constexpr int kKP = 128 + 16;    // tile pitch (FP16): 288 B
 
 struct KVStage {
     uint4 k0, k1, k2, k3;  // K: chunk (key c/16, dims 8·(c%16)), c = tid + 256 i
-    uint4 v0, v1, v2, v3;  // V: keys 4·(lane%16) + i, dims 8·(lane/16 + 4·wave)
+    uint4 v0, v1, v2, v3;  // V: the same chunks of the V rows
 };
 
-__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
-__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xFFFF0000u); }
-
-// Per-thread byte offsets of the K / V chunks a thread stages, relative to the tile's first key.
+// Per-thread byte offsets of the K / V chunks a thread stages (key c / 16, dims 8·(c % 16),
+// c = tid + 256 i), relative to the tile's first key.
 struct KVOffsets {
-    uint32_t k[4], v[4];
+    uint32_t k[4];
 };
 
 __device__ __forceinline__ KVOffsets kv_offsets(uint32_t kv_row) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63u;
-    const uint32_t dg = (lane >> 4) + 4 * (tid >> 6), kg = lane & 15u;
+    const uint32_t tid = threadIdx.x;
     KVOffsets o;
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t c = tid + 256u * i;  // K: key c / 16, dims 8·(c % 16)
+        const uint32_t c = tid + 256u * i;
         o.k[i] = ((c >> 4) * kv_row + (c & 15u) * 8) * 2;
-        o.v[i] = ((4 * kg + i) * kv_row + dg * 8) * 2;  // V: key 4·kg + i, dims 8·dg
     }
     return o;
 }
@@ -582,31 +571,39 @@ __device__ __forceinline__ void kv_load(const uint16_t* kc, const uint16_t* vc, 
     s.k1 = ld(rk, off.k[1]);
     s.k2 = ld(rk, off.k[2]);
     s.k3 = ld(rk, off.k[3]);
-    s.v0 = ld(rv, off.v[0]);
-    s.v1 = ld(rv, off.v[1]);
-    s.v2 = ld(rv, off.v[2]);
-    s.v3 = ld(rv, off.v[3]);
+    s.v0 = ld(rv, off.k[0]);
+    s.v1 = ld(rv, off.k[1]);
+    s.v2 = ld(rv, off.k[2]);
+    s.v3 = ld(rv, off.k[3]);
 }
 
 __device__ __forceinline__ void kv_store(const KVStage& s, _Float16* kt, _Float16* vt) {
     const uint32_t tid = threadIdx.x;
-    _Float16* kd = kt + (tid >> 4) * kKP + (tid & 15u) * 8;  // + 16 keys per i
-    *(uint4*)(kd) = s.k0;
-    *(uint4*)(kd + 16 * kKP) = s.k1;
-    *(uint4*)(kd + 32 * kKP) = s.k2;
-    *(uint4*)(kd + 48 * kKP) = s.k3;
-    // V transposed: dims 8·dg + e get the four keys 4·kg .. 4·kg + 3 as one 8-byte run
-    const uint32_t lane = tid & 63u, dg = (lane >> 4) + 4 * (tid >> 6), kg = lane & 15u;
-    const uint32_t r0[4] = {s.v0.x, s.v0.y, s.v0.z, s.v0.w};
-    const uint32_t r1[4] = {s.v1.x, s.v1.y, s.v1.z, s.v1.w};
-    const uint32_t r2[4] = {s.v2.x, s.v2.y, s.v2.z, s.v2.w};
-    const uint32_t r3[4] = {s.v3.x, s.v3.y, s.v3.z, s.v3.w};
-    _Float16* vd = vt + (dg * 8) * kVP + vt_slot(kg * 4);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        *(uint2*)(vd + (2 * c) * kVP) = make_uint2(lo_pair(r0[c], r1[c]), lo_pair(r2[c], r3[c]));
-        *(uint2*)(vd + (2 * c + 1) * kVP) = make_uint2(hi_pair(r0[c], r1[c]), hi_pair(r2[c], r3[c]));
-    }
+    const uint32_t at = (tid >> 4) * kKP + (tid & 15u) * 8;  // + 16 keys per i
+    *(uint4*)(kt + at) = s.k0;
+    *(uint4*)(kt + at + 16 * kKP) = s.k1;
+    *(uint4*)(kt + at + 32 * kKP) = s.k2;
+    *(uint4*)(kt + at + 48 * kKP) = s.k3;
+    *(uint4*)(vt + at) = s.v0;
+    *(uint4*)(vt + at + 16 * kKP) = s.v1;
+    *(uint4*)(vt + at + 32 * kKP) = s.v2;
+    *(uint4*)(vt + at + 48 * kKP) = s.v3;
+}
+
+// A fragment of V^T for O^T += V^T·P^T: output row m = dims 16 j + m, k-slots = keys key0 + 0..3
+// (elements 0-3) and key0 + 16 + 0..3 (elements 4-7), read from the [key][dim] tile with two
+// ds_read_b64_tr_b16. Within each 16-lane group that instruction gives lane i the halves
+// (i mod 4) of the 8-byte rows that lanes 4k + i / 4 address (k = 0..3, in order); so lane fr
+// addresses key key0 + fr / 4, dims 16 j + 4 (fr mod 4), and lane i receives dim 16 j + i at
+// the four keys.
+typedef short as4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ ah8 v_frag(const _Float16* vb, uint32_t key0, uint32_t j, uint32_t fr) {
+    typedef __attribute__((address_space(3))) as4* lds_as4;
+    _Float16* p = (_Float16*)vb + (key0 + (fr >> 2)) * kKP + 16 * j + 4 * (fr & 3u);
+    const as4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_as4)p);
+    const as4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_as4)(p + 16 * kKP));
+    const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+    return __builtin_bit_cast(ah8, make_uint4(ua.x, ua.y, ub.x, ub.y));
 }
 
 // Reductions over the four lanes l, l^16, l^32, l^48 (one query row's lane group) with the
@@ -637,7 +634,7 @@ template <int QT>  // query tiles of 16 rows per wave
 __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
     constexpr uint32_t kPQ = 16 * QT;  // query rows per workgroup
     __shared__ __attribute__((aligned(16))) _Float16 kt[2][kPK * kKP];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[2][128 * kVP];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][kPK * kKP];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t nqb = (a.rows + kPQ - 1) / kPQ;
     // Work order: L = 0 is the heaviest (latest) query block. Workgroup k of the first half of
@@ -756,12 +753,12 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
                 }
         }
         // O^T += V^T P^T: A = V^T rows (dims 16 j + fr), k-slots = keys 32 ks2 + {4 fg .. +3,
-        // 16 + 4 fg .. +3} (one 16-byte run in slot order), the keys the lane's P values hold
+        // 16 + 4 fg .. +3}, the keys the lane's P values hold
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
             for (int ks2 = 0; ks2 < 2; ++ks2) {
-                const ah8 vf = *(const ah8*)(vb + (16 * j + fr) * kVP + 32 * ks2 + 8 * fg);
+                const ah8 vf = v_frag(vb, 32 * ks2 + 4 * fg, j, fr);
 #pragma unroll
                 for (int t = 0; t < QT; ++t) {
                     o[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[ks2][t], o[j][t], 0, 0, 0);
