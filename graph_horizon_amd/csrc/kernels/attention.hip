@@ -526,68 +526,44 @@ typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPK = 64;          // key positions per tile
-// K and V tiles share one layout, [64 keys][128 dims] at a 288-byte pitch, chosen from the
-// gfx950 bank model (128 four-byte banks): a K fragment read (ds_read_b128, 32 lanes per pass:
-// 16 key rows x 2 chunks) and a V transposing read (ds_read_b64_tr_b16, 64 lanes: 16 key rows
-// x 32 bytes) each land on distinct banks, since 72·r mod 128 differs for 16 consecutive rows r.
-constexpr int kKP = 128 + 16;    // tile pitch (FP16): 288 B
+// K and V tiles share one layout: [64 keys][128 dims] in 256-byte rows, the 32-byte block b of
+// row r holding dims 16 (b ^ sw(r)) .. + 16, sw(r) = (r / 2) mod 8. With 128 four-byte banks,
+// a K fragment read (ds_read_b128, 32 lanes per pass: 16 consecutive rows x 2 chunks of one
+// block) and a V transposing read (ds_read_b64_tr_b16, 64 lanes: 16 consecutive rows x one
+// block) each meet 16 distinct (r mod 2, sw(r)) pairs, so every lane lands on its own banks.
+__device__ __forceinline__ uint32_t kv_sw(uint32_t r) { return (r >> 1) & 7u; }
+// offset in halves of dims 16·blk .. + 16 of row r
+__device__ __forceinline__ uint32_t kv_at(uint32_t r, uint32_t blk) { return r * 128 + 16 * (blk ^ kv_sw(r)); }
 
-struct KVStage {
-    uint4 k0, k1, k2, k3;  // K: chunk (key c/16, dims 8·(c%16)), c = tid + 256 i
-    uint4 v0, v1, v2, v3;  // V: the same chunks of the V rows
-};
+#define GH_LDS __attribute__((address_space(3)))
 
-// Per-thread byte offsets of the K / V chunks a thread stages (key c / 16, dims 8·(c % 16),
-// c = tid + 256 i), relative to the tile's first key.
-struct KVOffsets {
-    uint32_t k[4];
-};
-
-__device__ __forceinline__ KVOffsets kv_offsets(uint32_t kv_row) {
-    const uint32_t tid = threadIdx.x;
-    KVOffsets o;
+// Stage keys t0 .. t0+63 of K and V straight into their tiles by LDS DMA (global_load_lds_dwordx4:
+// lane i of a load lands at byte 16 i of its 1 KiB destination, four 256-byte rows): wave w
+// loads rows 16 w .. 16 w + 15, lane i of load q the 16-byte chunk of row r = 16 w + 4 q + i / 16
+// that belongs in slot i mod 16. Keys past kv_end (masked; their weight is 0) re-read key
+// kv_end - 1, so every value in the tile is a finite cache value and no load leaves the range.
+// The loads are issued from inline assembly: the compiler does not count them, so it adds no
+// wait before the reads of the other tile buffer; the caller waits (vmcnt(0)) before the
+// barrier that hands the tile over. (Untracked loads can only make the compiler's own waits
+// stricter, and the tile loop issues no tracked global loads.)
+__device__ __forceinline__ void kv_dma(const uint16_t* kc, const uint16_t* vc, uint32_t kv_row,
+                                       uint32_t t0, uint32_t kv_end, _Float16* kt, _Float16* vt) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, sl = lane & 15u;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t c = tid + 256u * i;
-        o.k[i] = ((c >> 4) * kv_row + (c & 15u) * 8) * 2;
+    for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t r = 16 * wave + 4 * q + (lane >> 4);
+        const uint32_t c = ((((sl >> 1) ^ kv_sw(r)) << 1) | (sl & 1u));  // the row's chunk for this slot
+        const size_t src = (size_t)min(t0 + r, kv_end - 1) * kv_row + 8 * c;
+        const uint32_t at = (16 * wave + 4 * q) * 128;
+        const uint32_t dk = (uint32_t)(uintptr_t)(GH_LDS void*)(kt + at);
+        const uint32_t dv = (uint32_t)(uintptr_t)(GH_LDS void*)(vt + at);
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((uint64_t)(uintptr_t)(kc + src)),
+                     "{m0}"(__builtin_amdgcn_readfirstlane(dk))
+                     : "memory");
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"((uint64_t)(uintptr_t)(vc + src)),
+                     "{m0}"(__builtin_amdgcn_readfirstlane(dv))
+                     : "memory");
     }
-    return o;
-}
-
-// Stage keys t0 .. t0+63 through buffer loads whose range ends at key kv_end: the hardware
-// returns zeros past it (those keys are causally masked and carry zero weight), so no per-load
-// clamp or 64-bit address arithmetic is needed.
-__device__ __forceinline__ void kv_load(const uint16_t* kc, const uint16_t* vc, uint32_t kv_row,
-                                        uint32_t t0, uint32_t kv_end, const KVOffsets& off, KVStage& s) {
-    const uint32_t bytes = (kv_end - t0) * kv_row * 2;
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(kc + (size_t)t0 * kv_row), 0, (int)bytes, kBufWord3);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(vc + (size_t)t0 * kv_row), 0, (int)bytes, kBufWord3);
-    auto ld = [](__amdgpu_buffer_rsrc_t r, uint32_t o) {
-        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
-    };
-    s.k0 = ld(rk, off.k[0]);
-    s.k1 = ld(rk, off.k[1]);
-    s.k2 = ld(rk, off.k[2]);
-    s.k3 = ld(rk, off.k[3]);
-    s.v0 = ld(rv, off.k[0]);
-    s.v1 = ld(rv, off.k[1]);
-    s.v2 = ld(rv, off.k[2]);
-    s.v3 = ld(rv, off.k[3]);
-}
-
-__device__ __forceinline__ void kv_store(const KVStage& s, _Float16* kt, _Float16* vt) {
-    const uint32_t tid = threadIdx.x;
-    const uint32_t at = (tid >> 4) * kKP + (tid & 15u) * 8;  // + 16 keys per i
-    *(uint4*)(kt + at) = s.k0;
-    *(uint4*)(kt + at + 16 * kKP) = s.k1;
-    *(uint4*)(kt + at + 32 * kKP) = s.k2;
-    *(uint4*)(kt + at + 48 * kKP) = s.k3;
-    *(uint4*)(vt + at) = s.v0;
-    *(uint4*)(vt + at + 16 * kKP) = s.v1;
-    *(uint4*)(vt + at + 32 * kKP) = s.v2;
-    *(uint4*)(vt + at + 48 * kKP) = s.v3;
 }
 
 // A fragment of V^T for O^T += V^T·P^T: output row m = dims 16 j + m, k-slots = keys key0 + 0..3
@@ -595,13 +571,13 @@ __device__ __forceinline__ void kv_store(const KVStage& s, _Float16* kt, _Float1
 // ds_read_b64_tr_b16. Within each 16-lane group that instruction gives lane i the halves
 // (i mod 4) of the 8-byte rows that lanes 4k + i / 4 address (k = 0..3, in order); so lane fr
 // addresses key key0 + fr / 4, dims 16 j + 4 (fr mod 4), and lane i receives dim 16 j + i at
-// the four keys.
+// the four keys. Rows r and r + 16 share sw(r).
 typedef short as4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ ah8 v_frag(const _Float16* vb, uint32_t key0, uint32_t j, uint32_t fr) {
-    typedef __attribute__((address_space(3))) as4* lds_as4;
-    _Float16* p = (_Float16*)vb + (key0 + (fr >> 2)) * kKP + 16 * j + 4 * (fr & 3u);
+    typedef GH_LDS as4* lds_as4;
+    _Float16* p = (_Float16*)vb + kv_at(key0 + (fr >> 2), j) + 4 * (fr & 3u);
     const as4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_as4)p);
-    const as4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_as4)(p + 16 * kKP));
+    const as4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_as4)(p + 16 * 128));
     const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
     return __builtin_bit_cast(ah8, make_uint4(ua.x, ua.y, ub.x, ub.y));
 }
@@ -633,8 +609,8 @@ typedef _Float16 ah2 __attribute__((ext_vector_type(2)));
 template <int QT>  // query tiles of 16 rows per wave
 __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
     constexpr uint32_t kPQ = 16 * QT;  // query rows per workgroup
-    __shared__ __attribute__((aligned(16))) _Float16 kt[2][kPK * kKP];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[2][kPK * kKP];
+    __shared__ __attribute__((aligned(16))) _Float16 kt[2][kPK * 128];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][kPK * 128];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t nqb = (a.rows + kPQ - 1) / kPQ;
     // Work order: L = 0 is the heaviest (latest) query block. Workgroup k of the first half of
@@ -678,10 +654,14 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
     }
 
     const uint32_t kv_row32 = (uint32_t)kv_row;
-    const KVOffsets off = kv_offsets(kv_row32);
-    KVStage st;
-    kv_load(kc, vc, kv_row32, 0, kv_end, off, st);
-    kv_store(st, kt[0], vt[0]);
+    kv_dma(kc, vc, kv_row32, 0, kv_end, kt[0], vt[0]);
+    // the query fragments are taken here, so the compiler settles their loads before the tile
+    // loop (it does not see the explicit wait below) and puts no load wait inside the loop
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qf[t][ks]));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA has landed
     __syncthreads();
     // Tiles whose last key is at or before the block's first query position need no causal
     // mask (nor do they hold the clamped duplicates past kv_end); only the diagonal ones do.
@@ -690,7 +670,8 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
         constexpr bool kMask = decltype(masked)::value;
         const uint32_t cur = tile & 1u, t0 = tile * kPK;
         const bool more = tile + 1 < ntiles;
-        if (more) kv_load(kc, vc, kv_row32, t0 + kPK, kv_end, off, st);
+        // the next tile goes into the other buffers, whose reads ended before the last barrier
+        if (more) kv_dma(kc, vc, kv_row32, t0 + kPK, kv_end, kt[cur ^ 1u], vt[cur ^ 1u]);
         const _Float16* kb = kt[cur];
         const _Float16* vb = vt[cur];
         // S^T tiles: [key tile kk][q tile t], lane holds keys 16 kk + 4 fg + e of query fr
@@ -701,7 +682,7 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
             for (int t = 0; t < QT; ++t) s[kk][t] = af4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const ah8 kf = *(const ah8*)(kb + (16 * kk + fr) * kKP + 32 * ks + 8 * fg);
+                const ah8 kf = *(const ah8*)(kb + kv_at(16 * kk + fr, 2 * ks + (fg >> 1)) + 8 * (fg & 1u));
 #pragma unroll
                 for (int t = 0; t < QT; ++t)
                     s[kk][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[t][ks], s[kk][t], 0, 0, 0);
@@ -765,8 +746,8 @@ __device__ __forceinline__ void attn_prefill_g4(const GhAttnArgs& a) {
                     o[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[ks2][t], o[j][t], 0, 0, 0);
                 }
             }
-        if (more) kv_store(st, kt[cur ^ 1u], vt[cur ^ 1u]);
-        __syncthreads();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of the next tile has landed
+        __syncthreads();  // every wave's has, and every read of this tile is done
     };
     uint32_t tile = 0;
     for (; tile < ntiles && tile * kPK + kPK - 1 <= first_pos; ++tile) step(tile, Flag<false>{});
