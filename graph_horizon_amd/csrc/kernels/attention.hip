@@ -527,11 +527,13 @@ typedef float af4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPK = 64;          // key positions per tile
 // K and V tiles share one layout: [64 keys][128 dims] in 256-byte rows, the 32-byte block b of
-// row r holding dims 16 (b ^ sw(r)) .. + 16, sw(r) = (r / 2) mod 8. With 128 four-byte banks,
-// a K fragment read (ds_read_b128, 32 lanes per pass: 16 consecutive rows x 2 chunks of one
-// block) and a V transposing read (ds_read_b64_tr_b16, 64 lanes: 16 consecutive rows x one
-// block) each meet 16 distinct (r mod 2, sw(r)) pairs, so every lane lands on its own banks.
-__device__ __forceinline__ uint32_t kv_sw(uint32_t r) { return (r >> 1) & 7u; }
+// row r holding dims 16 (b ^ sw(r)) .. + 16, sw(r) = r mod 8. Measured with
+// SQ_LDS_BANK_CONFLICT on gfx950 (a probe running each fragment read pattern alone): the K
+// fragment reads (ds_read_b128: 16 consecutive rows x 2 chunks of one block per 32 lanes) and
+// the V transposing reads (ds_read_b64_tr_b16: 16 consecutive rows x one block) are free of
+// conflicts with sw(r) = r mod 8, and conflicted with (r / 2) mod 8 (half the LDS cycles),
+// (r / 4) mod 8 or no swizzle.
+__device__ __forceinline__ uint32_t kv_sw(uint32_t r) { return r & 7u; }
 // offset in halves of dims 16·blk .. + 16 of row r
 __device__ __forceinline__ uint32_t kv_at(uint32_t r, uint32_t blk) { return r * 128 + 16 * (blk ^ kv_sw(r)); }
 
