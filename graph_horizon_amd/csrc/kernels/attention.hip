@@ -136,7 +136,9 @@ struct AttnHot {
 template <int G>
 struct AttnShared {
     float wm[kWaves][G], wl[kWaves][G];  // running max and Σe of each wave, per head
-    float wacc[kWaves][G][128];          // Σe·V of each wave, per head and value dim
+    // Σe·V of each wave, per head and value dim; rows padded to 132 floats so that the lanes of
+    // the G heads, which store the same value dims at once, do not share banks
+    float wacc[kWaves][G][132];
     float wsplit[G][kMaxSplits];
     uint32_t last;
 };
