@@ -41,7 +41,7 @@ const KernelName kKernels[] = {
     {K_KV_WRITE, "gh_kv_write"},           {K_ARGMAX_PARTIAL, "gh_argmax_partial"},
     {K_ARGMAX_FINAL, "gh_argmax_final"},   {K_ATTN_G1, "gh_attn_g1"},
     {K_ATTN_G2, "gh_attn_g2"},             {K_ATTN_MFMA_G4, "gh_attn_mfma_g4"},
-    {K_ATTN_MFMA_G8, "gh_attn_mfma_g8"},
+    {K_ATTN_MFMA_G8, "gh_attn_mfma_g8"},   {K_ATTN_MFMA_G4_S16, "gh_attn_mfma_g4_s16"},
 
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},
     {K_GEMM3_MIXED_R128, "gh_gemm3_mixed_r128"},
@@ -346,6 +346,8 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
     if (((uint64_t)kv->context + 2048) * kv->kv_heads * kv->head_dim * 2 >= (1ull << 31))
         return fail(b, GH_E_UNSUPPORTED, "attention: a layer's K or V cache of 2 GiB or more");
     const uint32_t splits = attention_splits(b, max_pos + 1, kv->kv_heads, rows);
+    // the merge of a launch of at most 16 splits reads 16 slots (same bits, half the loads)
+    if (k == K_ATTN_MFMA_G4 && splits <= 16) k = K_ATTN_MFMA_G4_S16;
     char* ws = nullptr;
     void* counters = nullptr;
     uint32_t group_rows = rows;

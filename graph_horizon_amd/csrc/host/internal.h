@@ -56,6 +56,7 @@ enum GhKernel : int {
     K_ATTN_G2,
     K_ATTN_MFMA_G4,
     K_ATTN_MFMA_G8,
+    K_ATTN_MFMA_G4_S16,
     // prefill GEMM tile variants (tokens x rows per workgroup), Q4_K then Q6_K
     K_GEMM_REDUCE,
     K_GEMM_TAIL,

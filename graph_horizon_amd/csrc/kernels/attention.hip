@@ -143,7 +143,7 @@ struct AttnShared {
     uint32_t last;
 };
 
-template <int G>
+template <int G, uint32_t MS = kMaxSplits>
 __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& hot, AttnShared<G>& sh,
                                             uint32_t nsplit);
 
@@ -216,7 +216,9 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
 // the output; with several splits the last workgroup of the (row, kv head) merges them:
 //   M = max m_w, L = Σ l_w e^{m_w - M}, ACC = Σ acc_w e^{m_w - M}, then across splits
 //   out = Σ_s e^{m_s-M} acc_s / Σ_s e^{m_s-M} l_s.
-template <int G>
+// MS: split slots the merge reads (the launch's split count is at most MS); slots past nsplit
+// re-read the last split and get weight 0, which leaves every sum's bits unchanged.
+template <int G, uint32_t MS>
 __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& hot, AttnShared<G>& sh,
                                             uint32_t nsplit) {
     auto& wm = sh.wm;
@@ -277,13 +279,13 @@ __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& 
     // nsplit re-read split nsplit - 1 and get weight 0; unconditional loads measured faster
     // than skipping them)
     constexpr uint32_t kOut = (uint32_t)G * 128 / 256;  // outputs per thread (G >= 2)
-    float pv[kOut > 0 ? kOut : 1][kMaxSplits];
+    float pv[kOut > 0 ? kOut : 1][MS];
 #pragma unroll
     for (uint32_t o = 0; o < kOut; ++o) {
         const uint32_t i = tid + 256 * o, h = i >> 7, d = i & 127u;
         const GH_GLOBAL float* pa = gh_gp<float>(a.part_acc) + (pbase + (size_t)h * a.splits) * 128 + d;
 #pragma unroll
-        for (uint32_t j = 0; j < kMaxSplits; ++j) pv[o][j] = ld_agent(pa + (size_t)min(j, nsplit - 1) * 128);
+        for (uint32_t j = 0; j < MS; ++j) pv[o][j] = ld_agent(pa + (size_t)min(j, nsplit - 1) * 128);
     }
     // weights e^{m_s - M} / L per (head, split): lanes are splits, wave h handles head h
     for (uint32_t h = wave; h < (uint32_t)G; h += kWaves) {
@@ -303,7 +305,7 @@ __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& 
             const uint32_t i = tid + 256 * o, h = i >> 7, d = i & 127u;
             float acc_o = 0.0f;
 #pragma unroll
-            for (uint32_t j = 0; j < kMaxSplits; ++j) acc_o += wsplit[h][j] * pv[o][j];
+            for (uint32_t j = 0; j < MS; ++j) acc_o += wsplit[h][j] * pv[o][j];
             gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0 + h) * 128 + d] = gh_f2h(acc_o);
         }
     } else {
@@ -312,7 +314,7 @@ __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& 
             const GH_GLOBAL float* pa = gh_gp<float>(a.part_acc) + pbase * 128 + tid;
             float acc_o = 0.0f;
 #pragma unroll
-            for (uint32_t j = 0; j < kMaxSplits; ++j)
+            for (uint32_t j = 0; j < MS; ++j)
                 acc_o += wsplit[0][j] * ld_agent(pa + (size_t)min(j, nsplit - 1) * 128);
             gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0) * 128 + tid] = gh_f2h(acc_o);
         }
@@ -431,7 +433,7 @@ __device__ __forceinline__ void mchunk_step(const MChunk& r, const dh8 (&qf)[4],
     }
 }
 
-template <int G>
+template <int G, uint32_t MS = kMaxSplits>
 __device__ __forceinline__ void attn_mfma_body(const GhAttnArgs& a, const AttnHot& hot) {
     static_assert(G == 4 || G == 8, "matrix-core decode serves 4 or 8 query heads per kv head");
     __shared__ AttnShared<G> sh;
@@ -492,7 +494,7 @@ __device__ __forceinline__ void attn_mfma_body(const GhAttnArgs& a, const AttnHo
 #pragma unroll
             for (int t = 0; t < 8; ++t) sh.wacc[wave][n][32 * g + 8 * i + t] = acc[t][i];
     }
-    attn_finish<G>(a, hot, sh, nsplit);
+    attn_finish<G, MS>(a, hot, sh, nsplit);
 }
 
 }  // namespace
@@ -505,6 +507,8 @@ GH_KERNEL __launch_bounds__(256) void gh_attn_g1(GH_ATTN_PARAMS) { attn_body<1>(
 GH_KERNEL __launch_bounds__(256) void gh_attn_g2(GH_ATTN_PARAMS) { attn_body<2>(a, GH_ATTN_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4(GH_ATTN_PARAMS) { attn_mfma_body<4>(a, GH_ATTN_HOT); }
 GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g8(GH_ATTN_PARAMS) { attn_mfma_body<8>(a, GH_ATTN_HOT); }
+// launches of at most 16 splits: the merge reads 16 slots instead of 32
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4_s16(GH_ATTN_PARAMS) { attn_mfma_body<4, 16>(a, GH_ATTN_HOT); }
 
 // ---------------------------------------------------------------------------------------------
 // Causal GQA prefill attention on the matrix cores (flash attention, G = 4 query heads per kv
