@@ -139,6 +139,8 @@ struct AttnShared {
     // Σe·V of each wave, per head and value dim; rows padded to 132 floats so that the lanes of
     // the G heads, which store the same value dims at once, do not share banks
     float wacc[kWaves][G][132];
+    float we[kWaves][G];       // e^{m_w - M} per wave and head (the wave merge's weights)
+    float hm[G], hl[G];        // M and L per head
     float wsplit[G][kMaxSplits];
     uint32_t last;
 };
@@ -230,19 +232,30 @@ __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& 
     const uint32_t split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
     const uint32_t h0 = kvh * G;
     __syncthreads();
-    const size_t pbase = ((size_t)row * hot.q_heads + h0) * a.splits;
-    for (uint32_t i = tid; i < (uint32_t)G * 128; i += 256) {
-        const uint32_t h = i >> 7, d = i & 127u;
+    // the waves' weights, M and L once per head (not once per value dim)
+    if (tid < (uint32_t)G) {
+        const uint32_t h = tid;
         float M = -__builtin_inff();
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w][h]);
-        float L = 0.0f, v = 0.0f;
+        float L = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             const float e = wm[w][h] == -__builtin_inff() ? 0.0f : expf(wm[w][h] - M);
+            sh.we[w][h] = e;
             L += e * wl[w][h];
-            v += e * wacc[w][h][d];
         }
+        sh.hm[h] = M;
+        sh.hl[h] = L;
+    }
+    __syncthreads();
+    const size_t pbase = ((size_t)row * hot.q_heads + h0) * a.splits;
+    for (uint32_t i = tid; i < (uint32_t)G * 128; i += 256) {
+        const uint32_t h = i >> 7, d = i & 127u;
+        const float M = sh.hm[h], L = sh.hl[h];
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) v += sh.we[w][h] * wacc[w][h][d];
         if (nsplit == 1) {
             gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0 + h) * 128 + d] = gh_f2h(v / L);
         } else {
