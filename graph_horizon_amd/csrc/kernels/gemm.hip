@@ -8,7 +8,8 @@
 //   gemm3_body (dequantizing; the C3 workload): warp-specialized. Waves 4-7 (producers) keep
 //     the raw weight bytes of 4 units in flight in registers and dequantize each unit into its
 //     LDS stage as FP16, one row per lane; waves 0-3 (consumers) fetch their activation lines
-//     one unit ahead straight into LDS with global_load_lds_dwordx4 and run the MFMA tiles.
+//     one unit ahead (three in the 128-token tiles) straight into LDS with
+//     global_load_lds_dwordx4 and run the MFMA tiles.
 //     Q4_K: w = FP16(RNE(the reference's FP32 dequantized weight)), computed as dequant_row
 //     does ((d·sc)·q - dmin·mn, cpu/dequant.rs:93-123). Q6_K: (q - 32)·(d·sc) as one fused
 //     multiply-add u·da + (-32·da) rounded once to FP16 (v_fma_mix); the reference rounds the
@@ -222,9 +223,13 @@ __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc
 // and dequantize each unit into a kS-stage LDS ring, kS - 1 units ahead of the consumers. One
 // barrier per unit: in the interval of unit u the consumers read stage (u - u0) % kS while the
 // producers fill unit u + kS - 1 into the stage read during unit u - 1.
-// LDS of gemm3_body: kS = 3 weight stages, then each consumer wave's two activation buffers.
-#define GH_GEMM3_LDS(BR) (3 * (BR) * LDK + 4 * 2 * 64 * 64)
-#define GH_GEMM3_LDS_T(BR, WT) (3 * (BR) * LDK + 4 * 2 * (WT) * 64)
+// LDS of gemm3_body: kS = 3 weight stages, then each consumer wave's GH_GEMM3_XB(WT) activation
+// buffers (one unit each: the unit being read and the units in flight behind it). Three units
+// in flight for the 128-token tiles (8B prefill of 128 tokens 6.50 -> 6.45 ms, bit-identical);
+// the 256-token tiles keep one (two measured no faster: 512 x 12288 -> 4096 105 -> 108 us).
+#define GH_GEMM3_XB(WT) ((WT) == 32 ? 4 : 2)
+#define GH_GEMM3_LDS(BR) (3 * (BR) * LDK + 4 * GH_GEMM3_XB(64) * 64 * 64)
+#define GH_GEMM3_LDS_T(BR, WT) (3 * (BR) * LDK + 4 * GH_GEMM3_XB(WT) * (WT) * 64)
 
 // Tile (bx, by) and split bz of one matrix (a.w, a.rows, a.out); lds3 holds GH_GEMM3_LDS(BR)
 // halves; partials go to columns pc .. of rows ps long.
@@ -275,31 +280,39 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     }
 
     // ---- consumers ----
-    // Activations are fetched as whole lines, one unit ahead, straight into the wave's own LDS
-    // rows (only this wave touches them; the per-unit barrier's wait completes the loads), from
-    // which the A fragments are read — each 128-byte line is requested once instead of once per
-    // 16-k step, and no registers hold it on the way (8B prefill gate/up 85 -> 80 us).
+    // Activations are fetched as whole lines straight into the wave's own LDS rows (only this
+    // wave touches them), kXA units ahead of the unit being read, from which the A fragments are
+    // read — each 128-byte line is requested once instead of once per 16-k step, and no
+    // registers hold it on the way. The loads are issued from inline assembly so that the
+    // compiler does not count them: with the builtin, the workgroup fence of every per-unit
+    // barrier waited for all of them (vmcnt(0)), so each unit waited out a full L2 round trip
+    // for the next one. Here each unit waits only until the next unit's lines have landed
+    // (loads complete in issue order; the consumers issue no other memory operations in the
+    // loop), so kXA units stay in flight.
+    constexpr int kXB = GH_GEMM3_XB(WT), kXA = kXB - 1;
     const uint32_t t0 = by * (4 * WT) + wave * WT;
     const uint32_t fm = lane & 31u, fg = lane >> 5;
     const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
-    uint32_t xrow[NX];
+    uint64_t xrow[NX];
 #pragma unroll
-    for (int i = 0; i < NX; ++i) xrow[i] = min(t0 + 8 * i + (lane >> 3), a.n - 1) * a.in_dim;
-    // Activations go straight to LDS (global_load_lds_dwordx4: lane l of a load lands at byte
-    // 16 l of its 1 KiB destination). Load i covers rows 8 i .. 8 i + 7 of the wave's 64; lane
-    // l fetches chunk (l % 8) ^ sw(r) of row r = 8 i + l / 8, so chunk c of row r sits at slot
-    // c ^ sw(r). Every row starts at bank 0 (128-byte pitch); with sw(r) = (r / 2) % 8 a
-    // fragment read (rows fm = 0..31 of one chunk) is free of bank conflicts, as measured with
-    // SQ_LDS_BANK_CONFLICT on gfx950 (sw(r) = (r / 4) % 8 and r % 8 are two-way conflicted:
-    // 7.3 against 3.8 LDS-active cycles per read). Two buffers per wave, one unit each.
-    _Float16* xw = lds3 + kS * BR * LDK + wave * (2 * WT * 64);
+    for (int i = 0; i < NX; ++i)
+        xrow[i] = (uint64_t)(uintptr_t)(x + (uint64_t)min(t0 + 8 * i + (lane >> 3), a.n - 1) * a.in_dim);
+    // global_load_lds_dwordx4: lane l of a load lands at byte 16 l of its 1 KiB destination. Load
+    // i covers rows 8 i .. 8 i + 7 of the wave's WT; lane l fetches chunk (l % 8) ^ sw(r) of row
+    // r = 8 i + l / 8, so chunk c of row r sits at slot c ^ sw(r). Every row starts at bank 0
+    // (128-byte pitch); with sw(r) = (r / 2) % 8 a fragment read (rows fm = 0..31 of one chunk)
+    // is free of bank conflicts, as measured with SQ_LDS_BANK_CONFLICT on gfx950 (sw(r) =
+    // (r / 4) % 8 and r % 8 are two-way conflicted: 7.3 against 3.8 LDS-active cycles per read).
+    _Float16* xw = lds3 + kS * BR * LDK + wave * (kXB * WT * 64);
     auto load_rows = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
             const uint32_t r = 8 * i + (lane >> 3), c = (lane & 7u) ^ ((r >> 1) & 7u);
-            __builtin_amdgcn_global_load_lds((const GH_GLOBAL void*)(x + xrow[i] + chunk_k<FMT>(u, c)),
-                                             (__attribute__((address_space(3))) void*)(xw + b * (WT * 64) + i * 512),
-                                             16, 0, 0);
+            const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(
+                xw + b * (WT * 64) + i * 512);
+            asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(xrow[i] + 2ull * chunk_k<FMT>(u, c)),
+                         "{m0}"(__builtin_amdgcn_readfirstlane(dst))
+                         : "memory");
         }
     };
     f16v acc[TI][TJ];
@@ -307,10 +320,14 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f16v{};
-    load_rows(u0, 0);
+#pragma unroll
+    for (int i = 0; i < kXA; ++i) load_rows(uc(u0 + i), i);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NX * (kXA - 1)) : "memory");  // unit u0 has landed
     __syncthreads();
+    // unit u is read from buffer b = (u - u0) % kXB; unit u + kXA goes into buffer (b + kXA) %
+    // kXB, the one read during unit u - 1 (those reads ended before its barrier)
     auto step = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
-        load_rows(uc(u + 1), b ^ 1u);
+        load_rows(uc(u + kXA), (b + kXA) % kXB);
         __builtin_amdgcn_sched_barrier(0);  // the loads go out before anything waits
         const _Float16* wb = wstage((u - u0) % kS);
         const _Float16* xb = xw + b * (WT * 64);
@@ -330,15 +347,19 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
                 for (int j = 0; j < TJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NX * (kXA - 1)) : "memory");  // unit u + 1 has landed
         __syncthreads();
     };
-    // the unrolled body has no exits (exact wait counts across the back edge); tail after
+    // the unrolled body has no exits and compile-time buffer indices; tail after
     uint32_t u = u0;
-    for (; u + 2 <= u1; u += 2) {
-        step(u, 0);
-        step(u + 1, 1);
+    for (; u + kXB <= u1; u += kXB) {
+#pragma unroll
+        for (int b = 0; b < kXB; ++b) step(u + b, b);
     }
-    if (u < u1) step(u, 0);
+#pragma unroll
+    for (int b = 0; b < kXB - 1; ++b)
+        if (u + b < u1) step(u + b, b);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past u1 have landed
     gemm_write<TI, TJ, true>(a, acc, t0, r0, fm, fg, bz, ps, pc);
 }
 
