@@ -44,6 +44,7 @@ const KernelName kKernels[] = {
     {K_ATTN_MFMA_G8, "gh_attn_mfma_g8"},   {K_ATTN_MFMA_G4_S16, "gh_attn_mfma_g4_s16"},
 
     {K_GEMM_REDUCE, "gh_gemm_reduce"},     {K_GEMM_TAIL, "gh_gemm_tail"},
+    {K_GEMM_REDUCE_SWIGLU, "gh_gemm_reduce_swiglu"},
     {K_GEMM3_MIXED_R128, "gh_gemm3_mixed_r128"},
     {K_GEMM_REDUCE_SEG, "gh_gemm_reduce_seg"},     {K_ATTN_PREFILL_G4, "gh_attn_prefill_g4"},
     {K_ATTN_PREFILL_G4_R16, "gh_attn_prefill_g4_r16"},
@@ -859,56 +860,16 @@ namespace gh {
 constexpr uint32_t kGemmMinTokens = 8;
 constexpr uint32_t kGemmTailMaxRows = 8192;  // gh_gemm_tail: two 16-value items per thread
 
-// One GEMM launch over tr x tt tiles and `splits` K ranges; with splits > 1 the kernel writes
-// FP32 partials to the workspace and gh_gemm_reduce sums them in split order. `e` adds the
-// SiLU epilogue (in the GEMM or the reduce) or replaces the reduce by gh_gemm_tail (residual
-// add and RMSNorm of each output row).
-// w16: the registered FP16 copy of w that the kernel reads instead of w (0: none)
-static int gemm_launch(gh_backend* b, GhKernel k, uint32_t block, uint32_t tr, uint32_t tt,
-                       uint32_t splits, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n,
-                       const GemmEpi* e, uint64_t w16 = 0) {
-    // the kernels give split z the units [z per, min(units, (z + 1) per)), per = ceil(units /
-    // splits): shrink splits to ceil(units / per) until every split is non-empty
-    const uint32_t units = w->cols / 64;
-    for (;;) {
-        const uint32_t per = ceil_div(units, splits), s = ceil_div(units, per);
-        if (s == splits) break;
-        splits = s;
-    }
-    GhGemmArgs ga{};
-    ga.x = a->addr;
-    ga.w = w16 ? w16 : w->addr;
-    ga.out = out;
-    ga.in_dim = w->cols;
-    ga.rows = w->rows;
-    ga.n = n;
-    ga.splits = splits;
-    const bool tail = e && e->resid;
-    if (e && !tail) {
-        ga.epi = e->epi;
-        ga.aux = e->aux;
-    }
-    if (splits > 1) {
-        int rc = ensure_workspace(b, (size_t)splits * n * w->rows * 4);
-        if (rc) return rc;
-        ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
-    }
-    int rc = launch(b, k, tr, tt, splits, block, &ga);
-    if (!rc && tail) {
-        ga.aux = e->resid;
-        ga.norm = e->norm;
-        ga.normed = e->normed;
-        ga.eps = e->eps;
-        return launch(b, K_GEMM_TAIL, n, 1, 1, 256, &ga);
-    }
-    if (rc || splits == 1) return rc;
-    const uint64_t total = (uint64_t)n * w->rows;
-    return launch(b, K_GEMM_REDUCE, (uint32_t)std::min<uint64_t>(ceil_div(total, (uint64_t)256), 4096), 1, 1,
-                  256, &ga);
-}
+// The launch plan of one GEMM: kernel, row and token tiles, and K splits (every split
+// non-empty); w16 is the registered FP16 copy of w that the kernel reads instead (0: none).
+struct GemmPlan {
+    GhKernel k;
+    uint32_t tr, tt, splits;
+    uint64_t w16;
+};
 
-int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n, const GemmEpi* e) {
-    const uint32_t in_dim = w->cols, rows = w->rows, units = in_dim / 64;
+static GemmPlan plan_gemm(gh_backend* b, const gh_buf* w, uint32_t n) {
+    const uint32_t rows = w->rows, units = w->cols / 64;
     // splits: at most 16 and at least 8 units of 64 k per split
     auto clamp_splits = [&](uint32_t s) {
         return std::max<uint32_t>(1, std::min<uint32_t>({s, std::max<uint32_t>(1, units / 8), 16u}));
@@ -940,8 +901,108 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         k = br == 96 ? (q4 ? K_GEMM4W_Q4K_R96 : K_GEMM4W_Q6K_R96) : (q4 ? K_GEMM4W_Q4K_R128 : K_GEMM4W_Q6K_R128);
     const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
     const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
-    const uint32_t splits = clamp_splits(std::max<uint32_t>(1, slots / tiles));
-    return gemm_launch(b, k, 512, tr, tt, splits, out, a, w, n, e, w16);
+    uint32_t splits = clamp_splits(std::max<uint32_t>(1, slots / tiles));
+    // the kernels give split z the units [z per, min(units, (z + 1) per)), per = ceil(units /
+    // splits): shrink splits to ceil(units / per) until every split is non-empty
+    for (;;) {
+        const uint32_t per = ceil_div(units, splits), s = ceil_div(units, per);
+        if (s == splits) break;
+        splits = s;
+    }
+    return GemmPlan{k, tr, tt, splits, w16};
+}
+
+// The GEMM kernel of plan p alone; with p.splits > 1 its FP32 partials [splits][n][rows] go to
+// `part` (which holds p.splits * n * rows floats).
+static int gemm_kernel(gh_backend* b, const GemmPlan& p, uint64_t out, uint64_t part, const gh_buf* a,
+                       const gh_buf* w, uint32_t n, uint32_t epi = GH_GEMM_EPI_F16, uint64_t aux = 0) {
+    GhGemmArgs ga{};
+    ga.x = a->addr;
+    ga.w = p.w16 ? p.w16 : w->addr;
+    ga.out = out;
+    ga.part = part;
+    ga.in_dim = w->cols;
+    ga.rows = w->rows;
+    ga.n = n;
+    ga.splits = p.splits;
+    ga.epi = epi;
+    ga.aux = aux;
+    return launch(b, p.k, p.tr, p.tt, p.splits, 512, &ga);
+}
+
+// One GEMM launch over its plan's tiles and K splits; with splits > 1 the kernel writes FP32
+// partials to the workspace and gh_gemm_reduce sums them in split order. `e` adds the SiLU
+// epilogue (in the GEMM or the reduce) or replaces the reduce by gh_gemm_tail (residual add
+// and RMSNorm of each output row).
+int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n, const GemmEpi* e) {
+    const GemmPlan p = plan_gemm(b, w, n);
+    const bool tail = e && e->resid;
+    const uint32_t epi = e && !tail ? e->epi : GH_GEMM_EPI_F16;
+    const uint64_t aux = e && !tail ? e->aux : 0;
+    uint64_t part = 0;
+    if (p.splits > 1) {
+        int rc = ensure_workspace(b, (size_t)p.splits * n * w->rows * 4);
+        if (rc) return rc;
+        part = (uint64_t)((char*)b->ws + kArgmaxBytes);
+    }
+    int rc = gemm_kernel(b, p, out, part, a, w, n, epi, aux);
+    if (rc) return rc;
+    GhGemmArgs ga{};
+    ga.out = out;
+    ga.part = part;
+    ga.rows = w->rows;
+    ga.n = n;
+    ga.splits = p.splits;
+    if (tail) {
+        ga.aux = e->resid;
+        ga.norm = e->norm;
+        ga.normed = e->normed;
+        ga.eps = e->eps;
+        return launch(b, K_GEMM_TAIL, n, 1, 1, 256, &ga);
+    }
+    if (p.splits == 1) return GH_OK;
+    ga.epi = epi;
+    ga.aux = aux;
+    const uint64_t total = (uint64_t)n * w->rows;
+    return launch(b, K_GEMM_REDUCE, (uint32_t)std::min<uint64_t>(ceil_div(total, (uint64_t)256), 4096), 1, 1,
+                  256, &ga);
+}
+
+// SwiGLU's two projections of one input: out = silu_mul(f16(x wg^T), f16(x wu^T)). Where the
+// GEMMs split K, both write their partials and one reduce (gh_gemm_reduce_swiglu) rounds each
+// sum to FP16 and applies silu_mul; otherwise the up GEMM applies it in its epilogue to the
+// gate's FP16 output in `gate`. The values of op_gemm(gate), op_gemm(up) and silu_mul.
+int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const gh_buf* a, const gh_buf* wg,
+                   const gh_buf* wu, uint32_t n) {
+    if (!is_weight(wg) || !is_weight(wu) || wg->rows != wu->rows || wg->cols != wu->cols)
+        return fail(b, GH_E_INVALID, "gemm swiglu: gate and up of one shape");
+    if (n < kGemmMinTokens) return fail(b, GH_E_UNSUPPORTED, "gemm swiglu: GEMM path only");
+    const uint64_t cells = (uint64_t)n * wg->rows;
+    if (!fits(a, (uint64_t)n * wg->cols * 2) || !fits(out, cells * 2) || !fits(gate, cells * 2))
+        return fail(b, GH_E_RANGE, "gemm swiglu: buffer too small");
+    const GemmPlan pg = plan_gemm(b, wg, n), pu = plan_gemm(b, wu, n);
+    if (pg.splits == 1 || pu.splits != pg.splits || wg->rows % 4) {
+        GemmEpi e;
+        e.epi = GH_GEMM_EPI_SILU;
+        e.aux = gate->addr;
+        int rc = op_gemm(b, gate->addr, a, wg, n);
+        return rc ? rc : op_gemm(b, out->addr, a, wu, n, &e);
+    }
+    const size_t half = (size_t)pg.splits * cells * 4;
+    int rc = ensure_workspace(b, 2 * half);
+    if (rc) return rc;
+    const uint64_t part = (uint64_t)((char*)b->ws + kArgmaxBytes);
+    rc = gemm_kernel(b, pg, 0, part, a, wg, n);
+    if (!rc) rc = gemm_kernel(b, pu, 0, part + half, a, wu, n);
+    if (rc) return rc;
+    GhGemmArgs ga{};
+    ga.out = out->addr;
+    ga.part = part;
+    ga.rows = wg->rows;
+    ga.n = n;
+    ga.splits = pg.splits;
+    return launch(b, K_GEMM_REDUCE_SWIGLU, (uint32_t)std::min<uint64_t>(ceil_div(cells / 4, (uint64_t)256), 4096), 1,
+                  1, 256, &ga);
 }
 
 // The SiLU epilogue and the tail apply to every GEMM (n >= kGemmMinTokens).

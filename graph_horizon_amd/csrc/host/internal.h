@@ -60,6 +60,7 @@ enum GhKernel : int {
     // prefill GEMM tile variants (tokens x rows per workgroup), Q4_K then Q6_K
     K_GEMM_REDUCE,
     K_GEMM_TAIL,
+    K_GEMM_REDUCE_SWIGLU,
     K_GEMM3_MIXED_R128,
     K_GEMM_REDUCE_SEG,
     K_ATTN_PREFILL_G4,
@@ -217,6 +218,11 @@ struct GemmEpi {
 int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint32_t n,
             const GemmEpi* e = nullptr);
 bool gemm_epi_applies(uint32_t n, uint32_t out_dim, bool tail);
+// SwiGLU's gate and up projections of one FP16 input (n >= 8 tokens) and silu_mul, with one
+// split reduce for both GEMMs where they split K; `gate` receives the gate's FP16 output only
+// where they do not. The values of op_gemm(gate), op_gemm(up) and silu_mul.
+int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const gh_buf* a, const gh_buf* wg,
+                   const gh_buf* wu, uint32_t n);
 // gh_matmul_batched with an epilogue (checked buffers): gate != nullptr selects the SiLU
 // epilogue; resid != nullptr the residual add, and norm/normed the RMSNorm after it.
 int op_matmul_epi(gh_backend* b, const gh_buf* out, const gh_buf* a, const gh_buf* w, uint32_t in_dim,

@@ -206,9 +206,10 @@ bool fusable(const gh_model* m, uint32_t li) {
 // One transformer layer over `rows` packed rows at absolute positions base + r
 // (+ *pos_ptr when the position lives on the device). With `normed` (prefill), the GEMM path's
 // epilogues carry the glue: the O and down projections' output rows go straight into the
-// residual and the following RMSNorm (gh_gemm_tail), the up projection applies silu_mul to the
-// gate; *normed on return says the next layer's attention norm is already in s.normed. The
-// values are those of the separate ops below.
+// residual and the following RMSNorm (gh_gemm_tail), silu_mul is applied in the gate and up
+// projections' shared split reduce (or the up projection's epilogue); *normed on return says
+// the next layer's attention norm is already in s.normed. The values are those of the
+// separate ops below.
 int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t base,
           uint32_t rows, const void* pos_ptr, bool* normed = nullptr) {
     if (rows == 1 && fusable(m, li)) return layer_decode_fused(m, enc, s, li, base, pos_ptr);
@@ -272,10 +273,11 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
         if (!rc) rc = gh_rmsnorm_x(b, enc, &s.normed, &s.x, &w[GH_T_FFN_NORM], d, c.rms_epsilon, rows);
     }
     gh_no_barrier(b);
-    if (!rc) rc = gh_matmul_batched(b, enc, &s.gate, &s.normed, &w[GH_T_FFN_GATE], d, ffn, rows);
     if (fuse && gemm_epi_applies(rows, ffn, false)) {
-        if (!rc) rc = op_matmul_epi(b, &s.act, &s.normed, &w[GH_T_FFN_UP], d, ffn, rows, &s.gate, nullptr);
+        // gate, up and silu_mul: where the GEMMs split K, one reduce for both
+        if (!rc) rc = op_gemm_swiglu(b, &s.act, &s.gate, &s.normed, &w[GH_T_FFN_GATE], &w[GH_T_FFN_UP], rows);
     } else {
+        if (!rc) rc = gh_matmul_batched(b, enc, &s.gate, &s.normed, &w[GH_T_FFN_GATE], d, ffn, rows);
         if (!rc) rc = gh_matmul_batched(b, enc, &s.up, &s.normed, &w[GH_T_FFN_UP], d, ffn, rows);
         if (!rc) rc = gh_silu_mul(b, enc, &s.act, &s.gate, &s.up, ffn * rows);
     }

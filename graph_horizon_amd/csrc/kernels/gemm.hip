@@ -32,8 +32,8 @@
 //
 // Split-K (grid.z > 1): each split covers a contiguous range of units and writes FP32
 // partials [split][n][rows]; gh_gemm_reduce sums them in split order and rounds to FP16
-// (gh_gemm_reduce_seg and gh_gemm_tail fold the prefill driver's RoPE, K/V-cache writes,
-// residual add and RMSNorm into that sum).
+// (gh_gemm_reduce_seg, gh_gemm_reduce_swiglu and gh_gemm_tail fold the prefill driver's RoPE,
+// K/V-cache writes, silu_mul, residual add and RMSNorm into that sum).
 #include "gh_common.h"
 
 namespace {
@@ -615,6 +615,35 @@ GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce(GhGemmArgs a) {
         float s = 0.0f;
         for (uint32_t k = 0; k < a.splits; ++k) s += gh_gp<float>(a.part)[k * total + i];
         gemm_store(a, i, s);
+    }
+}
+
+// SwiGLU's gate and up GEMMs reduced together: partials [2][splits][n][rows] (the gate's, then
+// the up projection's), each sum taken in split order and rounded to FP16 as gh_gemm_reduce
+// rounds it, then out = silu_mul(gate, up) (gh_silu_mul_h, elementwise/activation.rs:16-29):
+// the bits of gh_gemm_reduce on the gate followed by the up reduce with the SiLU epilogue.
+// Four adjacent outputs per thread (rows is a multiple of 4).
+GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce_swiglu(GhGemmArgs a) {
+    const uint64_t nq = (uint64_t)a.n * a.rows / 4;
+    // launched with min(ceil(nq / 256), 4096) workgroups of 256
+    const uint64_t groups = min((nq + 255) / 256, (uint64_t)4096);
+    const GH_GLOBAL float4* p = gh_gp<float4>(a.part);
+    for (uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x; q < nq; q += groups * 256) {
+        float4 g = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u = g;
+        for (uint32_t z = 0; z < a.splits; ++z) {
+            const float4 pg = p[z * nq + q], pu = p[(a.splits + z) * nq + q];
+            g.x += pg.x;
+            g.y += pg.y;
+            g.z += pg.z;
+            g.w += pg.w;
+            u.x += pu.x;
+            u.y += pu.y;
+            u.z += pu.z;
+            u.w += pu.w;
+        }
+        const uint32_t o0 = gh_silu_mul_h(gh_f2h(g.x), gh_f2h(u.x)) | ((uint32_t)gh_silu_mul_h(gh_f2h(g.y), gh_f2h(u.y)) << 16);
+        const uint32_t o1 = gh_silu_mul_h(gh_f2h(g.z), gh_f2h(u.z)) | ((uint32_t)gh_silu_mul_h(gh_f2h(g.w), gh_f2h(u.w)) << 16);
+        gh_gpw<uint2>(a.out)[q] = make_uint2(o0, o1);
     }
 }
 

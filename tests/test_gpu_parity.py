@@ -555,18 +555,21 @@ def test_fused_decode_is_bit_identical_to_op_by_op(hip, shape_name):
 
 
 @pytest.mark.parametrize("n", [37, 300])
-def test_prefill_driver_is_bit_identical_to_op_by_op(hip, n):
+@pytest.mark.parametrize("shape_name", ["tiny", "small"])
+def test_prefill_driver_is_bit_identical_to_op_by_op(hip, shape_name, n):
     """The driver's prefill (one batch: GEMV for n < 8 rows, the MFMA GEMMs above, the
     warp-specialized ones from 256 rows, with the glue folded into GEMM epilogues and split
     reduces and Q/K/V in one launch) leaves the same logits and KV bits as recording every
     trait op separately (prefill::record_batch over the C ABI). The tiny shape's GEMMs run one
-    K split each, so the fused and the separate launches sum in the same order; where the split
-    counts differ (the 8B shape's Q/K/V: 2 in the fused launch, 4/16/16 alone) the results
-    differ only by FP32 re-association, checked against the oracle in test_gpu_model_shapes."""
+    K split each and the small shape's two (four for down), alike in the fused and the separate
+    launches, so both sum in the same order; the small shape's gate and up GEMMs then share one
+    split reduce that applies silu_mul (gh_gemm_reduce_swiglu). Where the split counts differ
+    (the 8B shape's Q/K/V launch against the three projections alone) the results differ only
+    by FP32 re-association, checked against the oracle in test_gpu_model_shapes."""
     from graph_horizon_amd import HipModel
     from graph_over_abi import AbiGraph
 
-    shape = synth.SHAPES["tiny"]
+    shape = synth.SHAPES[shape_name]
     ctx = 320
     ref = AbiGraph(hip, shape, 43, ctx)
     gm = HipModel(hip, synth.model_config(shape, ctx, 512))
