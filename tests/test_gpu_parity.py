@@ -455,6 +455,31 @@ def test_model_prefill_matches_oracle(hip):
     om.close()
 
 
+@pytest.mark.parametrize("n", [8, 32, 128])
+def test_model_prefill_short_chunk_matches_oracle(hip, n):
+    """A prompt of n rows in one chunk (8: the smallest GEMM batch; 32; 128: one full 128-token
+    tile) on the small shape, whose GEMMs split K (gate and up through their shared SiLU reduce,
+    Q/K/V through the RoPE reduce, O and down through the residual tails), against the oracle's
+    prefill of the same prompt: the logits and every K/V cache row the chunk wrote."""
+    shape, ctx = synth.SHAPES["small"], 160
+    gm, om = _models(hip, "small", 33, ctx, prefill_rows=128)
+    toks = list(np.random.default_rng(50 + n).integers(0, shape.vocab_size, n))
+    gm.prefill(toks, 0)
+    om.prefill(toks, 0, 128)
+    got, want = gm.read_logits(), om.logits()
+    assert np.abs(want).max() > 0.1
+    assert np.allclose(got, want, rtol=2e-2, atol=2e-2)
+    kv = gm.kv()
+    kvw = shape.kv_head_count * shape.head_dim
+    m = shape.block_count * ctx * kvw
+    for role, buf in ((0, kv.k), (1, kv.v)):
+        dev = O.f32(hip.download(buf, np.uint16, m)).reshape(shape.block_count, ctx, kvw)[:, :n]
+        ora = O.f32(om.kv(role)).reshape(shape.block_count, ctx, kvw)[:, :n]
+        assert np.max(np.abs(dev - ora)) <= 2e-2 * max(float(np.abs(ora).max()), 1.0), role
+    gm.close()
+    om.close()
+
+
 def test_model_prefill_policy_chunks(hip):
     """prefill_rows = 0 takes gh_prefill_rows (2048-row chunks): a 2500-token prompt in two
     chunks (2048 + 452 rows, the second attending across the first) gives the logits and KV
