@@ -870,24 +870,27 @@ struct GemmPlan {
 
 static GemmPlan plan_gemm(gh_backend* b, const gh_buf* w, uint32_t n) {
     const uint32_t rows = w->rows, units = w->cols / 64;
-    // splits: at most 16 and at least 8 units of 64 k per split
+    // Batches of 128 tokens or fewer take 128-token tiles (kGemmTallTokens).
+    const bool tall = n >= kGemmTallTokens;
+    // splits: at most 16, and at least 8 units of 64 k per split (12 in the 128-token tiles,
+    // where a workgroup's fixed costs weigh more: 4096 x 4096 at 128 tokens in 96-row tiles x 5
+    // splits 22.2 us against 26.0 in 128-row tiles x 8 splits of 8 units)
+    const uint32_t min_units = tall ? 8u : 12u;
     auto clamp_splits = [&](uint32_t s) {
-        return std::max<uint32_t>(1, std::min<uint32_t>({s, std::max<uint32_t>(1, units / 8), 16u}));
+        return std::max<uint32_t>(1, std::min<uint32_t>({s, std::max<uint32_t>(1, units / min_units), 16u}));
     };
     const bool q4 = w->format == GH_FMT_Q4_K;
     // Row height (measured at 512 tokens on the 8B and 14B shapes): one workgroup per CU,
-    // s = CUs / tiles splits, and the height whose tiles x splits fill the CUs' last wave
-    // better — 96 rows for 12288 x 4096 (256 tiles against 192 of 128 rows), 128 rows
-    // otherwise. Narrow outputs (<= 1024 rows) take 96 rows with two workgroups per CU
-    // and up to 16 splits: their few units per split leave latency for a second to hide.
-    // Batches of 128 tokens or fewer take 128-token tiles (kGemmTallTokens).
-    const bool tall = n >= kGemmTallTokens;
+    // s = CUs / tiles splits (clamped as above), and the height whose tiles x splits fill the
+    // CUs' last wave better — 96 rows for 12288 x 4096 (256 tiles against 192 of 128 rows),
+    // 128 rows otherwise. Narrow outputs (<= 1024 rows) take 96 rows with two workgroups per
+    // CU and up to 16 splits: their few units per split leave latency for a second to hide.
     const uint32_t tt = ceil_div(n, tall ? 256u : 128u), cus = b->cus;
     // a registered FP16 copy of w: the same sums with the weights copied, not dequantized
     const auto copy = b->w16.find(w->addr);
     const uint64_t w16 = copy == b->w16.end() || !tall ? 0 : copy->second;
     auto fill = [&](uint32_t br) {
-        const uint32_t t = ceil_div(rows, br) * tt, s = std::max<uint32_t>(1, cus / t);
+        const uint32_t t = ceil_div(rows, br) * tt, s = clamp_splits(std::max<uint32_t>(1, cus / t));
         const uint64_t ts = (uint64_t)t * s;
         return (double)ts / ((double)cus * (double)ceil_div(ts, cus));
     };
@@ -1067,8 +1070,11 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
     bool copies = tall;
     for (uint32_t i = 0; i < nseg; ++i) copies = copies && b->w16.count(segs[i].w->addr);
     const uint32_t tt = ceil_div(n, tall ? 256u : 128u), units = in_dim / 64;
-    // splits: the CUs over the tiles, at most 16 and at least 8 units per split, none empty
-    uint32_t splits = std::max<uint32_t>(1, std::min<uint32_t>({b->cus / (tiles * tt), std::max<uint32_t>(1, units / 8), 16u}));
+    // splits: the CUs over the tiles, at most 16 and at least 8 units per split (12 in the
+    // 128-token tiles, as op_gemm), none empty
+    const uint32_t min_units = tall ? 8u : 12u;
+    uint32_t splits =
+        std::max<uint32_t>(1, std::min<uint32_t>({b->cus / (tiles * tt), std::max<uint32_t>(1, units / min_units), 16u}));
     for (;;) {
         const uint32_t per = ceil_div(units, splits), s = ceil_div(units, per);
         if (s == splits) break;

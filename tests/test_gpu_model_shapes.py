@@ -107,7 +107,10 @@ def test_full_width_prefill_driver_matches_op_by_op(hip, name, n):
     cache. The fused Q/K/V launch splits K differently (2 against 4 and 8), so a few values
     round to the neighbouring FP16; one block keeps that from being amplified by a second
     block of random weights (whose residual grows to thousands and whose attention is nearly
-    one-hot), and every difference is bounded against the tensor's scale."""
+    one-hot), and every difference is bounded against the tensor's scale. On the 8B shape at
+    100 rows (one 128-token tile) every GEMM splits K alike in the fused and the separate
+    launches on MI355X's 256 CUs (Q/K/V five splits each), so the driver, gate and up through
+    their shared SiLU reduce included, is bit-identical there."""
     from graph_over_abi import AbiGraph
 
     shape = dataclasses.replace(synth.SHAPES[name], name=f"{name}-1", block_count=1)
@@ -123,9 +126,12 @@ def test_full_width_prefill_driver_matches_op_by_op(hip, name, n):
     gm.prefill(toks, 0)
     got = gm.read_logits()
     assert np.isfinite(got).all()
+    d = shape.embedding_length
+    if name == "8b" and n <= 128:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert np.array_equal(gm.read_x().view(np.uint32), ref.prefill_x[(n - 1) * d:].view(np.uint32))
     scale = max(np.abs(want).max(), 1.0)
     assert np.max(np.abs(got - want)) <= 2e-3 * scale, np.max(np.abs(got - want)) / scale
-    d = shape.embedding_length
     xw = ref.prefill_x[(n - 1) * d:].astype(np.float64)
     xg = gm.read_x().astype(np.float64)
     assert np.max(np.abs(xg - xw)) <= 2e-3 * max(np.abs(xw).max(), 1.0)

@@ -458,9 +458,9 @@ def test_model_prefill_matches_oracle(hip):
 @pytest.mark.parametrize("n", [8, 32, 128])
 def test_model_prefill_short_chunk_matches_oracle(hip, n):
     """A prompt of n rows in one chunk (8: the smallest GEMM batch; 32; 128: one full 128-token
-    tile) on the small shape, whose GEMMs split K (gate and up through their shared SiLU reduce,
-    Q/K/V through the RoPE reduce, O and down through the residual tails), against the oracle's
-    prefill of the same prompt: the logits and every K/V cache row the chunk wrote."""
+    tile) on the small shape (the down GEMM splits K, its residual tail summing the splits),
+    against the oracle's prefill of the same prompt: the logits and every K/V cache row the
+    chunk wrote."""
     shape, ctx = synth.SHAPES["small"], 160
     gm, om = _models(hip, "small", 33, ctx, prefill_rows=128)
     toks = list(np.random.default_rng(50 + n).integers(0, shape.vocab_size, n))
@@ -586,9 +586,10 @@ def test_prefill_driver_is_bit_identical_to_op_by_op(hip, shape_name, n):
     warp-specialized ones from 256 rows, with the glue folded into GEMM epilogues and split
     reduces and Q/K/V in one launch) leaves the same logits and KV bits as recording every
     trait op separately (prefill::record_batch over the C ABI). The tiny shape's GEMMs run one
-    K split each and the small shape's two (four for down), alike in the fused and the separate
-    launches, so both sum in the same order; the small shape's gate and up GEMMs then share one
-    split reduce that applies silu_mul (gh_gemm_reduce_swiglu). Where the split counts differ
+    K split each; the small shape's run one (two for down) at 37 rows and two (four for down)
+    at 300, alike in the fused and the separate launches, so both sum in the same order; at 300
+    rows its gate and up GEMMs share one split reduce that applies silu_mul
+    (gh_gemm_reduce_swiglu). Where the split counts differ
     (the 8B shape's Q/K/V launch against the three projections alone) the results differ only
     by FP32 re-association, checked against the oracle in test_gpu_model_shapes."""
     from graph_horizon_amd import HipModel
