@@ -12,7 +12,8 @@ Also reported on the same line:
   roofline      the metric's GEMV: Q4_K 4096x4096 with x ~ N(0,1), launched back to
                 back over the model's 68 distinct Q and O weights (642 MB, beyond the 256 MB
                 MALL), timed with HIP events on the backend stream;
-  config        the 12288x4096 gate/up-shape GEMV, the C3 prefill GEMMs, a 2048-token prefill
+  config        the 12288x4096 gate/up-shape GEMV, the C3 prefill GEMMs, a 128-token prefill
+                (a short prompt: one chunk over the Q4_K/Q6_K weights), a 2048-token prefill
                 (one chunk of the policy's size, over the FP16 weight copies), the C4 attention
                 cases and the C5 14B-shaped decoder (512-token prefill, greedy decode);
   cpu_baseline  the CPU oracle (a C++ restatement of the reference's AVX2 CPU kernels) on all
@@ -281,6 +282,7 @@ def main():
         "roofline": roofline,
     }
     result["config"]["prefill_gemm_c3"] = prefill_gemm(hip, model, shape, tensors, 512)
+    result["config"]["prefill_128"] = prefill_short(hip, model, shape, 128)
     model.close()
     result["config"]["prefill_2048"] = prefill_long(hip, HipModel, shape, tensors, 2048)
     result["config"]["attention_c4"] = c4_attention(hip)
@@ -581,6 +583,23 @@ def vendor_gemm(shape, sizes=(128, 512, 2048), reps=6):
         torch.cuda.empty_cache()
     print(json.dumps({"vendor_gemm": out}), flush=True)
     hip.close()
+
+
+def prefill_short(hip, model, shape, n):
+    """A short prompt (one chunk of n <= 128 rows: the 128-token GEMM tiles over the Q4_K/Q6_K
+    weights, no FP16 copies) at position 0 of the bench's model, after its decode leg: the
+    median of three timed prefills after an untimed one."""
+    prompt = np.random.default_rng(13).integers(0, shape.vocab_size, n).astype(np.uint32)
+    model.prefill(prompt, 0)
+    times = []
+    for _ in range(3):
+        hip.synchronize()
+        hip.timer_start()
+        model.prefill(prompt, 0)
+        times.append(hip.timer_stop())
+    ms = float(np.median(times))
+    log(f"bench: prefill {n} tokens (short prompt) in {ms:.3f} ms ({n / (ms / 1e3):.0f} tok/s)")
+    return {"tokens": n, "ms": round(ms, 3), "tok_s": round(n / (ms / 1e3), 1), "fp16_weight_copies": False}
 
 
 def prefill_long(hip, HipModel, shape, tensors, n):
