@@ -3,8 +3,9 @@
 //             (block.rs:17-107), mlp::record (mlp.rs:12-61), tail::record (tail.rs:11-59);
 //   prefill — prefill::prefill / record_batch (graph/prefill/encode.rs:16-106) and
 //             prefill::layer::record (prefill/layer.rs:18-122).
-// The greedy loop replays one captured HIP graph per token: the token id and position live in
-// device memory, the step ends with an on-device argmax that becomes the next step's input.
+// The greedy loop replays a captured HIP graph per token (one graph per range of positions):
+// the token id and position live in device memory, the step ends with an on-device argmax that
+// becomes the next step's input.
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
@@ -18,6 +19,21 @@ using namespace gh;
 
 namespace {
 constexpr uint32_t kNoLayer = 0xFFFFFFFFu;
+
+// Decode steps run from graphs captured per position range: each range's attention launch is
+// sized for the range's last position (one split per 64-position chunk, at most 32), so a step
+// at a short position of a long cache does not launch the idle splits of the whole context
+// (at most a fifth of a range's splits idle from 256 positions on). Ranges end at these
+// positions and at the cache's context (from 2048 positions the split count is 32 anyway; a
+// forced split count, gh_set_attention_splits, keeps one range over the whole context).
+constexpr uint32_t kStepRangeEnds[] = {64, 128, 192, 256, 320, 384, 512, 640, 768, 1024, 1280, 1536, 2048};
+constexpr uint32_t kStepRanges = sizeof(kStepRangeEnds) / sizeof(kStepRangeEnds[0]) + 1;
+
+struct StepGraph {
+    hipGraphExec_t exec = nullptr;
+    hipGraph_t graph = nullptr;
+    uint64_t gen = 0;  // backend generation the graph was captured against
+};
 
 struct Scratch {  // backend/buffers.rs:17-29, sized for `rows` token rows
     gh_buf x, normed, q, k, v, attn, proj, gate, up, act, ffn_out;
@@ -37,9 +53,8 @@ struct gh_model {
     gh_kv kv{};
     GhRopeTable rope;  // this model's YaRN table for positions 0 .. kv_context - 1
     std::vector<gh_buf> owned;
-    hipGraphExec_t step = nullptr;
-    hipGraph_t step_graph = nullptr;
-    uint64_t step_gen = 0;  // backend generation the step graph was captured against
+    std::array<StepGraph, kStepRanges> steps{};  // decode step graphs by position range
+    uint32_t step_len = 0;  // positions the decode step being recorded serves (0: the context)
     uint32_t last_rows = 0;  // rows of the most recent pass (for read_x)
     bool last_prefill = false;
     // FP16 copies of the layer matrices for the prefill GEMMs (registered in b->w16), made
@@ -185,7 +200,7 @@ int layer_decode_fused(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t 
     const gh_buf *xin = nullptr, *nw = nullptr;
     int rc = normed(&w[GH_T_ATTN_NORM], &xin, &nw);
     if (!rc) rc = op_gemv(b, qkv, 3, xin, 1, base, pos_ptr, c.key_length, nullptr, nw, c.rms_epsilon, &m->rope);
-    const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base;
+    const uint32_t max_pos = pos_ptr ? (m->step_len ? m->step_len : m->kv.context) - 1 : base;
     if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, 1, li, pos_ptr, max_pos);
     const GemvSeg o{&w[GH_T_ATTN_OUTPUT], s.x.addr, GH_EPI_RESID};
     if (!rc) rc = op_gemv(b, &o, 1, &s.attn, 1, 0, nullptr, 0, nullptr);
@@ -260,7 +275,7 @@ int layer(gh_model* m, gh_encoder* enc, const Scratch& s, uint32_t li, uint32_t 
         if (!rc) rc = op_rope(b, m->rope, &s.k, c.kv_head_count, c.key_length, base, rows, GH_ROPE_KEY, pos_ptr);
         if (!rc) rc = op_kv_write(b, &m->kv, &s.k, &s.v, koff, voff, rows * c.kv_head_count, pos_ptr);
     }
-    const uint32_t max_pos = pos_ptr ? m->kv.context - 1 : base + rows - 1;
+    const uint32_t max_pos = pos_ptr ? (m->step_len ? m->step_len : m->kv.context) - 1 : base + rows - 1;
     if (!rc) rc = op_attention(b, &s.attn, &s.q, &m->kv, c.head_count, base, rows, li, pos_ptr, max_pos);
     if (fuse && gemm_epi_applies(rows, d, true)) {
         // out-projection, residual add and mlp::record's norm in one GEMM + tail
@@ -335,10 +350,72 @@ int record_step(gh_model* m, gh_encoder* enc) {
     return rc;
 }
 
-// Runs `steps` decode steps from (token, pos): the captured step graph replayed (captured on
-// first use, again after the backend's workspace or RoPE table moved), or with
-// GH_MODEL_NO_GRAPH the same kernels launched on the stream. Each step leaves its logits,
-// its argmax in history[pos] and the next (token, pos) in m->scalars.
+// End (exclusive) of decode position range k; the range of position pos.
+uint32_t step_range_end(const gh_model* m, uint32_t k) {
+    const uint32_t ctx = m->kv.context;
+    if (m->b->attn_splits || k + 1 >= kStepRanges) return ctx;
+    return std::min(kStepRangeEnds[k], ctx);
+}
+
+uint32_t step_range(const gh_model* m, uint32_t pos) {
+    uint32_t k = 0;
+    while (k + 1 < kStepRanges && pos >= step_range_end(m, k)) ++k;
+    return k;
+}
+
+void destroy_steps(gh_model* m) {
+    for (StepGraph& g : m->steps) {
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        if (g.graph) (void)hipGraphDestroy(g.graph);
+        g = StepGraph{};
+    }
+}
+
+// The step graph of position range k, captured on first use and again after the backend's
+// workspace or RoPE table moved.
+int ensure_step(gh_model* m, uint32_t k) {
+    gh_backend* b = m->b;
+    StepGraph& sg = m->steps[k];
+    if (sg.exec && sg.gen != b->gen) {
+        (void)hipGraphExecDestroy(sg.exec);
+        (void)hipGraphDestroy(sg.graph);
+        sg = StepGraph{};
+    }
+    if (sg.exec) return GH_OK;
+    // size the attention partials and merge counters for the whole context's split count in
+    // force now (gh_set_attention_splits may have raised it since gh_model_create), so that no
+    // range's capture grows them (which would move the workspace under the other ranges'
+    // graphs): nothing may grow while the capture records
+    const uint32_t splits = attention_splits(b, m->kv.context, m->cfg.kv_head_count, 1);
+    int rc = ensure_workspace(b, attention_workspace(1, m->cfg.head_count, splits));
+    if (!rc) rc = ensure_counters(b, m->cfg.kv_head_count);
+    if (rc) return rc;
+    gh_encoder* enc = nullptr;
+    rc = gh_begin(b, &enc);
+    if (rc) return rc;
+    rc = hip_check(b, hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    if (!rc) {
+        b->capturing = true;
+        m->step_len = step_range_end(m, k);
+        int rec = record_step(m, enc);
+        m->step_len = 0;
+        b->capturing = false;
+        hipGraph_t g = nullptr;
+        int end = hip_check(b, hipStreamEndCapture(b->stream, &g), "hipStreamEndCapture");
+        rc = rec ? rec : end;
+        if (!rc) rc = hip_check(b, hipGraphInstantiate(&sg.exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+        if (rc && g) (void)hipGraphDestroy(g);
+        else sg.graph = g;
+        sg.gen = b->gen;
+    }
+    b->enc_open = false;
+    return rc;
+}
+
+// Runs `steps` decode steps from (token, pos): the step graphs of the positions' ranges
+// replayed, or with GH_MODEL_NO_GRAPH the same kernels launched on the stream. Each step leaves
+// its logits, its argmax in history[pos] and the next (token, pos) in m->scalars, from which
+// the next step (in the same graph or the next range's) continues.
 int run_steps(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps) {
     gh_backend* b = m->b;
     const uint32_t init[4] = {pos, token, 0, 0};
@@ -347,7 +424,11 @@ int run_steps(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps) {
         rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
         gh_encoder* enc = nullptr;
         if (!rc) rc = gh_begin(b, &enc);
-        for (uint32_t i = 0; i < steps && !rc; ++i) rc = record_step(m, enc);
+        for (uint32_t i = 0; i < steps && !rc; ++i) {
+            m->step_len = step_range_end(m, step_range(m, pos + i));  // the graph's split grid
+            rc = record_step(m, enc);
+        }
+        m->step_len = 0;
         if (enc) {
             int rs = gh_submit(b, enc);
             rc = rc ? rc : rs;
@@ -356,42 +437,17 @@ int run_steps(gh_model* m, uint32_t token, uint32_t pos, uint32_t steps) {
         m->last_prefill = false;
         return rc;
     }
-    if (m->step && m->step_gen != b->gen) {
-        (void)hipGraphExecDestroy(m->step);
-        (void)hipGraphDestroy(m->step_graph);
-        m->step = nullptr;
-        m->step_graph = nullptr;
-    }
-    if (!m->step) {
-        // size the attention partials and merge counters for the split count in force now
-        // (gh_set_attention_splits may have raised it since gh_model_create): nothing may grow
-        // while the capture records
-        const uint32_t splits = attention_splits(b, m->kv.context, m->cfg.kv_head_count, 1);
-        rc = ensure_workspace(b, attention_workspace(1, m->cfg.head_count, splits));
-        if (!rc) rc = ensure_counters(b, m->cfg.kv_head_count);
-        if (rc) return rc;
-        gh_encoder* enc = nullptr;
-        rc = gh_begin(b, &enc);
-        if (rc) return rc;
-        rc = hip_check(b, hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-        if (!rc) {
-            b->capturing = true;
-            int rec = record_step(m, enc);
-            b->capturing = false;
-            hipGraph_t g = nullptr;
-            int end = hip_check(b, hipStreamEndCapture(b->stream, &g), "hipStreamEndCapture");
-            rc = rec ? rec : end;
-            if (!rc) rc = hip_check(b, hipGraphInstantiate(&m->step, g, nullptr, nullptr, 0), "hipGraphInstantiate");
-            if (rc && g) (void)hipGraphDestroy(g);
-            else m->step_graph = g;
-            m->step_gen = b->gen;
-        }
-        b->enc_open = false;
-        if (rc) return rc;
-    }
-    rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
+    // every range the steps cross is captured before the first replay; a capture that grew the
+    // workspace (which moves it) leaves the ranges captured before it stale, so they are
+    // captured again (the second pass grows nothing: every capture sizes for the context)
+    const uint32_t k0 = step_range(m, pos), k1 = step_range(m, pos + steps - 1);
+    for (int pass = 0; pass < 2 && !rc; ++pass)
+        for (uint32_t k = k0; k <= k1 && !rc; ++k) rc = ensure_step(m, k);
+    for (uint32_t k = k0; k <= k1 && !rc; ++k)
+        if (m->steps[k].gen != b->gen) rc = fail(b, GH_E_STATE, "decode: step graphs kept moving");
+    if (!rc) rc = gh_upload(b, &m->scalars, 0, init, sizeof(init));
     for (uint32_t i = 0; i < steps && !rc; ++i)
-        rc = hip_check(b, hipGraphLaunch(m->step, b->stream), "hipGraphLaunch");
+        rc = hip_check(b, hipGraphLaunch(m->steps[step_range(m, pos + i)].exec, b->stream), "hipGraphLaunch");
     m->last_rows = 1;
     m->last_prefill = false;
     return rc;
@@ -490,8 +546,7 @@ int gh_model_create(gh_backend* b, const gh_model_config* cfg, gh_model** out) {
 void gh_model_destroy(gh_model* m) {
     if (!m) return;
     free_w16(m);
-    if (m->step) (void)hipGraphExecDestroy(m->step);
-    if (m->step_graph) (void)hipGraphDestroy(m->step_graph);
+    destroy_steps(m);
     for (gh_buf& buf : m->owned) gh_free_buffer(m->b, &buf);
     for (auto& l : m->layers)
         for (gh_buf& w : l)
@@ -536,12 +591,7 @@ int gh_model_load_tensor(gh_model* m, uint32_t layer_index, uint32_t tensor, uin
     free_w16(m);  // made again from the new weights by the next long prefill
     m->w16_failed = false;
     if (slot->addr) gh_free_buffer(m->b, slot);
-    if (m->step) {
-        (void)hipGraphExecDestroy(m->step);
-        (void)hipGraphDestroy(m->step_graph);
-        m->step = nullptr;
-        m->step_graph = nullptr;
-    }
+    destroy_steps(m);
     return gh_load_weight(m->b, format, bytes, len, in, out, slot);
 }
 

@@ -177,23 +177,28 @@ def test_greedy_graph_with_forced_splits_matches_stream(hip):
 
 
 def test_graph_replay_ignores_partials_of_earlier_steps(hip):
-    """The replayed decode graph's attention grid is fixed (4 splits at a 256-position
-    context), while the splits in use follow the position. A run that crosses position 64
-    (two splits in use) leaves real partials and merge state behind; replaying the first steps
-    again (one split in use) must give the first run's tokens."""
+    """A replayed decode graph whose attention grid is fixed at 4 splits (forced: one step
+    graph over the whole 256-position context), while the splits in use follow the position.
+    A run that crosses position 64 (two splits in use) leaves real partials and merge state
+    behind; replaying the first steps again (one split in use) must give the first run's
+    tokens."""
     from graph_horizon_amd import HipModel, synth
 
     shape = synth.SHAPES["tiny"]
-    gm = HipModel(hip, synth.model_config(shape, 256, 64))
-    for layer, tid, fmt, data in synth.model_tensors(shape, 33):
-        gm.load_tensor(layer, tid, fmt, data)
-    prompt = [3, 99, 1500, 42]
-    gm.prefill(prompt, 0)
-    first = gm.read_argmax()
-    short = gm.decode_greedy(first, 4, 8)
-    gm.prefill(prompt, 0)
-    long = gm.decode_greedy(first, 4, 70)
-    gm.prefill(prompt, 0)
-    again = gm.decode_greedy(first, 4, 8)
-    gm.close()
+    hip.set_attention_splits(4)
+    try:
+        gm = HipModel(hip, synth.model_config(shape, 256, 64))
+        for layer, tid, fmt, data in synth.model_tensors(shape, 33):
+            gm.load_tensor(layer, tid, fmt, data)
+        prompt = [3, 99, 1500, 42]
+        gm.prefill(prompt, 0)
+        first = gm.read_argmax()
+        short = gm.decode_greedy(first, 4, 8)
+        gm.prefill(prompt, 0)
+        long = gm.decode_greedy(first, 4, 70)
+        gm.prefill(prompt, 0)
+        again = gm.decode_greedy(first, 4, 8)
+        gm.close()
+    finally:
+        hip.set_attention_splits(0)
     assert np.array_equal(long[:8], short) and np.array_equal(again, short)

@@ -536,18 +536,21 @@ def test_model_rejects_bad_inputs(hip):
     gm.close()
 
 
-def test_greedy_decode_stream_launch_equals_graph(hip):
-    """GH_MODEL_NO_GRAPH launches the same step kernels directly: identical tokens."""
+@pytest.mark.parametrize("ctx,prompt,steps", [(64, 3, 20), (300, 60, 80)])
+def test_greedy_decode_stream_launch_equals_graph(hip, ctx, prompt, steps):
+    """GH_MODEL_NO_GRAPH launches the same step kernels directly: identical tokens. The second
+    case decodes positions 60..139 of a 300-position cache, across the decode step graphs'
+    position ranges (ends 64 and 128: 1, 2 and then 4 attention splits), both ways."""
     from graph_horizon_amd import HipModel
 
     shape = synth.SHAPES["tiny"]
     outs = []
     for flags in (0, F.MODEL_NO_GRAPH):
-        gm = HipModel(hip, synth.model_config(shape, 64, 16, flags=flags))
+        gm = HipModel(hip, synth.model_config(shape, ctx, 64, flags=flags))
         for layer, tid, fmt, data in synth.model_tensors(shape, 35):
             gm.load_tensor(layer, tid, fmt, data)
-        gm.prefill([4, 5, 6], 0)
-        outs.append(gm.decode_greedy(9, 3, 20))
+        gm.prefill(list(range(4, 4 + prompt)), 0)
+        outs.append(gm.decode_greedy(9, prompt, steps))
         gm.close()
     assert np.array_equal(outs[0], outs[1])
 
