@@ -31,6 +31,8 @@ const KernelName kKernels[] = {
     {K_GEMV_Q6K_R1_N, "gh_gemv_q6k_r1_n"}, {K_GEMV_Q6K_R2_N, "gh_gemv_q6k_r2_n"},
     {K_GEMV_MIXED_R2_N, "gh_gemv_mixed_r2_n"},
     {K_GEMV_SWIGLU_R1_N, "gh_gemv_swiglu_r1_n"}, {K_GEMV_SWIGLU_R2_N, "gh_gemv_swiglu_r2_n"},
+    {K_GEMV_Q4K_R2_NW, "gh_gemv_q4k_r2_nw"},     {K_GEMV_Q6K_R2_NW, "gh_gemv_q6k_r2_nw"},
+    {K_GEMV_MIXED_R2_NW, "gh_gemv_mixed_r2_nw"}, {K_GEMV_SWIGLU_R2_NW, "gh_gemv_swiglu_r2_nw"},
     {K_GEMV_Q4K_R1_D, "gh_gemv_q4k_r1_d"}, {K_GEMV_Q4K_R2_D, "gh_gemv_q4k_r2_d"},
     {K_GEMV_Q6K_R1_D, "gh_gemv_q6k_r1_d"}, {K_GEMV_Q6K_R2_D, "gh_gemv_q6k_r2_d"},
     {K_GEMV_Q4K_R1_K, "gh_gemv_q4k_r1_k"}, {K_GEMV_Q4K_R2_K, "gh_gemv_q4k_r2_k"},
@@ -560,6 +562,17 @@ int op_gemv(gh_backend* b, const GemvSeg* segs, uint32_t nseg, const gh_buf* x, 
             case K_GEMV_SWIGLU_R1: k = K_GEMV_SWIGLU_R1_N; break;
             case K_GEMV_SWIGLU_R2: k = K_GEMV_SWIGLU_R2_N; break;
             default: return fail(b, GH_E_UNSUPPORTED, "gemv: no RMSNorm variant");
+        }
+        // rows of 65-128 units: both chunks of a task requested at once (same bits)
+        const uint32_t units = in_dim / 64;
+        if (units > 64 && units <= 128) {
+            switch (k) {
+                case K_GEMV_Q4K_R2_N: k = K_GEMV_Q4K_R2_NW; break;
+                case K_GEMV_Q6K_R2_N: k = K_GEMV_Q6K_R2_NW; break;
+                case K_GEMV_MIXED_R2_N: k = K_GEMV_MIXED_R2_NW; break;
+                case K_GEMV_SWIGLU_R2_N: k = K_GEMV_SWIGLU_R2_NW; break;
+                default: break;
+            }
         }
     }
     uint32_t task = 0;

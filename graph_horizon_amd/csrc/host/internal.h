@@ -32,6 +32,10 @@ enum GhKernel : int {
     K_GEMV_MIXED_R2_N,
     K_GEMV_SWIGLU_R1_N,
     K_GEMV_SWIGLU_R2_N,
+    K_GEMV_Q4K_R2_NW,
+    K_GEMV_Q6K_R2_NW,
+    K_GEMV_MIXED_R2_NW,
+    K_GEMV_SWIGLU_R2_NW,
     // direct-x variants (single token, one matrix, in_dim <= 4096, no RMSNorm)
     K_GEMV_Q4K_R1_D,
     K_GEMV_Q4K_R2_D,

@@ -460,7 +460,10 @@ __device__ __forceinline__ uint32_t i_end(const GhGemvArgs& a, const GhHot& h, u
 // together before any arithmetic; lanes past the last unit re-read the last unit (addresses
 // stay valid, loads stay unconditional so the wait counts stay exact) and add nothing.
 // `primed`: the caller already loaded the first chunk of the first task into wa.
-template <uint32_t FMT, int R, int M>
+// W2 (rows of 65-128 units, in_dim 4160..8192): both chunks' weights are requested before
+// either is computed, into two register sets, so a task waits on one memory round trip instead
+// of two (the same per-lane order of the sums, so the same bits).
+template <uint32_t FMT, int R, int M, bool W2 = false>
 __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg& sg,
                                             uint32_t first, uint32_t stride, uint32_t ntask,
                                             uint32_t t, uint32_t nb, const uint4* xs,
@@ -480,15 +483,27 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
         EpiIn<R> ei;
-        for (uint32_t c = 0; c < nch; ++c) {
-            const uint32_t u = c * 64 + lane, uc = min(u, units - 1);
-            if (!primed) load_step<FMT, R, M>(w, sg.rows, nb, k * R, uc, wa);
+        if constexpr (W2) {
+            WRow<FMT> wb[M][R];
+            const uint32_t u1 = 64 + lane;
+            if (!primed) load_step<FMT, R, M>(w, sg.rows, nb, k * R, lane, wa);
             primed = false;
-            if (c == 0) {
-                __builtin_amdgcn_sched_barrier(0);  // the weights go out before anything waits
-                epi_load<R, M == 2>(a, sg, t, k * R, pos, ei);
+            load_step<FMT, R, M>(w, sg.rows, nb, k * R, min(u1, units - 1), wb);
+            __builtin_amdgcn_sched_barrier(0);  // the weights go out before anything waits
+            epi_load<R, M == 2>(a, sg, t, k * R, pos, ei);
+            compute_step<FMT, R, M>(xs, sums, units, lane, mk, wa, acc);
+            if (u1 < units) compute_step<FMT, R, M>(xs, sums, units, u1, mk, wb, acc);
+        } else {
+            for (uint32_t c = 0; c < nch; ++c) {
+                const uint32_t u = c * 64 + lane, uc = min(u, units - 1);
+                if (!primed) load_step<FMT, R, M>(w, sg.rows, nb, k * R, uc, wa);
+                primed = false;
+                if (c == 0) {
+                    __builtin_amdgcn_sched_barrier(0);  // the weights go out before anything waits
+                    epi_load<R, M == 2>(a, sg, t, k * R, pos, ei);
+                }
+                if (u < units) compute_step<FMT, R, M>(xs, sums, units, u, mk, wa, acc);
             }
-            if (u < units) compute_step<FMT, R, M>(xs, sums, units, u, mk, wa, acc);
         }
         float v[M][R];
 #pragma unroll
@@ -508,7 +523,7 @@ __device__ __forceinline__ void run_segment(const GhGemvArgs& a, const GhGemvSeg
 // 8B decode at 567-576 tok/s against 589-592 (605 against 628 with the norm weights also
 // requested up front), and an L2 warm-up of the first task (one dword per load) in place of
 // priming was slower still; for the output GEMV priming measured neutral.
-template <int R, int MODE, bool NORM, bool PRIME = !NORM>
+template <int R, int MODE, bool NORM, bool PRIME = !NORM, bool W2 = false>
 __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
     // The position (RoPE / KV-cache epilogues) is read first: loads complete in issue order,
     // so read at the epilogue it waited for every weight load issued before it (the QKV
@@ -652,16 +667,17 @@ __device__ __forceinline__ void gemv_body(const GhGemvArgs& a, const GhHot& h) {
         }
         __syncthreads();
         if constexpr (MODE == kModeQ6) {
-            run_segment<kQ6K, R, M>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r, pos_all);
+            run_segment<kQ6K, R, M, W2>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r, pos_all);
         } else if constexpr (MODE == kModeMixed) {
             if (sg.fmt == kQ4K) {
-                run_segment<kQ4K, R, M>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r, pos_all);
+                run_segment<kQ4K, R, M, W2>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r,
+                                            pos_all);
             } else {
                 WRow<kQ6K> w6[M][R];
-                run_segment<kQ6K, R, M>(a, sg, first, nw, ntask, t, nb, xs6, xsum6, mk, false, w6, pos_all);
+                run_segment<kQ6K, R, M, W2>(a, sg, first, nw, ntask, t, nb, xs6, xsum6, mk, false, w6, pos_all);
             }
         } else {
-            run_segment<kQ4K, R, M>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r, pos_all);
+            run_segment<kQ4K, R, M, W2>(a, sg, first, nw, ntask, t, nb, xs4, xsum4, mk, primed && t == 0, w0r, pos_all);
         }
     }
 }
@@ -835,6 +851,20 @@ GH_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gh
 }
 GH_GEMV(gh_gemv_swiglu_r1, 1, kModeSwiglu)
 GH_GEMV(gh_gemv_swiglu_r2, 2, kModeSwiglu)
+// RMSNorm kernels for rows of 65-128 units (in_dim 4160..8192, e.g. the 14B shape's 5120): both
+// 64-unit chunks of a task requested at once (suffix _nw)
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q4k_r2_nw(GH_HOT_PARAMS) {
+    gemv_body<2, kModeQ4, true, false, true>(a, GH_HOT);
+}
+GH_KERNEL __launch_bounds__(256) void gh_gemv_q6k_r2_nw(GH_HOT_PARAMS) {
+    gemv_body<2, kModeQ6, true, false, true>(a, GH_HOT);
+}
+GH_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gh_gemv_mixed_r2_nw(GH_HOT_PARAMS) {
+    gemv_body<2, kModeMixed, true, false, true>(a, GH_HOT);
+}
+GH_KERNEL __launch_bounds__(256) void gh_gemv_swiglu_r2_nw(GH_HOT_PARAMS) {
+    gemv_body<2, kModeSwiglu, true, false, true>(a, GH_HOT);
+}
 // direct-x variants (suffix _d): single token, one matrix, in_dim <= 4096, no RMSNorm
 GH_KERNEL __launch_bounds__(512) void gh_gemv_q4k_r1_d(GH_HOT_PARAMS) { gemv_direct<1, kQ4K>(a, GH_HOT); }
 GH_KERNEL __launch_bounds__(512) void gh_gemv_q4k_r2_d(GH_HOT_PARAMS) { gemv_direct<2, kQ4K>(a, GH_HOT); }
