@@ -248,10 +248,11 @@ def main():
         tok, pos = int(out[-1]), pos + args.warmup
     hip.synchronize()
     hip.timer_start()
-    model.decode_greedy(tok, pos, args.steps)
+    toks = model.decode_greedy(tok, pos, args.steps)
     ms = hip.timer_stop()
     tok_s = args.steps / (ms / 1e3)
     log(f"bench: {args.steps} decode steps in {ms:.2f} ms -> {tok_s:.1f} tok/s")
+    merge_ab = xcd_merge_ab(hip, model, tok, pos, args.steps, args.warmup, toks, tok_s)
 
     roofline = c1_roofline(hip, model, shape)
     result = {
@@ -278,6 +279,7 @@ def main():
                         "tok_s": round(args.prompt / (prefill_ms / 1e3), 1)},
             "decode_weight_roofline_frac": round(per_token * tok_s / (HBM_PEAK_GBPS * 1e9), 4),
             "q4k_gemv_12288x4096": gemv_gate_shape(hip, model, shape),
+            "attention_merge_ab": merge_ab,
         },
         "roofline": roofline,
     }
@@ -294,6 +296,28 @@ def main():
         result["cpu_baseline"] = cpu_baseline(shape, tensors, kv_host, kv_context, args.prompt,
                                               first, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def xcd_merge_ab(hip, model, tok, pos, steps, warmup, toks, tok_s):
+    """The same decode steps again with decode attention's split merge through device memory
+    instead of one XCD's L2 (same box, same positions): tok/s of both forms, and whether the
+    token streams agree (the two merges give the same bits)."""
+    if not hip.xcd_count:
+        return {"xcds": 0, "note": "dispatch placement not confirmed: device-memory merge only"}
+    hip.set_attention_xcd_merge(False)
+    try:
+        model.decode_greedy(tok, pos, max(warmup, 1))  # records the graphs again
+        hip.synchronize()
+        hip.timer_start()
+        other = model.decode_greedy(tok, pos, steps)
+        ms = hip.timer_stop()
+    finally:
+        hip.set_attention_xcd_merge(True)
+    ab = {"xcds": hip.xcd_count, "xcd_local_tok_s": round(tok_s, 2),
+          "device_memory_tok_s": round(steps / (ms / 1e3), 2),
+          "same_tokens": bool(np.array_equal(toks, other))}
+    log(f"bench: attention merge A/B {json.dumps(ab)}")
+    return ab
 
 
 def model_weight(model, layer, tid):

@@ -123,6 +123,8 @@ SIGNATURES = {
     "gh_timer_stop": (I32, [P, C.POINTER(F32)]),
     "gh_synchronize": (I32, [P]),
     "gh_set_attention_splits": (I32, [P, U32]),
+    "gh_set_attention_xcd_merge": (I32, [P, I32]),
+    "gh_xcd_count": (U32, [P]),
     "gh_stream_probe": (I32, [P, P, BUFP, U64, U64, BUFP, U32]),
     "gh_scratch_info": (I32, [P, C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)]),
     "gh_model_create": (I32, [P, C.POINTER(GhModelConfig), C.POINTER(P)]),

@@ -225,6 +225,16 @@ class HipBackend:
         """Decode attention workgroups per (row, kv head); 0 = the backend's policy."""
         self._ok(self.lib.gh_set_attention_splits(self.h, splits), "set_attention_splits")
 
+    def set_attention_xcd_merge(self, enable: bool):
+        """Decode attention's split merge through one XCD's L2 (True, the default where the
+        start-up probe confirmed the dispatch rule) or through device memory (False)."""
+        self._ok(self.lib.gh_set_attention_xcd_merge(self.h, int(bool(enable))), "set_attention_xcd_merge")
+
+    @property
+    def xcd_count(self) -> int:
+        """XCDs confirmed by the start-up dispatch probe (0: not confirmed)."""
+        return int(self.lib.gh_xcd_count(self.h))
+
 
 class HipModel:
     """The C++ graph driver (gh_model_*): MistralGraph's decode and prefill over the backend."""

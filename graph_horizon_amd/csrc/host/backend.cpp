@@ -61,6 +61,10 @@ const KernelName kKernels[] = {
     {K_GEMM3_Q4K_R128_T128, "gh_gemm3_q4k_r128_t128"}, {K_GEMM3_Q6K_R128_T128, "gh_gemm3_q6k_r128_t128"},
     {K_GEMM3_Q4K_R96_T128, "gh_gemm3_q4k_r96_t128"},   {K_GEMM3_Q6K_R96_T128, "gh_gemm3_q6k_r96_t128"},
     {K_GEMM3_MIXED_R128_T128, "gh_gemm3_mixed_r128_t128"},
+    {K_ATTN_G1_X, "gh_attn_g1_x"},             {K_ATTN_G2_X, "gh_attn_g2_x"},
+    {K_ATTN_MFMA_G4_X, "gh_attn_mfma_g4_x"},   {K_ATTN_MFMA_G8_X, "gh_attn_mfma_g8_x"},
+    {K_ATTN_MFMA_G4_S16_X, "gh_attn_mfma_g4_s16_x"},
+    {K_XCD_PROBE, "gh_xcd_probe"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -311,14 +315,16 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
                  uint32_t q_heads, uint32_t base, uint32_t rows, uint32_t layer,
                  const void* pos_ptr, uint32_t max_pos, const AttnScratch* fixed) {
     const uint32_t group = q_heads / kv->kv_heads;
+    // the XCD-local split merge when the start-up probe confirmed the dispatch rule it needs
+    const bool xl = b->attn_xcd_merge && b->xcds != 0;
     GhKernel k;
     switch (group) {
-        case 1: k = K_ATTN_G1; break;
-        case 2: k = K_ATTN_G2; break;
+        case 1: k = xl ? K_ATTN_G1_X : K_ATTN_G1; break;
+        case 2: k = xl ? K_ATTN_G2_X : K_ATTN_G2; break;
         // four or eight query heads per kv head: the matrix-core decode (the K and value dims
         // are 128, which check_attention and the model enforce)
-        case 4: k = K_ATTN_MFMA_G4; break;
-        case 8: k = K_ATTN_MFMA_G8; break;
+        case 4: k = xl ? K_ATTN_MFMA_G4_X : K_ATTN_MFMA_G4; break;
+        case 8: k = xl ? K_ATTN_MFMA_G8_X : K_ATTN_MFMA_G8; break;
         default: return fail(b, GH_E_UNSUPPORTED, "attention: GQA group must be 1, 2, 4 or 8");
     }
     // Batched prefill on the matrix cores: 32-row query blocks x kv heads (G = 4, head 128).
@@ -351,6 +357,10 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
     const uint32_t splits = attention_splits(b, max_pos + 1, kv->kv_heads, rows);
     // the merge of a launch of at most 16 splits reads 16 slots (same bits, half the loads)
     if (k == K_ATTN_MFMA_G4 && splits <= 16) k = K_ATTN_MFMA_G4_S16;
+    if (k == K_ATTN_MFMA_G4_X && splits <= 16) k = K_ATTN_MFMA_G4_S16_X;
+    // the kernels take the head counts and the launch's rows as 16-bit fields
+    if (q_heads > 0xFFFFu || kv->kv_heads > 0xFFFFu)
+        return fail(b, GH_E_UNSUPPORTED, "attention: more than 65535 heads");
     char* ws = nullptr;
     void* counters = nullptr;
     uint32_t group_rows = rows;
@@ -365,7 +375,7 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         // bound the partials: rows in groups that fit a 256 MiB workspace
         const size_t per_row = attention_workspace(1, q_heads, splits);
         group_rows = (uint32_t)std::max<size_t>(1, ((size_t)256 << 20) / per_row);
-        group_rows = std::min(group_rows, rows);
+        group_rows = std::min({group_rows, rows, 0xFFFFu});
         rc = ensure_workspace(b, attention_workspace(group_rows, q_heads, splits));
         if (!rc) rc = ensure_counters(b, (size_t)group_rows * kv->kv_heads);
         if (rc) return rc;
@@ -396,9 +406,13 @@ int op_attention(gh_backend* b, const gh_buf* out, const gh_buf* q, const gh_kv*
         a.splits = splits;
         a.scale = 1.0f / std::sqrt((float)kv->head_dim);
         // leading scalar parameters (preloaded into SGPRs), then the full arguments
-        void* params[] = {&a.q, &a.kc, &a.vc, &a.pos_ptr, &a.layer, &a.context, &a.q_heads, &a.kv_heads, &a};
-        rc = hip_check(b, hipModuleLaunchKernel(b->fn[k], splits, kv->kv_heads, nr, 256, 1, 1, 0, b->stream, params,
-                                                nullptr),
+        uint32_t heads = q_heads | kv->kv_heads << 16, shape = nr | (xl ? b->xcds : 0u) << 16;
+        void* params[] = {&a.q, &a.kc, &a.vc, &a.pos_ptr, &a.layer, &a.context, &heads, &shape, &a};
+        // XL: workgroup (x, split, z) serves the (row, kv head) pair z·xcds + x, so all splits of
+        // a pair share workgroup ids modulo xcds, i.e. one XCD
+        const uint32_t gx = xl ? b->xcds : splits, gy = xl ? splits : kv->kv_heads,
+                       gz = xl ? ceil_div(nr * kv->kv_heads, b->xcds) : nr;
+        rc = hip_check(b, hipModuleLaunchKernel(b->fn[k], gx, gy, gz, 256, 1, 1, 0, b->stream, params, nullptr),
                        "hipModuleLaunchKernel");
         if (rc) return rc;
     }
@@ -628,6 +642,49 @@ using namespace gh;
 
 extern "C" {
 
+// The XCD count when the dispatcher places workgroup i of a launch on XCD i mod n, else 0.
+// Four launches record each workgroup's XCD (gh_xcd_probe): a 1-D grid of 16384 workgroups
+// (more than the device holds at once; n = the XCDs seen), then grids of the XCD-local
+// attention's form (n, splits, groups), whose workgroups must share the XCD of their x.
+uint32_t probe_xcds(gh_backend* b) {
+    constexpr uint32_t kWgs = 16384;
+    void* d = nullptr;
+    if (hipMalloc(&d, kWgs * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    std::vector<uint32_t> h(kWgs);
+    uint32_t n = 0;
+    bool ok = true;
+    const uint32_t shapes[4][3] = {{kWgs, 1, 1}, {0, 9, 1}, {0, 32, 4}, {0, 3, 7}};
+    for (int pass = 0; pass < 4 && ok; ++pass) {
+        const uint32_t gx = pass ? n : shapes[0][0], gy = shapes[pass][1], gz = shapes[pass][2];
+        const uint32_t total = gx * gy * gz;
+        uint64_t out = (uint64_t)d;
+        uint32_t px = gx, py = gy;
+        void* params[] = {&out, &px, &py};
+        ok = hipModuleLaunchKernel(b->fn[K_XCD_PROBE], gx, gy, gz, 64, 1, 1, 0, b->stream, params, nullptr) ==
+                 hipSuccess &&
+             hipMemcpyAsync(h.data(), d, (size_t)total * 4, hipMemcpyDeviceToHost, b->stream) == hipSuccess &&
+             hipStreamSynchronize(b->stream) == hipSuccess;
+        if (!ok) break;
+        if (pass == 0) {
+            std::vector<uint32_t> seen;
+            for (uint32_t i = 0; i < total && seen.size() <= 16; ++i)
+                if (std::find(seen.begin(), seen.end(), h[i]) == seen.end()) seen.push_back(h[i]);
+            n = (uint32_t)seen.size();
+            ok = n >= 1 && n <= 16;
+        }
+        // distinct XCDs for x = 0 .. n-1, and every workgroup on the XCD of its x
+        for (uint32_t i = 0; ok && i < n; ++i)
+            for (uint32_t j = 0; ok && j < i; ++j) ok = h[i] != h[j];
+        for (uint32_t i = 0; ok && i < total; ++i) ok = h[i] == h[i % gx % n];
+    }
+    (void)hipGetLastError();
+    (void)hipFree(d);
+    return ok ? n : 0;
+}
+
 int gh_create(const gh_config* cfg, gh_backend** out) {
     if (!out) return GH_E_INVALID;
     *out = nullptr;
@@ -670,6 +727,10 @@ int gh_create(const gh_config* cfg, gh_backend** out) {
     (void)hipGetLastError();
     if (!rc) rc = ensure_workspace(b, 0);
     if (!rc) rc = noalloc_init(b);
+    if (!rc) {
+        b->xcds = probe_xcds(b);
+        b->attn_xcd_merge = b->xcds != 0;
+    }
     if (rc) {
         gh_destroy(b);
         return rc;
@@ -1365,6 +1426,17 @@ int gh_synchronize(gh_backend* b) {
     if (!b) return GH_E_INVALID;
     return hip_check(b, hipStreamSynchronize(b->stream), "hipStreamSynchronize");
 }
+
+int gh_set_attention_xcd_merge(gh_backend* b, int enable) {
+    if (!b) return GH_E_INVALID;
+    if (enable && !b->xcds)
+        return fail(b, GH_E_UNSUPPORTED, "attention: the device's workgroup-to-XCD placement was not confirmed");
+    b->attn_xcd_merge = enable != 0;
+    ++b->gen;  // recorded decode graphs hold the other kernel
+    return GH_OK;
+}
+
+uint32_t gh_xcd_count(const gh_backend* b) { return b ? b->xcds : 0; }
 
 int gh_set_attention_splits(gh_backend* b, uint32_t splits) {
     if (!b) return GH_E_INVALID;

@@ -89,6 +89,13 @@ enum GhKernel : int {
     K_GEMM3_Q4K_R96_T128,
     K_GEMM3_Q6K_R96_T128,
     K_GEMM3_MIXED_R128_T128,
+    // decode attention, XCD-local split merge (grid (xcds, splits, pair groups))
+    K_ATTN_G1_X,
+    K_ATTN_G2_X,
+    K_ATTN_MFMA_G4_X,
+    K_ATTN_MFMA_G8_X,
+    K_ATTN_MFMA_G4_S16_X,
+    K_XCD_PROBE,
     K_COUNT
 };
 
@@ -127,6 +134,11 @@ struct gh_backend {
     size_t counter_slots = 0;
     GhRopeTable rope;  // the trait ops' table (gh_rope_yarn, gh_rope_yarn_batched)
     uint32_t attn_splits = 0;  // gh_set_attention_splits: 0 = attention_splits' policy
+    // XCDs of the device when its dispatcher was seen to place workgroup i of every probed
+    // launch on XCD i mod xcds (0: not seen; decode attention then merges its splits at agent
+    // scope); attn_xcd_merge: the XCD-local merge is in use (gh_set_attention_xcd_merge)
+    uint32_t xcds = 0;
+    bool attn_xcd_merge = false;
     void* noalloc_scratch = nullptr;  // this device's copy of the no-allocation scratch array
     // FP16 copies of weights (gh_dequant_f16 layout), by the weight's device address: the
     // warp-specialized GEMMs read a registered copy instead of dequantizing (same values).

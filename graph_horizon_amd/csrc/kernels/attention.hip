@@ -18,6 +18,13 @@
 //   out = Σ_s e^{m_s-M} acc_s / Σ_s e^{m_s-M} l_s,  M = max_s m_s
 // — the reference's three-pass softmax-weighted V sum (attention/mod.rs:220-258), re-associated.
 // head_dim = value_dim = 128; splits <= kMaxSplits.
+//
+// XCD-local form (the `_x` kernels): grid (xcds, splits, ceil(rows·kv_heads / xcds)), where
+// workgroup (x, split, z) serves the (row, kv head) pair p = z·xcds + x. The dispatcher hands
+// workgroup i of a launch to XCD i mod xcds (the host verifies this at start-up with
+// gh_xcd_probe and keeps the agent-scope form otherwise), so every split of a pair runs on one
+// XCD and the partials travel through that XCD's L2 — plain stores, which the CU's L1 writes
+// through into the L2, and loads that miss the L1 — instead of through device memory.
 #include "gh_common.h"
 
 namespace {
@@ -117,20 +124,45 @@ __device__ __forceinline__ void chunk_step(const ChunkRegs<G>& r, const uint4 (&
     }
 }
 
-// Agent-scope relaxed atomic accesses for the split partials (see the merge in attn_body).
-__device__ __forceinline__ void st_agent(GH_GLOBAL float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const GH_GLOBAL float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // The decode kernels' first-needed arguments, passed as leading scalar kernel parameters that
 // the dispatch preloads into SGPRs: the query, cache and position loads need no kernarg load.
 struct AttnHot {
     uint64_t q, kc, vc, pos_ptr;
     uint32_t layer, context, q_heads, kv_heads;
+    uint32_t rows, xcds;  // query rows of the launch; XCD count of the XL grid
 };
+
+// The workgroup's split, kv head and query row: from the grid's three axes, or (XL) from the
+// (row, kv head) pair p = z·xcds + x, whose splits run along y. row >= rows marks a
+// workgroup of the last z past the pairs (it exits before any load).
+struct AttnIds {
+    uint32_t split, kvh, row;
+};
+template <bool XL>
+__device__ __forceinline__ AttnIds attn_ids(const GhAttnArgs& a, const AttnHot& hot) {
+    if constexpr (!XL) {
+        return {blockIdx.x, blockIdx.y, blockIdx.z};
+    } else {
+        const uint32_t p = blockIdx.z * hot.xcds + blockIdx.x;
+        return {blockIdx.y, p % hot.kv_heads, p / hot.kv_heads};
+    }
+}
+
+// The split partials' exchange. Agent scope (any placement of the splits): stores written
+// through to the device coherence point and loads that do not hit another XCD's stale L2
+// line. XCD-local (XL, every split of the pair on this XCD): plain stores, which land in the
+// shared L2 (the CU's L1 writes through), and loads that miss the reading CU's L1 (the
+// workgroup-scope atomic load is encoded with sc0, an L1 miss; the data comes from the L2).
+template <bool XL>
+__device__ __forceinline__ void st_part(GH_GLOBAL float* p, float v) {
+    if constexpr (XL) *p = v;
+    else __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool XL>
+__device__ __forceinline__ float ld_part(const GH_GLOBAL float* p) {
+    if constexpr (XL) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Per-wave softmax state of a decode workgroup, merged by attn_finish.
 template <int G>
@@ -145,15 +177,17 @@ struct AttnShared {
     uint32_t last;
 };
 
-template <int G, uint32_t MS = kMaxSplits>
+template <int G, bool XL, uint32_t MS = kMaxSplits>
 __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& hot, AttnShared<G>& sh,
-                                            uint32_t nsplit);
+                                            AttnIds id, uint32_t nsplit);
 
-template <int G>
+template <int G, bool XL>
 __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& hot) {
     __shared__ AttnShared<G> sh;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
+    const AttnIds id = attn_ids<XL>(a, hot);
+    if (XL && id.row >= hot.rows) return;
+    const uint32_t split = id.split, kvh = id.kvh, row = id.row;
     const uint32_t h0 = kvh * G;
     // FP16 query slices [32·qd, +32) of the G heads, as 16 pairs each (issued before the
     // position is known)
@@ -211,7 +245,7 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
         sh.wacc[wave][h][2 * lane] = acc[h][0];
         sh.wacc[wave][h][2 * lane + 1] = acc[h][1];
     }
-    attn_finish<G>(a, hot, sh, nsplit);
+    attn_finish<G, XL>(a, hot, sh, id, nsplit);
 }
 
 // Merge of the four waves' states (in sh) into the workgroup's partial or, with one split,
@@ -220,16 +254,16 @@ __device__ __forceinline__ void attn_body(const GhAttnArgs& a, const AttnHot& ho
 //   out = Σ_s e^{m_s-M} acc_s / Σ_s e^{m_s-M} l_s.
 // MS: split slots the merge reads (the launch's split count is at most MS); slots past nsplit
 // re-read the last split and get weight 0, which leaves every sum's bits unchanged.
-template <int G, uint32_t MS>
+template <int G, bool XL, uint32_t MS>
 __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& hot, AttnShared<G>& sh,
-                                            uint32_t nsplit) {
+                                            AttnIds id, uint32_t nsplit) {
     auto& wm = sh.wm;
     auto& wl = sh.wl;
     auto& wacc = sh.wacc;
     auto& wsplit = sh.wsplit;
     auto& last = sh.last;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
+    const uint32_t split = id.split, kvh = id.kvh, row = id.row;
     const uint32_t h0 = kvh * G;
     __syncthreads();
     // the waves' weights, M and L once per head (not once per value dim)
@@ -260,10 +294,10 @@ __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& 
             gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0 + h) * 128 + d] = gh_f2h(v / L);
         } else {
             const size_t pi = pbase + (size_t)h * a.splits + split;
-            st_agent(gh_gpw<float>(a.part_acc) + pi * 128 + d, v);
+            st_part<XL>(gh_gpw<float>(a.part_acc) + pi * 128 + d, v);
             if (d == 0) {
-                st_agent(gh_gpw<float>(a.part_m) + pi, M);
-                st_agent(gh_gpw<float>(a.part_l) + pi, L);
+                st_part<XL>(gh_gpw<float>(a.part_m) + pi, M);
+                st_part<XL>(gh_gpw<float>(a.part_l) + pi, L);
             }
         }
     }
@@ -298,14 +332,14 @@ __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& 
         const uint32_t i = tid + 256 * o, h = i >> 7, d = i & 127u;
         const GH_GLOBAL float* pa = gh_gp<float>(a.part_acc) + (pbase + (size_t)h * a.splits) * 128 + d;
 #pragma unroll
-        for (uint32_t j = 0; j < MS; ++j) pv[o][j] = ld_agent(pa + (size_t)min(j, nsplit - 1) * 128);
+        for (uint32_t j = 0; j < MS; ++j) pv[o][j] = ld_part<XL>(pa + (size_t)min(j, nsplit - 1) * 128);
     }
     // weights e^{m_s - M} / L per (head, split): lanes are splits, wave h handles head h
     for (uint32_t h = wave; h < (uint32_t)G; h += kWaves) {
         const size_t base = pbase + (size_t)h * a.splits;
         const uint32_t s2 = min(lane, nsplit - 1);
-        const float ms = ld_agent(gh_gp<float>(a.part_m) + base + s2);
-        const float ls = ld_agent(gh_gp<float>(a.part_l) + base + s2);
+        const float ms = ld_part<XL>(gh_gp<float>(a.part_m) + base + s2);
+        const float ls = ld_part<XL>(gh_gp<float>(a.part_l) + base + s2);
         const float M = gh_wave_max(lane < nsplit ? ms : -__builtin_inff());
         const float w = lane < nsplit ? expf(ms - M) : 0.0f;
         const float L = gh_wave_sum(w * ls);
@@ -328,7 +362,7 @@ __device__ __forceinline__ void attn_finish(const GhAttnArgs& a, const AttnHot& 
             float acc_o = 0.0f;
 #pragma unroll
             for (uint32_t j = 0; j < MS; ++j)
-                acc_o += wsplit[0][j] * ld_agent(pa + (size_t)min(j, nsplit - 1) * 128);
+                acc_o += wsplit[0][j] * ld_part<XL>(pa + (size_t)min(j, nsplit - 1) * 128);
             gh_gpw<uint16_t>(a.out)[((size_t)row * hot.q_heads + h0) * 128 + tid] = gh_f2h(acc_o);
         }
     }
@@ -446,12 +480,14 @@ __device__ __forceinline__ void mchunk_step(const MChunk& r, const dh8 (&qf)[4],
     }
 }
 
-template <int G, uint32_t MS = kMaxSplits>
+template <int G, bool XL, uint32_t MS = kMaxSplits>
 __device__ __forceinline__ void attn_mfma_body(const GhAttnArgs& a, const AttnHot& hot) {
     static_assert(G == 4 || G == 8, "matrix-core decode serves 4 or 8 query heads per kv head");
     __shared__ AttnShared<G> sh;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, n = lane & 15u, g = lane >> 4;
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
+    const AttnIds id = attn_ids<XL>(a, hot);
+    if (XL && id.row >= hot.rows) return;
+    const uint32_t split = id.split, kvh = id.kvh, row = id.row;
     const uint32_t h0 = kvh * G;
     // B fragments of the query: head n (zero past G), dims 32 s + 8 g .. + 8
     dh8 qf[4];
@@ -507,21 +543,42 @@ __device__ __forceinline__ void attn_mfma_body(const GhAttnArgs& a, const AttnHo
 #pragma unroll
             for (int t = 0; t < 8; ++t) sh.wacc[wave][n][32 * g + 8 * i + t] = acc[t][i];
     }
-    attn_finish<G, MS>(a, hot, sh, nsplit);
+    attn_finish<G, XL, MS>(a, hot, sh, id, nsplit);
 }
 
 }  // namespace
 
+// heads = q_heads | kv_heads << 16, shape = rows | xcds << 16 (eight leading parameters are
+// preloaded)
 #define GH_ATTN_PARAMS                                                                          \
     uint64_t q, uint64_t kc, uint64_t vc, uint64_t pos_ptr, uint32_t layer, uint32_t context,     \
-        uint32_t q_heads, uint32_t kv_heads, GhAttnArgs a
-#define GH_ATTN_HOT AttnHot{q, kc, vc, pos_ptr, layer, context, q_heads, kv_heads}
-GH_KERNEL __launch_bounds__(256) void gh_attn_g1(GH_ATTN_PARAMS) { attn_body<1>(a, GH_ATTN_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_g2(GH_ATTN_PARAMS) { attn_body<2>(a, GH_ATTN_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4(GH_ATTN_PARAMS) { attn_mfma_body<4>(a, GH_ATTN_HOT); }
-GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g8(GH_ATTN_PARAMS) { attn_mfma_body<8>(a, GH_ATTN_HOT); }
+        uint32_t heads, uint32_t shape, GhAttnArgs a
+#define GH_ATTN_HOT \
+    AttnHot{q, kc, vc, pos_ptr, layer, context, heads & 0xFFFFu, heads >> 16, shape & 0xFFFFu, shape >> 16}
+GH_KERNEL __launch_bounds__(256) void gh_attn_g1(GH_ATTN_PARAMS) { attn_body<1, false>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_g2(GH_ATTN_PARAMS) { attn_body<2, false>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4(GH_ATTN_PARAMS) { attn_mfma_body<4, false>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g8(GH_ATTN_PARAMS) { attn_mfma_body<8, false>(a, GH_ATTN_HOT); }
 // launches of at most 16 splits: the merge reads 16 slots instead of 32
-GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4_s16(GH_ATTN_PARAMS) { attn_mfma_body<4, 16>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4_s16(GH_ATTN_PARAMS) {
+    attn_mfma_body<4, false, 16>(a, GH_ATTN_HOT);
+}
+// the XCD-local forms (grid (xcds, splits, pair groups))
+GH_KERNEL __launch_bounds__(256) void gh_attn_g1_x(GH_ATTN_PARAMS) { attn_body<1, true>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_g2_x(GH_ATTN_PARAMS) { attn_body<2, true>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4_x(GH_ATTN_PARAMS) { attn_mfma_body<4, true>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g8_x(GH_ATTN_PARAMS) { attn_mfma_body<8, true>(a, GH_ATTN_HOT); }
+GH_KERNEL __launch_bounds__(256) void gh_attn_mfma_g4_s16_x(GH_ATTN_PARAMS) {
+    attn_mfma_body<4, true, 16>(a, GH_ATTN_HOT);
+}
+
+// The XCD each workgroup runs on (HW_REG_XCC_ID bits 3:0), at out[linear workgroup id]: the
+// host's start-up check of the dispatcher's workgroup-to-XCD rule.
+GH_KERNEL __launch_bounds__(64) void gh_xcd_probe(uint64_t out, uint32_t gx, uint32_t gy) {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    if (threadIdx.x == 0) gh_gpw<uint32_t>(out)[blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z)] = v & 0xFu;
+}
 
 // ---------------------------------------------------------------------------------------------
 // Causal GQA prefill attention on the matrix cores (flash attention, G = 4 query heads per kv

@@ -211,6 +211,15 @@ int gh_synchronize(gh_backend* b);
  * chunk); 0 restores the backend's policy (about two workgroups per CU). At most 32. Graphs
  * recorded before the call are re-recorded on their next use. */
 int gh_set_attention_splits(gh_backend* b, uint32_t splits);
+/* Decode attention's split merge (no counterpart in the reference: a test and tuning hook).
+ * gh_create checks whether the device's dispatcher places workgroup i of a launch on XCD
+ * i mod n (n = gh_xcd_count, 0 when not confirmed); if so, decode attention runs every split of
+ * a (row, kv head) on one XCD and exchanges the partials through that XCD's L2 (enable = 1, the
+ * default then), else through device memory (enable = 0). The results are the same bits either
+ * way. Enabling without a confirmed placement fails with GH_E_UNSUPPORTED. Graphs recorded
+ * before the call are re-recorded on their next use. */
+int gh_set_attention_xcd_merge(gh_backend* b, int enable);
+uint32_t gh_xcd_count(const gh_backend* b);
 
 /* A plain streaming read of [offset, offset + bytes) of `src` by `workgroups` workgroups of
  * 256 threads (no counterpart in the reference: a measurement kernel). It stands for the

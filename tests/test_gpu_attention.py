@@ -143,15 +143,65 @@ def test_decode_every_forced_split_count(hip, qh, kvh):
     qb, ob = hip.from_host(q), hip.alloc_buffer(qh * 128 * 2)
     cases = [(0, 0), (63, 1), (64, 0), (700, 1), (2047, 1)]
     want = {c: O.f32(O.attention_decode(q, kc, vc, 128, kvh, qh, c[0], c[1], ctx)) for c in cases}
+    modes = [False, True] if hip.xcd_count else [False]
     try:
         for splits in range(1, 33):
             hip.set_attention_splits(splits)
             for pos, layer in cases:
-                hip.attention_decode(ob, qb, kv, qh, pos, layer)
-                got = O.f32(hip.download(ob, np.uint16, qh * 128))
-                _close(got, want[(pos, layer)], f"splits {splits} pos {pos}")
+                bits = []
+                for xcd in modes:  # the split merge through device memory, then one XCD's L2
+                    hip.set_attention_xcd_merge(xcd)
+                    hip.attention_decode(ob, qb, kv, qh, pos, layer)
+                    bits.append(hip.download(ob, np.uint16, qh * 128))
+                    _close(O.f32(bits[-1]), want[(pos, layer)], f"splits {splits} pos {pos} xcd {xcd}")
+                assert all(np.array_equal(b, bits[0]) for b in bits), f"merge forms differ: {splits} {pos}"
     finally:
         hip.set_attention_splits(0)
+        hip.set_attention_xcd_merge(bool(hip.xcd_count))
+    _free(hip, qb, ob, kv.k, kv.v)
+
+
+def test_xcd_probe_confirms_the_mi355x_dispatch():
+    """The start-up probe sees the eight XCDs of an MI355X (256 CUs) in one partition and
+    workgroup i of each probed launch on XCD i mod 8, so decode attention merges its splits
+    through one XCD's L2 by default."""
+    from graph_horizon_amd import HipBackend
+
+    with HipBackend() as b:
+        print(f"xcd_count {b.xcd_count}")
+        assert b.xcd_count == 8
+
+
+@pytest.mark.parametrize("qh,kvh,n", [(12, 3, 7), (64, 8, 5), (32, 8, 20), (16, 16, 3)],
+                         ids=["g4-kv3", "g8", "g4-rows20", "g1-kv16"])
+def test_multi_row_decode_kernels_xcd_grid(hip, qh, kvh, n):
+    """Rows below the matrix-core prefill's minimum (or groups it does not serve) run the
+    decode kernels with several query rows. In the XCD-local grid the (row, kv head) pairs fill
+    z-groups of xcds, the last one partly (kv_heads 3: 21 pairs): both merge forms give the
+    same bits, within the oracle bar, at every split count the row lengths allow."""
+    if not hip.xcd_count:
+        pytest.skip("dispatch placement not confirmed on this device")
+    rng = np.random.default_rng(qh * 7 + kvh + n)
+    ctx, base = 1024, 600
+    kc = O.f16(rng.standard_normal(ctx * kvh * 128).astype(np.float32))
+    vc = O.f16(rng.standard_normal(ctx * kvh * 128).astype(np.float32))
+    q = O.f16(rng.standard_normal(n * qh * 128).astype(np.float32))
+    kv = _kv(hip, 1, ctx, kvh, kc, vc)
+    qb, ob = hip.from_host(q), hip.alloc_buffer(n * qh * 128 * 2)
+    want = O.f32(O.attention_prefill(q, kc, vc, 128, kvh, qh, base, n, 0, ctx))
+    try:
+        for splits in (0, 1, 5, 11):
+            hip.set_attention_splits(splits)
+            bits = []
+            for xcd in (False, True):
+                hip.set_attention_xcd_merge(xcd)
+                hip.attention_prefill(ob, qb, kv, qh, base, n, 0)
+                bits.append(hip.download(ob, np.uint16, n * qh * 128))
+                _close(O.f32(bits[-1]), want, f"splits {splits} xcd {xcd}")
+            assert np.array_equal(bits[0], bits[1]), f"merge forms differ at {splits} splits"
+    finally:
+        hip.set_attention_splits(0)
+        hip.set_attention_xcd_merge(True)
     _free(hip, qb, ob, kv.k, kv.v)
 
 
