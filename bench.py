@@ -180,6 +180,9 @@ def main():
                     help="calibration only: the vendor library's dense FP16 GEMM (torch.matmul, "
                          "hipBLASLt) at the C3 shapes beside this build's dequantizing GEMMs, "
                          "same box, same timing")
+    ap.add_argument("--probe-tokens", type=int, default=512,
+                    help="token rows of --gemm-probe's GEMMs (512: the C3 shape; 8-128 run the "
+                         "128-token tiles)")
     ap.add_argument("--probe-bytes", default="9437184,94371840",
                     help="comma-separated read sizes for --floor-probe")
     ap.add_argument("--probe-groups", default="256,512,1024,2048",
@@ -197,7 +200,7 @@ def main():
         traffic_probe(synth.SHAPES["8b"])
         return
     if args.gemm_probe:
-        gemm_probe(synth.SHAPES["8b"])
+        gemm_probe(synth.SHAPES["8b"], args.probe_tokens)
         return
     if args.floor_probe:
         floor_probe([int(v) for v in args.probe_bytes.split(",")],

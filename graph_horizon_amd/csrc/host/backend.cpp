@@ -979,10 +979,10 @@ static GemmPlan plan_gemm(gh_backend* b, const gh_buf* w, uint32_t n) {
     const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
     const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
     uint32_t splits = clamp_splits(std::max<uint32_t>(1, slots / tiles));
-    // the kernels give split z the units [z per, min(units, (z + 1) per)), per = ceil(units /
-    // splits): shrink splits to ceil(units / per) until every split is non-empty
+    // the kernels give split z the units [z per, min(units, (z + 1) per)), per = whole blocks
+    // (gh_gemm_split_units): shrink splits to ceil(units / per) until every split is non-empty
     for (;;) {
-        const uint32_t per = ceil_div(units, splits), s = ceil_div(units, per);
+        const uint32_t per = gh_gemm_split_units(units, splits), s = ceil_div(units, per);
         if (s == splits) break;
         splits = s;
     }
@@ -1150,7 +1150,7 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
     uint32_t splits =
         std::max<uint32_t>(1, std::min<uint32_t>({b->cus / (tiles * tt), std::max<uint32_t>(1, units / min_units), 16u}));
     for (;;) {
-        const uint32_t per = ceil_div(units, splits), s = ceil_div(units, per);
+        const uint32_t per = gh_gemm_split_units(units, splits), s = ceil_div(units, per);
         if (s == splits) break;
         splits = s;
     }

@@ -5,11 +5,12 @@
 // one 64-weight unit per stage through a 3-stage LDS ring, one barrier per unit, with
 // v_mfma_f32_32x32x16_f16 tiles (A = activations, M = tokens; B = weights, N = rows; FP32
 // accumulators). Two forms:
-//   gemm3_body (dequantizing; the C3 workload): warp-specialized. Waves 4-7 (producers) keep
-//     the raw weight bytes of 4 units in flight in registers and dequantize each unit into its
-//     LDS stage as FP16, one row per lane; waves 0-3 (consumers) fetch their activation lines
-//     one unit ahead (three in the 128-token tiles) straight into LDS with
-//     global_load_lds_dwordx4 and run the MFMA tiles.
+//   gemm3_body (dequantizing; the C3 workload): warp-specialized. Waves 4-7 (producers) fetch
+//     the raw weight bytes of their rows a 256-weight block (4 units) at a time, the next block
+//     in flight while the current one is dequantized, and write each unit into its LDS stage as
+//     FP16, one row per lane; waves 0-3 (consumers) fetch their activation lines one unit
+//     ahead (three in the 128-token tiles) straight into LDS with global_load_lds_dwordx4 and
+//     run the MFMA tiles. K splits start and end on block boundaries (gh_gemm_split_units).
 //     Q4_K: w = FP16(RNE(the reference's FP32 dequantized weight)), computed as dequant_row
 //     does ((d·sc)·q - dmin·mn, cpu/dequant.rs:93-123). Q6_K: (q - 32)·(d·sc) as one fused
 //     multiply-add u·da + (-32·da) rounded once to FP16 (v_fma_mix); the reference rounds the
@@ -79,6 +80,44 @@ __device__ __forceinline__ void load_w(const GhGemmArgs& a, uint32_t r0, uint32_
         ws.qh = *gh_gp<uint4>(rq + 2ull * nb * 64);
         ws.hd = *gh_gp<uint4>(a.w + (uint64_t)a.rows * GH_Q6K_QLH_BYTES * nb + blk * 16);
         ws.d = *gh_gp<uint16_t>(a.w + (uint64_t)a.rows * 208 * nb + blk * 2);
+    }
+}
+
+// The raw bytes of one thread's part of a weight row over a whole 256-weight block (its 4
+// units), for the producers of gemm3_body. A unit's chunk of one row is 16 bytes, and the
+// 4 units of a block are 64 contiguous bytes of each plane, so the block's loads of each plane
+// are issued back to back: all but the first find the row's line already requested in the
+// CU's L1. Fetched one unit at a time, each 16-byte load of a different row is its own L1
+// miss, and the line is requested again for the next unit (it does not survive the activation
+// stream in the L1 between units), which held the kernels at the L1's rate of misses.
+template <uint32_t FMT>
+struct WBlock {
+    uint4 q[4];                       // Q4_K: qs chunks (half `part`); Q6_K: ql plane `part`
+    uint4 qh[FMT == kQ6K ? 4 : 1];    // Q6_K: qh chunks
+    uint4 hd;                         // Q4_K: block header; Q6_K: int8 scales
+    uint32_t d;                       // Q6_K: d (FP16 bits)
+};
+
+template <uint32_t FMT, int BR>
+__device__ __forceinline__ void load_wblock(const GhGemmArgs& a, uint32_t r0, uint32_t b, WBlock<FMT>& wb,
+                                            uint32_t tid) {
+    const uint32_t nb = a.in_dim >> 8;
+    const uint32_t row = min(r0 + tid % BR, a.rows - 1), part = tid / BR;
+    const uint64_t blk = (uint64_t)row * nb + b;
+    if constexpr (FMT == kQ4K) {
+        const uint64_t q = a.w + (uint64_t)row * GH_Q4K_QS_BYTES * nb + (uint64_t)part * nb * 64 + b * 64;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wb.q[j] = *gh_gp<uint4>(q + 16 * j);
+        wb.hd = *gh_gp<uint4>(a.w + (uint64_t)a.rows * GH_Q4K_QS_BYTES * nb + blk * 16);
+        wb.d = 0;
+    } else {
+        const uint64_t rq = a.w + (uint64_t)row * GH_Q6K_QLH_BYTES * nb + b * 64;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wb.q[j] = *gh_gp<uint4>(rq + (uint64_t)part * nb * 64 + 16 * j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wb.qh[j] = *gh_gp<uint4>(rq + 2ull * nb * 64 + 16 * j);
+        wb.hd = *gh_gp<uint4>(a.w + (uint64_t)a.rows * GH_Q6K_QLH_BYTES * nb + blk * 16);
+        wb.d = *gh_gp<uint16_t>(a.w + (uint64_t)a.rows * 208 * nb + blk * 2);
     }
 }
 
@@ -217,12 +256,12 @@ __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc
 
 // Warp-specialized variant for long batches: a 512-thread workgroup owns 4·WT tokens x BR rows
 // (WT = 64: 256 tokens; WT = 32: 128 tokens, for chunks of fewer than 256 rows, where split K
-// has to spread the units over many workgroups: the producers' kL units in flight keep those
-// short ranges streaming, where a tile with one unit of lookahead waited on memory). Waves 0-3 (consumers) run the matrix cores (WT tokens each, B from LDS). Waves 4-7 (producers) stream the weight bytes
-// kL units ahead of use — kL register sets, selected statically by unrolling the loop kL-fold —
-// and dequantize each unit into a kS-stage LDS ring, kS - 1 units ahead of the consumers. One
-// barrier per unit: in the interval of unit u the consumers read stage (u - u0) % kS while the
-// producers fill unit u + kS - 1 into the stage read during unit u - 1.
+// has to spread the units over many workgroups). Waves 0-3 (consumers) run the matrix cores
+// (WT tokens each, B from LDS). Waves 4-7 (producers) stream the weight bytes a block ahead of
+// use (two block register sets, selected statically by unrolling the block loop twice) and
+// dequantize each unit into a kS-stage LDS ring one unit ahead of the consumers. One barrier
+// per unit: in the interval of unit u the consumers read stage (u - u0) % kS while the
+// producers fill unit u + 1 into the stage read during unit u - 2.
 // LDS of gemm3_body: kS = 3 weight stages, then each consumer wave's GH_GEMM3_XB(WT) activation
 // buffers (one unit each: the unit being read and the units in flight behind it). Three units
 // in flight for the 128-token tiles (8B prefill of 128 tokens 6.50 -> 6.45 ms, bit-identical);
@@ -238,44 +277,54 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
     static_assert(WT == 64 || WT == 32, "consumer waves of 64 or 32 tokens");
     constexpr int TI = WT / 32, TJ = BR / 32, NX = WT / 8;  // NX: activation line loads per unit
-    constexpr int kS = 3, kL = 4;
+    constexpr int kS = 3;
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t r0 = bx * BR;
     const uint32_t units = a.in_dim / 64;
-    const uint32_t per = (units + a.splits - 1) / a.splits;
+    const uint32_t per = gh_gemm_split_units(units, a.splits);
     const uint32_t u0 = bz * per, u1 = min(units, u0 + per);
     if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
     auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };
 
     if (wave >= 4) {
         // ---- producers ----
+        // Raw weight bytes a block (4 units) at a time, two blocks in registers: block i + 2 is
+        // requested once block i has been dequantized, so each block has the 4 units of block
+        // i + 1 to arrive (splits start and end on block boundaries, gh_gemm_split_units).
+        // Unit u0 + k goes into stage k % kS one unit ahead of the consumers: every store is
+        // followed by a barrier (the first is the consumers' start), and one more closes the
+        // consumers' last interval (1 + n_units barriers, as the consumers meet).
         const uint32_t pt = threadIdx.x - 256;
         const bool wload = pt < 2 * BR;
-        WStage raw[kL];
+        const uint32_t b0 = u0 / 4, nblk = (u1 - u0) / 4;
+        auto bc = [&](uint32_t i) __attribute__((always_inline)) { return b0 + min(i, nblk - 1); };
+        WBlock<FMT> wb[2];
+        load_wblock<FMT, BR>(a, r0, bc(0), wb[0], pt);
+        load_wblock<FMT, BR>(a, r0, bc(1), wb[1], pt);
+        auto block = [&](uint32_t i, WBlock<FMT>& w) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < kL; ++i) load_w<FMT, BR>(a, r0, uc(u0 + i), raw[i], pt);
-#pragma unroll
-        for (int j = 0; j < kS - 1; ++j) {
-            if (wload && u0 + j < u1) store_w<FMT, BR>(u0 + j, raw[j], wstage(j), pt);
-            load_w<FMT, BR>(a, r0, uc(u0 + j + kL), raw[j], pt);
-        }
-        __syncthreads();
-        const uint32_t n_units = u1 - u0;
-        auto produce = [&](uint32_t kk, WStage& rs) __attribute__((always_inline)) {
-            const uint32_t p = u0 + kk + kS - 1;  // the unit produced in this interval
-            if (wload && p < u1) store_w<FMT, BR>(p, rs, wstage((kk + kS - 1) % kS), pt);
-            load_w<FMT, BR>(a, r0, uc(p + kL), rs, pt);
-            __syncthreads();
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t k = 4 * i + j;
+                if (wload)
+                    store_w<FMT, BR>(u0 + k, WStage{w.q[j], w.hd, w.qh[FMT == kQ6K ? j : 0], w.d}, wstage(k % kS),
+                                     pt);
+                __syncthreads();
+            }
+            // the reload stays after the block's last use of w (hoisted above it, the
+            // compiler gives w two registers sets and copies between them at the loop's back
+            // edge, which waits for the loads just issued)
+            __builtin_amdgcn_sched_barrier(0);
+            load_wblock<FMT, BR>(a, r0, bc(i + 2), w, pt);
+            __builtin_amdgcn_sched_barrier(0);
         };
-        uint32_t k = 0;
-        for (; k + kL <= n_units; k += kL) {  // no exits inside the unrolled body
-#pragma unroll
-            for (int i = 0; i < kL; ++i) produce(k + i, raw[(i + kS - 1) % kL]);
+        uint32_t i = 0;
+        for (; i + 2 <= nblk; i += 2) {  // no exits inside the unrolled body
+            block(i, wb[0]);
+            block(i + 1, wb[1]);
         }
-#pragma unroll
-        for (int i = 0; i < kL - 1; ++i)
-            if (k + i < n_units) produce(k + i, raw[(i + kS - 1) % kL]);
+        if (i < nblk) block(i, wb[0]);
+        __syncthreads();
         return;
     }
 
@@ -411,7 +460,7 @@ __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, u
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, g = wave / NR, hr = wave % NR;
     const uint32_t r0 = bx * BR;
     const uint32_t units = a.in_dim / 64;
-    const uint32_t per = (units + a.splits - 1) / a.splits;
+    const uint32_t per = gh_gemm_split_units(units, a.splits);
     const uint32_t u0 = bz * per, u1 = min(units, u0 + per);
     if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
     auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };

@@ -21,6 +21,18 @@
 #define GH_Q4K_QS_BYTES 128u
 #define GH_Q6K_QLH_BYTES 192u
 
+// Units of 64 k per split of a prefill GEMM's K range: whole 256-weight blocks (4 units), so
+// that every split's weight stream starts on a block boundary (the producers fetch a block's
+// bytes of a row together). Split z covers units [z·per, min(units, (z + 1)·per)); units is a
+// multiple of 4 (in_dim a multiple of 256). Shared by the kernels and the host's split plans.
+static inline
+#ifdef __HIPCC__
+__host__ __device__
+#endif
+uint32_t gh_gemm_split_units(uint32_t units, uint32_t splits) {
+    return ((units / 4 + splits - 1) / splits) * 4;
+}
+
 struct GhRepackArgs {
     uint64_t src;   // GGUF block bytes
     uint64_t dst;   // device layout
