@@ -290,6 +290,9 @@ def main():
     result["config"]["prefill_128"] = prefill_short(hip, model, shape, 128)
     model.close()
     result["config"]["prefill_2048"] = prefill_long(hip, HipModel, shape, tensors, 2048)
+    # the same prefills with no FP16 weight copies: the GEMMs dequantize the Q4_K/Q6_K weights
+    result["config"]["prefill_dequantizing"] = {
+        str(t): prefill_long(hip, HipModel, shape, tensors, t, copies=False) for t in (512, 2048)}
     result["config"]["attention_c4"] = c4_attention(hip)
     if not args.no_c5:
         result["config"]["decoder_c5"] = c5_decoder(hip, HipModel, args.prompt)
@@ -629,13 +632,17 @@ def prefill_short(hip, model, shape, n):
     return {"tokens": n, "ms": round(ms, 3), "tok_s": round(n / (ms / 1e3), 1), "fp16_weight_copies": False}
 
 
-def prefill_long(hip, HipModel, shape, tensors, n):
+def prefill_long(hip, HipModel, shape, tensors, n, copies=True):
     """A long prompt through the prefill policy's 2048-row chunks: the same 8B-shaped weights in
     a model of n positions, one n-token chunk. Its first prefill (untimed) also makes the FP16
-    copies of the layer matrices that the prefill GEMMs read; the second is timed."""
+    copies of the layer matrices that the prefill GEMMs read (copies=False: the model keeps
+    none, GH_MODEL_NO_F16_WEIGHTS, and the GEMMs dequantize the Q4_K/Q6_K weights tile by
+    tile); the second is timed."""
+    from graph_horizon_amd import _ffi as F
     from graph_horizon_amd import synth
 
-    model = HipModel(hip, synth.model_config(shape, n, prefill_rows=n))
+    flags = 0 if copies else F.MODEL_NO_F16_WEIGHTS
+    model = HipModel(hip, synth.model_config(shape, n, prefill_rows=n, flags=flags))
     for layer, tid, fmt, data in tensors:
         model.load_tensor(layer, tid, fmt, data)
     prompt = np.random.default_rng(11).integers(0, shape.vocab_size, n).astype(np.uint32)
@@ -645,9 +652,10 @@ def prefill_long(hip, HipModel, shape, tensors, n):
     model.prefill(prompt, 0)
     ms = hip.timer_stop()
     model.close()
-    log(f"bench: prefill {n} tokens (one chunk) in {ms:.2f} ms ({n / (ms / 1e3):.0f} tok/s)")
+    log(f"bench: prefill {n} tokens (one chunk{'' if copies else ', dequantizing'}) in {ms:.2f} ms "
+        f"({n / (ms / 1e3):.0f} tok/s)")
     return {"tokens": n, "chunk_rows": n, "ms": round(ms, 3), "tok_s": round(n / (ms / 1e3), 1),
-            "fp16_weight_copies": True}
+            "fp16_weight_copies": copies}
 
 
 def prefill_gemm(hip, model, shape, tensors, n):

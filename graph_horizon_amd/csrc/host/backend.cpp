@@ -942,6 +942,19 @@ struct GemmPlan {
     uint64_t w16;
 };
 
+// Threads per workgroup of a prefill GEMM kernel: the dequantizing 256-token tiles run eight
+// consumer and four producer waves, every other form eight waves.
+static uint32_t gemm_block(GhKernel k) {
+    switch (k) {
+        case K_GEMM3_Q4K_R96:
+        case K_GEMM3_Q6K_R96:
+        case K_GEMM3_Q4K_R128:
+        case K_GEMM3_Q6K_R128:
+        case K_GEMM3_MIXED_R128: return 768;
+        default: return 512;
+    }
+}
+
 static GemmPlan plan_gemm(gh_backend* b, const gh_buf* w, uint32_t n) {
     const uint32_t rows = w->rows, units = w->cols / 64;
     // Batches of 128 tokens or fewer take 128-token tiles (kGemmTallTokens).
@@ -977,7 +990,7 @@ static GemmPlan plan_gemm(gh_backend* b, const gh_buf* w, uint32_t n) {
     if (w16)
         k = br == 96 ? (q4 ? K_GEMM4W_Q4K_R96 : K_GEMM4W_Q6K_R96) : (q4 ? K_GEMM4W_Q4K_R128 : K_GEMM4W_Q6K_R128);
     const uint32_t tr = ceil_div(rows, br), tiles = tr * tt;
-    const uint32_t slots = narrow ? resident_wgs(b, k, 512, 0) : cus;
+    const uint32_t slots = narrow ? resident_wgs(b, k, gemm_block(k), 0) : cus;
     uint32_t splits = clamp_splits(std::max<uint32_t>(1, slots / tiles));
     // the kernels give split z the units [z per, min(units, (z + 1) per)), per = whole blocks
     // (gh_gemm_split_units): shrink splits to ceil(units / per) until every split is non-empty
@@ -1004,7 +1017,7 @@ static int gemm_kernel(gh_backend* b, const GemmPlan& p, uint64_t out, uint64_t 
     ga.splits = p.splits;
     ga.epi = epi;
     ga.aux = aux;
-    return launch(b, p.k, p.tr, p.tt, p.splits, 512, &ga);
+    return launch(b, p.k, p.tr, p.tt, p.splits, gemm_block(p.k), &ga);
 }
 
 // One GEMM launch over its plan's tiles and K splits; with splits > 1 the kernel writes FP32
@@ -1177,7 +1190,7 @@ int op_gemm_multi(gh_backend* b, const gh_buf* a, const GemmSegSpec* segs, uint3
         ga.part = (uint64_t)((char*)b->ws + kArgmaxBytes);
     }
     const GhKernel k = copies ? K_GEMM4W_MIXED_R128 : tall ? K_GEMM3_MIXED_R128 : K_GEMM3_MIXED_R128_T128;
-    int rc = launch(b, k, tiles, tt, splits, 512, &ga);
+    int rc = launch(b, k, tiles, tt, splits, gemm_block(k), &ga);
     if (rc) return rc;
     if (splits > 1) {
         const uint64_t npairs = (uint64_t)n * total / 2;

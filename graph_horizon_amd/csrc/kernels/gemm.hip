@@ -267,16 +267,26 @@ __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc
 // in flight for the 128-token tiles (8B prefill of 128 tokens 6.50 -> 6.45 ms, bit-identical);
 // the 256-token tiles keep one (two measured no faster: 512 x 12288 -> 4096 105 -> 108 us).
 #define GH_GEMM3_XB(WT) ((WT) == 32 ? 4 : 2)
-#define GH_GEMM3_LDS(BR) (3 * (BR) * LDK + 4 * GH_GEMM3_XB(64) * 64 * 64)
 #define GH_GEMM3_LDS_T(BR, WT) (3 * (BR) * LDK + 4 * GH_GEMM3_XB(WT) * (WT) * 64)
 
-// Tile (bx, by) and split bz of one matrix (a.w, a.rows, a.out); lds3 holds GH_GEMM3_LDS(BR)
-// halves; partials go to columns pc .. of rows ps long.
-template <uint32_t FMT, int BR, int WT = 64>
+// Tile (bx, by) and split bz of one matrix (a.w, a.rows, a.out); lds3 holds the kernel's LDS
+// block (GH_GEMM3_LDS_T / GH_GEMM3_LDS_C8 halves); partials go to columns pc .. of rows ps long.
+// NC: consumer waves (4, or 8 with WT = 32: 256 tokens in eight 32-token waves, two per SIMD,
+// the four producer waves after them in a 768-thread workgroup; XB: activation buffers per
+// consumer wave (GH_GEMM3_XB(WT) by default).
+// CR: consumer row groups. CR = 1: consumer wave w multiplies the WT tokens it fetches against
+// all BR rows. CR = 2 (WT = 32): wave w multiplies the 64 tokens fetched by waves w & ~1 and
+// w | 1 against rows (BR / 2)·(w % 2) .. + BR / 2, so each weight fragment is read from LDS by
+// half as many waves (with eight consumers the fragment reads were the kernel's largest LDS
+// traffic, and LDS traffic set its time).
+template <uint32_t FMT, int BR, int WT = 64, int NC = 4, int XB = GH_GEMM3_XB(WT), int CR = 1>
 __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
     static_assert(WT == 64 || WT == 32, "consumer waves of 64 or 32 tokens");
-    constexpr int TI = WT / 32, TJ = BR / 32, NX = WT / 8;  // NX: activation line loads per unit
+    static_assert(NC == 4 || (NC == 8 && WT == 32), "four consumer waves, or eight of 32 tokens");
+    static_assert(CR == 1 || (CR == 2 && WT == 32 && BR % 64 == 0), "row halves: 32-token waves, 64-row halves");
+    // per consumer wave: TI x TJ tiles of 32 x 32; NX: activation line loads per unit
+    constexpr int TI = WT * CR / 32, TJ = BR / (32 * CR), NX = WT / 8;
     constexpr int kS = 3;
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -287,7 +297,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     if (u0 >= u1) return;  // workgroup-uniform; the host sizes splits so that none is empty
     auto uc = [&](uint32_t u) __attribute__((always_inline)) { return min(u, u1 - 1); };
 
-    if (wave >= 4) {
+    if (wave >= (uint32_t)NC) {
         // ---- producers ----
         // Raw weight bytes a block (4 units) at a time, two blocks in registers: block i + 2 is
         // requested once block i has been dequantized, so each block has the 4 units of block
@@ -295,7 +305,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
         // Unit u0 + k goes into stage k % kS one unit ahead of the consumers: every store is
         // followed by a barrier (the first is the consumers' start), and one more closes the
         // consumers' last interval (1 + n_units barriers, as the consumers meet).
-        const uint32_t pt = threadIdx.x - 256;
+        const uint32_t pt = threadIdx.x - 64 * NC;
         const bool wload = pt < 2 * BR;
         const uint32_t b0 = u0 / 4, nblk = (u1 - u0) / 4;
         auto bc = [&](uint32_t i) __attribute__((always_inline)) { return b0 + min(i, nblk - 1); };
@@ -338,8 +348,12 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     // for the next one. Here each unit waits only until the next unit's lines have landed
     // (loads complete in issue order; the consumers issue no other memory operations in the
     // loop), so kXA units stay in flight.
-    constexpr int kXB = GH_GEMM3_XB(WT), kXA = kXB - 1;
-    const uint32_t t0 = by * (4 * WT) + wave * WT;
+    constexpr int kXB = XB, kXA = kXB - 1;
+    const uint32_t t0 = by * (NC * WT) + wave * WT;  // the tokens this wave fetches
+    // the tokens and rows it multiplies; tile i's 32 token rows sit in wave xw0 + i's buffers
+    // (CR = 2) or at rows 32 i of its own (CR = 1)
+    const uint32_t tc = by * (NC * WT) + (wave / CR) * (WT * CR), rc = (wave % CR) * (BR / CR);
+    const uint32_t xw0 = CR == 2 ? (wave & ~1u) : wave;
     const uint32_t fm = lane & 31u, fg = lane >> 5;
     const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
     uint64_t xrow[NX];
@@ -353,6 +367,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     // is free of bank conflicts, as measured with SQ_LDS_BANK_CONFLICT on gfx950 (sw(r) =
     // (r / 4) % 8 and r % 8 are two-way conflicted: 7.3 against 3.8 LDS-active cycles per read).
     _Float16* xw = lds3 + kS * BR * LDK + wave * (kXB * WT * 64);
+    const _Float16* xa = lds3 + kS * BR * LDK + xw0 * (kXB * WT * 64);
     auto load_rows = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
@@ -378,15 +393,15 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     auto step = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
         load_rows(uc(u + kXA), (b + kXA) % kXB);
         __builtin_amdgcn_sched_barrier(0);  // the loads go out before anything waits
-        const _Float16* wb = wstage((u - u0) % kS);
-        const _Float16* xb = xw + b * (WT * 64);
+        const _Float16* wb = wstage((u - u0) % kS) + rc * LDK;
+        const _Float16* xb = xa + b * (WT * 64);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             h8 af[TI], bf[TJ];
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
-                const uint32_t r = 32 * i + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
-                af[i] = *(const h8*)(xb + r * 64 + c * 8);
+                const uint32_t r = (CR == 2 ? 0 : 32 * i) + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
+                af[i] = *(const h8*)(xb + (CR == 2 ? i * (kXB * WT * 64) : 0) + r * 64 + c * 8);
             }
 #pragma unroll
             for (int j = 0; j < TJ; ++j) bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
@@ -409,17 +424,24 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     for (int b = 0; b < kXB - 1; ++b)
         if (u + b < u1) step(u + b, b);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past u1 have landed
-    gemm_write<TI, TJ, true>(a, acc, t0, r0, fm, fg, bz, ps, pc);
+    gemm_write<TI, TJ, true>(a, acc, tc, r0 + rc, fm, fg, bz, ps, pc);
 }
 
 }  // namespace
 
-// Tile variants: 128 tokens per workgroup (4 waves x 32) x 64 or 128 weight rows.
-// warp-specialized 256-token tiles (512 threads)
+// Warp-specialized 256-token tiles: eight 32-token consumer waves (two per SIMD, so one wave's
+// fragment reads and waits overlap the other's matrix work) and four producer waves, 768
+// threads, one unit of activation lookahead; 128-row tiles with the consumers tiled 4 x 2
+// (64 tokens x 64 rows each), 96-row tiles 8 x 1. Against four 64-token consumers (512 threads),
+// same box, bit-identical: 512 x 4096 -> 12288 (96 rows) 76.7 -> 71.8 us, 512 x 12288 -> 4096
+// (128 rows, 4 splits) 80.2 -> 73.6, 2048 x 4096 -> 4096 105.4 -> 92.7 (4 x 2 tiles; 101.3 as
+// 8 x 1), 2048 x 4096 -> 12288 291.6 -> 207.8 (128 rows 4 x 2, where the 96-row tiles take
+// 233.9).
+#define GH_GEMM3_LDS_C8(BR) (3 * (BR) * LDK + 8 * 2 * 32 * 64)
 #define GH_GEMM3(NAME, FMT, BR)                                                                    \
-    GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
-        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(BR)];                   \
-        gemm3_body<FMT, BR>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);                \
+    GH_KERNEL __launch_bounds__(768) void NAME(GhGemmArgs a) {                                     \
+        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_C8(BR)];                \
+        gemm3_body<FMT, BR, 32, 8, 2, (BR) == 128 ? 2 : 1>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0); \
     }
 GH_GEMM3(gh_gemm3_q4k_r128, kQ4K, 128)
 GH_GEMM3(gh_gemm3_q6k_r128, kQ6K, 128)
@@ -623,13 +645,16 @@ __device__ __forceinline__ void gemm3_mixed(const GhGemmArgs& a, _Float16* lds) 
     m.rows = a.seg[s].rows;
     m.out = a.seg[s].out;
     const uint32_t bx = blockIdx.x - a.seg[s].tile0;
+    // 256-token tiles (WT = 64 here: tokens per consumer-wave pair) in the 768-thread form
+    constexpr int W = WT == 64 ? 32 : WT, NC = WT == 64 ? 8 : 4, XB = WT == 64 ? 2 : GH_GEMM3_XB(32),
+                  CR = WT == 64 ? 2 : 1;
     if (a.seg[s].fmt == kQ4K)
-        gemm3_body<kQ4K, 128, WT>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+        gemm3_body<kQ4K, 128, W, NC, XB, CR>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
     else
-        gemm3_body<kQ6K, 128, WT>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+        gemm3_body<kQ6K, 128, W, NC, XB, CR>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
 }
-GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128(GhGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS(128)];
+GH_KERNEL __launch_bounds__(768) void gh_gemm3_mixed_r128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_C8(128)];
     gemm3_mixed<64>(a, lds);
 }
 // 128-token tiles, for batches of fewer than 256 tokens
