@@ -942,15 +942,19 @@ struct GemmPlan {
     uint64_t w16;
 };
 
-// Threads per workgroup of a prefill GEMM kernel: the dequantizing 256-token tiles run eight
-// consumer and four producer waves, every other form eight waves.
+// Threads per workgroup of a prefill GEMM kernel: the dequantizing 256-token tiles and the
+// 128-row 128-token tiles run eight consumer and four producer waves, every other form eight
+// waves.
 static uint32_t gemm_block(GhKernel k) {
     switch (k) {
         case K_GEMM3_Q4K_R96:
         case K_GEMM3_Q6K_R96:
         case K_GEMM3_Q4K_R128:
         case K_GEMM3_Q6K_R128:
-        case K_GEMM3_MIXED_R128: return 768;
+        case K_GEMM3_MIXED_R128:
+        case K_GEMM3_Q4K_R128_T128:
+        case K_GEMM3_Q6K_R128_T128:
+        case K_GEMM3_MIXED_R128_T128: return 768;
         default: return 512;
     }
 }

@@ -274,19 +274,25 @@ __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc
 // NC: consumer waves (4, or 8 with WT = 32: 256 tokens in eight 32-token waves, two per SIMD,
 // the four producer waves after them in a 768-thread workgroup; XB: activation buffers per
 // consumer wave (GH_GEMM3_XB(WT) by default).
-// CR: consumer row groups. CR = 1: consumer wave w multiplies the WT tokens it fetches against
-// all BR rows. CR = 2 (WT = 32): wave w multiplies the 64 tokens fetched by waves w & ~1 and
-// w | 1 against rows (BR / 2)·(w % 2) .. + BR / 2, so each weight fragment is read from LDS by
-// half as many waves (with eight consumers the fragment reads were the kernel's largest LDS
-// traffic, and LDS traffic set its time).
-template <uint32_t FMT, int BR, int WT = 64, int NC = 4, int XB = GH_GEMM3_XB(WT), int CR = 1>
+// Wave roles of the consumers. NF waves fetch the tile's activations, WT token rows each (the
+// tile is NF·WT tokens); NC waves multiply them, in NC / CR token groups x CR row groups: wave w
+// takes TW = NF·WT·CR / NC tokens from (w / CR)·TW against rows (BR / CR)·(w % CR) .. + BR / CR.
+//   NC = NF = 4, CR = 1: each consumer multiplies the tokens it fetched against all rows;
+//   NC = NF = 8, CR = 1 or 2: 256 tokens in eight 32-token fetches, two consumers per SIMD
+//     (CR = 2: 64 tokens x half the rows each);
+//   NC = 8, NF = 4, CR = 2: 128 tokens fetched by waves 0-3, consumers of 32 tokens x half the
+//     rows, two per SIMD.
+// With CR = 2 each weight fragment is read from LDS by half as many waves.
+template <uint32_t FMT, int BR, int WT = 64, int NC = 4, int XB = GH_GEMM3_XB(WT), int CR = 1, int NF = NC>
 __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
-    static_assert(WT == 64 || WT == 32, "consumer waves of 64 or 32 tokens");
-    static_assert(NC == 4 || (NC == 8 && WT == 32), "four consumer waves, or eight of 32 tokens");
-    static_assert(CR == 1 || (CR == 2 && WT == 32 && BR % 64 == 0), "row halves: 32-token waves, 64-row halves");
+    static_assert(WT == 64 || WT == 32, "fetches of 64 or 32 tokens");
+    static_assert((NC == 4 || NC == 8) && (NF == 4 || NF == 8) && NF <= NC, "four or eight consumers");
+    static_assert(CR == 1 || (CR == 2 && BR % 64 == 0), "row halves of 64-row multiples");
+    constexpr int TW = NF * WT * CR / NC;  // tokens per consumer wave
+    static_assert(TW % 32 == 0 && TW * NC == NF * WT * CR, "whole 32-token tiles per consumer");
     // per consumer wave: TI x TJ tiles of 32 x 32; NX: activation line loads per unit
-    constexpr int TI = WT * CR / 32, TJ = BR / (32 * CR), NX = WT / 8;
+    constexpr int TI = TW / 32, TJ = BR / (32 * CR), NX = WT / 8;
     constexpr int kS = 3;
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -349,17 +355,17 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     // (loads complete in issue order; the consumers issue no other memory operations in the
     // loop), so kXA units stay in flight.
     constexpr int kXB = XB, kXA = kXB - 1;
-    const uint32_t t0 = by * (NC * WT) + wave * WT;  // the tokens this wave fetches
-    // the tokens and rows it multiplies; tile i's 32 token rows sit in wave xw0 + i's buffers
-    // (CR = 2) or at rows 32 i of its own (CR = 1)
-    const uint32_t tc = by * (NC * WT) + (wave / CR) * (WT * CR), rc = (wave % CR) * (BR / CR);
-    const uint32_t xw0 = CR == 2 ? (wave & ~1u) : wave;
+    const bool fetcher = wave < (uint32_t)NF;
+    const uint32_t t0 = by * (NF * WT) + wave * WT;  // the tokens this wave fetches
+    // the tokens and rows it multiplies: tile i's 32 token rows are rows xr_i .. + 32 of fetch
+    // wave xf_i's buffers
+    const uint32_t tb = (wave / CR) * TW, tc = by * (NF * WT) + tb, rc = (wave % CR) * (BR / CR);
     const uint32_t fm = lane & 31u, fg = lane >> 5;
     const GH_GLOBAL uint16_t* x = gh_gp<uint16_t>(a.x);
-    uint64_t xrow[NX];
+    uint64_t xg[NX];
 #pragma unroll
     for (int i = 0; i < NX; ++i)
-        xrow[i] = (uint64_t)(uintptr_t)(x + (uint64_t)min(t0 + 8 * i + (lane >> 3), a.n - 1) * a.in_dim);
+        xg[i] = (uint64_t)(uintptr_t)(x + (uint64_t)min(t0 + 8 * i + (lane >> 3), a.n - 1) * a.in_dim);
     // global_load_lds_dwordx4: lane l of a load lands at byte 16 l of its 1 KiB destination. Load
     // i covers rows 8 i .. 8 i + 7 of the wave's WT; lane l fetches chunk (l % 8) ^ sw(r) of row
     // r = 8 i + l / 8, so chunk c of row r sits at slot c ^ sw(r). Every row starts at bank 0
@@ -367,14 +373,20 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     // is free of bank conflicts, as measured with SQ_LDS_BANK_CONFLICT on gfx950 (sw(r) =
     // (r / 4) % 8 and r % 8 are two-way conflicted: 7.3 against 3.8 LDS-active cycles per read).
     _Float16* xw = lds3 + kS * BR * LDK + wave * (kXB * WT * 64);
-    const _Float16* xa = lds3 + kS * BR * LDK + xw0 * (kXB * WT * 64);
+    const _Float16* xs = lds3 + kS * BR * LDK;
+    uint32_t xoff[TI], xrow[TI];  // tile i: offset of its fetch wave's buffers, first row
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        xoff[i] = ((tb + 32 * i) / WT) * (kXB * WT * 64);
+        xrow[i] = (tb + 32 * i) % WT;
+    }
     auto load_rows = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
             const uint32_t r = 8 * i + (lane >> 3), c = (lane & 7u) ^ ((r >> 1) & 7u);
             const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(
                 xw + b * (WT * 64) + i * 512);
-            asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(xrow[i] + 2ull * chunk_k<FMT>(u, c)),
+            asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(xg[i] + 2ull * chunk_k<FMT>(u, c)),
                          "{m0}"(__builtin_amdgcn_readfirstlane(dst))
                          : "memory");
         }
@@ -385,23 +397,24 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f16v{};
 #pragma unroll
-    for (int i = 0; i < kXA; ++i) load_rows(uc(u0 + i), i);
+    for (int i = 0; i < kXA; ++i)
+        if (NF == NC || fetcher) load_rows(uc(u0 + i), i);
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NX * (kXA - 1)) : "memory");  // unit u0 has landed
     __syncthreads();
     // unit u is read from buffer b = (u - u0) % kXB; unit u + kXA goes into buffer (b + kXA) %
     // kXB, the one read during unit u - 1 (those reads ended before its barrier)
     auto step = [&](uint32_t u, uint32_t b) __attribute__((always_inline)) {
-        load_rows(uc(u + kXA), (b + kXA) % kXB);
+        if (NF == NC || fetcher) load_rows(uc(u + kXA), (b + kXA) % kXB);
         __builtin_amdgcn_sched_barrier(0);  // the loads go out before anything waits
         const _Float16* wb = wstage((u - u0) % kS) + rc * LDK;
-        const _Float16* xb = xa + b * (WT * 64);
+        const _Float16* xb = xs + b * (WT * 64);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             h8 af[TI], bf[TJ];
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
-                const uint32_t r = (CR == 2 ? 0 : 32 * i) + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
-                af[i] = *(const h8*)(xb + (CR == 2 ? i * (kXB * WT * 64) : 0) + r * 64 + c * 8);
+                const uint32_t r = xrow[i] + fm, c = (2 * ks + fg) ^ ((r >> 1) & 7u);
+                af[i] = *(const h8*)(xb + xoff[i] + r * 64 + c * 8);
             }
 #pragma unroll
             for (int j = 0; j < TJ; ++j) bf[j] = *(const h8*)(wb + (32 * j + fm) * LDK + 16 * ks + 8 * fg);
@@ -453,10 +466,19 @@ GH_GEMM3(gh_gemm3_q6k_r96, kQ6K, 96)
         __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_T(BR, 32)];             \
         gemm3_body<FMT, BR, 32>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);            \
     }
-GH_GEMM3T(gh_gemm3_q4k_r128_t128, kQ4K, 128)
-GH_GEMM3T(gh_gemm3_q6k_r128_t128, kQ6K, 128)
 GH_GEMM3T(gh_gemm3_q4k_r96_t128, kQ4K, 96)
 GH_GEMM3T(gh_gemm3_q6k_r96_t128, kQ6K, 96)
+// 128-token tiles of 128 rows: the activations fetched by four waves, eight consumers of 32
+// tokens x 64 rows (two per SIMD), four producers, 768 threads. Against four consumers of 32
+// tokens x 128 rows, same box, bit-identical: 128 x 12288 -> 4096 (8 splits) 35.8 -> 33.9 us,
+// 128 x 4096 -> 4096 (4 splits) 17.2 (96-row tiles) -> 16.2, 128 x 5120 -> 16384 39.0 -> 37.1.
+#define GH_GEMM3T8(NAME, FMT, BR)                                                                  \
+    GH_KERNEL __launch_bounds__(768) void NAME(GhGemmArgs a) {                                     \
+        __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_T(BR, 32)];             \
+        gemm3_body<FMT, BR, 32, 8, GH_GEMM3_XB(32), 2, 4>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0); \
+    }
+GH_GEMM3T8(gh_gemm3_q4k_r128_t128, kQ4K, 128)
+GH_GEMM3T8(gh_gemm3_q6k_r128_t128, kQ6K, 128)
 
 // Over FP16 weight copies, every wave of the workgroup runs the matrix cores: 512 threads own
 // 256 tokens x BR rows, two waves per SIMD, so that one wave's LDS reads and waits overlap the
@@ -645,20 +667,20 @@ __device__ __forceinline__ void gemm3_mixed(const GhGemmArgs& a, _Float16* lds) 
     m.rows = a.seg[s].rows;
     m.out = a.seg[s].out;
     const uint32_t bx = blockIdx.x - a.seg[s].tile0;
-    // 256-token tiles (WT = 64 here: tokens per consumer-wave pair) in the 768-thread form
-    constexpr int W = WT == 64 ? 32 : WT, NC = WT == 64 ? 8 : 4, XB = WT == 64 ? 2 : GH_GEMM3_XB(32),
-                  CR = WT == 64 ? 2 : 1;
+    // the 768-thread forms: 256-token tiles (WT = 64) in eight 32-token fetches, 128-token tiles
+    // (WT = 32) in four; eight consumers of half the rows each
+    constexpr int XB = WT == 64 ? 2 : GH_GEMM3_XB(32), NF = WT == 64 ? 8 : 4;
     if (a.seg[s].fmt == kQ4K)
-        gemm3_body<kQ4K, 128, W, NC, XB, CR>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+        gemm3_body<kQ4K, 128, 32, 8, XB, 2, NF>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
     else
-        gemm3_body<kQ6K, 128, W, NC, XB, CR>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
+        gemm3_body<kQ6K, 128, 32, 8, XB, 2, NF>(m, lds, bx, blockIdx.y, blockIdx.z, a.rows, a.seg[s].col0);
 }
 GH_KERNEL __launch_bounds__(768) void gh_gemm3_mixed_r128(GhGemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_C8(128)];
     gemm3_mixed<64>(a, lds);
 }
 // 128-token tiles, for batches of fewer than 256 tokens
-GH_KERNEL __launch_bounds__(512) void gh_gemm3_mixed_r128_t128(GhGemmArgs a) {
+GH_KERNEL __launch_bounds__(768) void gh_gemm3_mixed_r128_t128(GhGemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_T(128, 32)];
     gemm3_mixed<32>(a, lds);
 }
