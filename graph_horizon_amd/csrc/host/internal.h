@@ -96,6 +96,7 @@ enum GhKernel : int {
     K_ATTN_MFMA_G8_X,
     K_ATTN_MFMA_G4_S16_X,
     K_XCD_PROBE,
+    K_GEMM3_SWIGLU_R96_T128,
     K_COUNT
 };
 

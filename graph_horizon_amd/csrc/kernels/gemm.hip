@@ -98,19 +98,30 @@ struct WBlock {
     uint32_t d;                       // Q6_K: d (FP16 bits)
 };
 
-template <uint32_t FMT, int BR>
+// PAIR (SwiGLU's gate and up in one tile, gh_gemm3_swiglu_r96_t128): LDS row lr of the 96 holds
+// gate row r0 + lr (lr < 32), up row r0 + lr - 32 (< 64), gate row r0 + lr - 32 (< 80) or up
+// row r0 + lr - 48, r0 = 48 · tile; the gate matrix at a.w, the up matrix (same shape) at a.aux.
+template <uint32_t FMT, int BR, bool PAIR = false>
 __device__ __forceinline__ void load_wblock(const GhGemmArgs& a, uint32_t r0, uint32_t b, WBlock<FMT>& wb,
                                             uint32_t tid) {
     const uint32_t nb = a.in_dim >> 8;
-    const uint32_t row = min(r0 + tid % BR, a.rows - 1), part = tid / BR;
+    const uint32_t lr = tid % BR, part = tid / BR;
+    uint64_t wbase = a.w;
+    uint32_t row = r0 + lr;
+    if constexpr (PAIR) {
+        row = r0 + (lr < 64 ? lr % 32u : 32u + (lr - 64) % 16u);
+        wbase = ((lr >= 32 && lr < 64) || lr >= 80) ? a.aux : a.w;
+    }
+    row = min(row, a.rows - 1);
     const uint64_t blk = (uint64_t)row * nb + b;
     if constexpr (FMT == kQ4K) {
-        const uint64_t q = a.w + (uint64_t)row * GH_Q4K_QS_BYTES * nb + (uint64_t)part * nb * 64 + b * 64;
+        const uint64_t q = wbase + (uint64_t)row * GH_Q4K_QS_BYTES * nb + (uint64_t)part * nb * 64 + b * 64;
 #pragma unroll
         for (int j = 0; j < 4; ++j) wb.q[j] = *gh_gp<uint4>(q + 16 * j);
-        wb.hd = *gh_gp<uint4>(a.w + (uint64_t)a.rows * GH_Q4K_QS_BYTES * nb + blk * 16);
+        wb.hd = *gh_gp<uint4>(wbase + (uint64_t)a.rows * GH_Q4K_QS_BYTES * nb + blk * 16);
         wb.d = 0;
     } else {
+        static_assert(!PAIR, "the gate/up pair tiles are Q4_K");
         const uint64_t rq = a.w + (uint64_t)row * GH_Q6K_QLH_BYTES * nb + b * 64;
 #pragma unroll
         for (int j = 0; j < 4; ++j) wb.q[j] = *gh_gp<uint4>(rq + (uint64_t)part * nb * 64 + 16 * j);
@@ -283,7 +294,8 @@ __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc
 //   NC = 8, NF = 4, CR = 2: 128 tokens fetched by waves 0-3, consumers of 32 tokens x half the
 //     rows, two per SIMD.
 // With CR = 2 each weight fragment is read from LDS by half as many waves.
-template <uint32_t FMT, int BR, int WT = 64, int NC = 4, int XB = GH_GEMM3_XB(WT), int CR = 1, int NF = NC>
+template <uint32_t FMT, int BR, int WT = 64, int NC = 4, int XB = GH_GEMM3_XB(WT), int CR = 1, int NF = NC,
+          bool PAIR = false>
 __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
     static_assert(WT == 64 || WT == 32, "fetches of 64 or 32 tokens");
@@ -295,8 +307,9 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     constexpr int TI = TW / 32, TJ = BR / (32 * CR), NX = WT / 8;
     constexpr int kS = 3;
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
+    static_assert(!PAIR || (BR == 96 && NC == 4 && NF == 4 && WT == 32 && CR == 1), "pair tiles: 96 rows x 128 tokens");
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t r0 = bx * BR;
+    const uint32_t r0 = bx * (PAIR ? BR / 2 : BR);
     const uint32_t units = a.in_dim / 64;
     const uint32_t per = gh_gemm_split_units(units, a.splits);
     const uint32_t u0 = bz * per, u1 = min(units, u0 + per);
@@ -316,8 +329,8 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
         const uint32_t b0 = u0 / 4, nblk = (u1 - u0) / 4;
         auto bc = [&](uint32_t i) __attribute__((always_inline)) { return b0 + min(i, nblk - 1); };
         WBlock<FMT> wb[2];
-        load_wblock<FMT, BR>(a, r0, bc(0), wb[0], pt);
-        load_wblock<FMT, BR>(a, r0, bc(1), wb[1], pt);
+        load_wblock<FMT, BR, PAIR>(a, r0, bc(0), wb[0], pt);
+        load_wblock<FMT, BR, PAIR>(a, r0, bc(1), wb[1], pt);
         auto block = [&](uint32_t i, WBlock<FMT>& w) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -331,7 +344,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
             // compiler gives w two registers sets and copies between them at the loop's back
             // edge, which waits for the loads just issued)
             __builtin_amdgcn_sched_barrier(0);
-            load_wblock<FMT, BR>(a, r0, bc(i + 2), w, pt);
+            load_wblock<FMT, BR, PAIR>(a, r0, bc(i + 2), w, pt);
             __builtin_amdgcn_sched_barrier(0);
         };
         uint32_t i = 0;
@@ -437,7 +450,22 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     for (int b = 0; b < kXB - 1; ++b)
         if (u + b < u1) step(u + b, b);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past u1 have landed
-    gemm_write<TI, TJ, true>(a, acc, tc, r0 + rc, fm, fg, bz, ps, pc);
+    if constexpr (PAIR) {
+        // one split (the host's plan): tile 0 holds gate rows r0 + fm, tile 1 the up rows of the
+        // same lanes, tile 2 gate rows r0 + 32 + fm in lanes fm < 16 and the matching up rows
+        // 16 lanes up. out = silu_mul(f16(gate), f16(up)), as gh_gemm_reduce_swiglu computes it.
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float up2 = __shfl_xor(acc[0][2][r], 16);
+            const uint32_t t = tc + 8 * (r >> 2) + 4 * fg + (r & 3);
+            if (t >= a.n) continue;
+            GH_GLOBAL uint16_t* o = gh_gpw<uint16_t>(a.out) + (uint64_t)t * a.rows;
+            if (r0 + fm < a.rows) o[r0 + fm] = gh_silu_mul_h(gh_f2h(acc[0][0][r]), gh_f2h(acc[0][1][r]));
+            if (fm < 16 && r0 + 32 + fm < a.rows) o[r0 + 32 + fm] = gh_silu_mul_h(gh_f2h(acc[0][2][r]), gh_f2h(up2));
+        }
+    } else {
+        gemm_write<TI, TJ, true>(a, acc, tc, r0 + rc, fm, fg, bz, ps, pc);
+    }
 }
 
 }  // namespace
@@ -468,6 +496,15 @@ GH_GEMM3(gh_gemm3_q6k_r96, kQ6K, 96)
     }
 GH_GEMM3T(gh_gemm3_q4k_r96_t128, kQ4K, 96)
 GH_GEMM3T(gh_gemm3_q6k_r96_t128, kQ6K, 96)
+// SwiGLU's gate (a.w) and up (a.aux) Q4_K projections of one input in one launch, for batches
+// of at most 128 tokens: each 96-row tile holds 48 gate rows and the same 48 up rows (PAIR in
+// load_wblock), K unsplit, and writes silu_mul(f16(x wg^T), f16(x wu^T)) straight to a.out
+// [n][rows] — no FP32 partials and no split reduce. Each output's sum runs over every unit in
+// k order, the sum of the unsplit gh_gemm3_q4k_*_t128 kernels.
+GH_KERNEL __launch_bounds__(512) void gh_gemm3_swiglu_r96_t128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_T(96, 32)];
+    gemm3_body<kQ4K, 96, 32, 4, GH_GEMM3_XB(32), 1, 4, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
+}
 // 128-token tiles of 128 rows: the activations fetched by four waves, eight consumers of 32
 // tokens x 64 rows (two per SIMD), four producers, 768 threads. Against four consumers of 32
 // tokens x 128 rows, same box, bit-identical: 128 x 12288 -> 4096 (8 splits) 35.8 -> 33.9 us,

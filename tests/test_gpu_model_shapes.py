@@ -108,9 +108,11 @@ def test_full_width_prefill_driver_matches_op_by_op(hip, name, n):
     round to the neighbouring FP16; one block keeps that from being amplified by a second
     block of random weights (whose residual grows to thousands and whose attention is nearly
     one-hot), and every difference is bounded against the tensor's scale. On the 8B shape at
-    100 rows (one 128-token tile) every GEMM splits K alike in the fused and the separate
-    launches on MI355X's 256 CUs (Q/K/V five splits each), so the driver, gate and up through
-    their shared SiLU reduce included, is bit-identical there."""
+    100 rows (one 128-token tile) Q/K/V, O and down split K alike in the fused and the separate
+    launches on MI355X's 256 CUs (Q/K/V five splits each); gate and up run in the fused
+    driver's one paired launch (gh_gemm3_swiglu_r96_t128, K unsplit) against two GEMMs of two
+    splits each op by op, a re-association of each FP32 sum that leaves every FP16 output of
+    these weights unchanged: the driver is bit-identical there."""
     from graph_over_abi import AbiGraph
 
     shape = dataclasses.replace(synth.SHAPES[name], name=f"{name}-1", block_count=1)

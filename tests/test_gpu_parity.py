@@ -582,17 +582,19 @@ def test_fused_decode_is_bit_identical_to_op_by_op(hip, shape_name):
     gm.close()
 
 
-@pytest.mark.parametrize("n", [37, 300])
+@pytest.mark.parametrize("n", [8, 37, 128, 300])
 @pytest.mark.parametrize("shape_name", ["tiny", "small"])
 def test_prefill_driver_is_bit_identical_to_op_by_op(hip, shape_name, n):
     """The driver's prefill (one batch: GEMV for n < 8 rows, the MFMA GEMMs above, the
     warp-specialized ones from 256 rows, with the glue folded into GEMM epilogues and split
     reduces and Q/K/V in one launch) leaves the same logits and KV bits as recording every
     trait op separately (prefill::record_batch over the C ABI). The tiny shape's GEMMs run one
-    K split each; the small shape's run one (two for down) at 37 rows and two (four for down)
-    at 300, alike in the fused and the separate launches, so both sum in the same order; at 300
-    rows its gate and up GEMMs share one split reduce that applies silu_mul
-    (gh_gemm_reduce_swiglu). Where the split counts differ
+    K split each; the small shape's run one (two for down) at 8-128 rows and two (four for
+    down) at 300, alike in the fused and the separate launches, so both sum in the same order.
+    At 8-128 rows the driver's gate and up run as one paired launch (gh_gemm3_swiglu_r96_t128:
+    48 gate + 48 up rows per tile, silu_mul in its epilogue; 22 and 43 tiles here, the last one
+    partial) against two unsplit GEMMs and silu_mul op by op; at 300 rows they share one split
+    reduce that applies silu_mul (gh_gemm_reduce_swiglu). Where the split counts differ
     (the 8B shape's Q/K/V launch against the three projections alone) the results differ only
     by FP32 re-association, checked against the oracle in test_gpu_model_shapes."""
     from graph_horizon_amd import HipModel
