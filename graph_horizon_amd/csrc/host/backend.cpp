@@ -65,7 +65,7 @@ const KernelName kKernels[] = {
     {K_ATTN_MFMA_G4_X, "gh_attn_mfma_g4_x"},   {K_ATTN_MFMA_G8_X, "gh_attn_mfma_g8_x"},
     {K_ATTN_MFMA_G4_S16_X, "gh_attn_mfma_g4_s16_x"},
     {K_XCD_PROBE, "gh_xcd_probe"},
-    {K_GEMM3_SWIGLU_R96_T128, "gh_gemm3_swiglu_r96_t128"},
+    {K_GEMM3_SWIGLU_R96_T128, "gh_gemm3_swiglu_r96_t128"}, {K_GEMM3_SWIGLU_R128_T128, "gh_gemm3_swiglu_r128_t128"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -1075,10 +1075,13 @@ int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const g
     const uint64_t cells = (uint64_t)n * wg->rows;
     if (!fits(a, (uint64_t)n * wg->cols * 2) || !fits(out, cells * 2) || !fits(gate, cells * 2))
         return fail(b, GH_E_RANGE, "gemm swiglu: buffer too small");
-    // 8-128 tokens, Q4_K gate and up whose 48-row pairs fill at most one wave of workgroups:
-    // one launch of 96-row tiles (48 gate rows + the same 48 up rows), K unsplit, silu_mul in
-    // the epilogue — no FP32 partials or split reduce (8B 128 x 4096 -> 2 x 12288: 256 tiles)
-    const uint32_t pair_tiles = ceil_div(wg->rows, 48u);
+    // 8-128 tokens, Q4_K gate and up whose row pairs fill at most one wave of workgroups: one
+    // launch of 96-row tiles (48 gate rows + the same 48 up rows) or, where those would be more
+    // than the CUs, 128-row tiles (64 + 64, eight consumers), K unsplit, silu_mul in the
+    // epilogue — no FP32 partials or split reduce (8B 128 x 4096 -> 2 x 12288: 256 tiles of
+    // 96; 14B 128 x 5120 -> 2 x 16384: 256 tiles of 128)
+    const bool pair96 = ceil_div(wg->rows, 48u) <= b->cus;
+    const uint32_t pair_tiles = ceil_div(wg->rows, pair96 ? 48u : 64u);
     if (n < kGemmTallTokens && wg->format == GH_FMT_Q4_K && wu->format == GH_FMT_Q4_K && pair_tiles <= b->cus) {
         GhGemmArgs ga{};
         ga.x = a->addr;
@@ -1089,7 +1092,8 @@ int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const g
         ga.rows = wg->rows;
         ga.n = n;
         ga.splits = 1;
-        return launch(b, K_GEMM3_SWIGLU_R96_T128, pair_tiles, ceil_div(n, 128u), 1, 512, &ga);
+        return launch(b, pair96 ? K_GEMM3_SWIGLU_R96_T128 : K_GEMM3_SWIGLU_R128_T128, pair_tiles, ceil_div(n, 128u),
+                      1, pair96 ? 512 : 768, &ga);
     }
     const GemmPlan pg = plan_gemm(b, wg, n), pu = plan_gemm(b, wu, n);
     if (pg.splits == 1 || pu.splits != pg.splits || wg->rows % 4) {

@@ -97,6 +97,7 @@ enum GhKernel : int {
     K_ATTN_MFMA_G4_S16_X,
     K_XCD_PROBE,
     K_GEMM3_SWIGLU_R96_T128,
+    K_GEMM3_SWIGLU_R128_T128,
     K_COUNT
 };
 

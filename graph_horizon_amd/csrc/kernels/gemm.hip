@@ -98,9 +98,11 @@ struct WBlock {
     uint32_t d;                       // Q6_K: d (FP16 bits)
 };
 
-// PAIR (SwiGLU's gate and up in one tile, gh_gemm3_swiglu_r96_t128): LDS row lr of the 96 holds
-// gate row r0 + lr (lr < 32), up row r0 + lr - 32 (< 64), gate row r0 + lr - 32 (< 80) or up
-// row r0 + lr - 48, r0 = 48 · tile; the gate matrix at a.w, the up matrix (same shape) at a.aux.
+// PAIR (SwiGLU's gate and up in one tile, gh_gemm3_swiglu_*_t128; the gate matrix at a.w, the up
+// matrix of the same shape at a.aux), r0 = BR / 2 · tile. BR = 96: LDS row lr holds gate row
+// r0 + lr (lr < 32), up row r0 + lr - 32 (< 64), gate row r0 + lr - 32 (< 80) or up row
+// r0 + lr - 48. BR = 128: rows alternate by 32, gate rows r0 .. + 32 | up rows r0 .. + 32 |
+// gate rows r0 + 32 .. + 32 | up rows r0 + 32 .. + 32.
 template <uint32_t FMT, int BR, bool PAIR = false>
 __device__ __forceinline__ void load_wblock(const GhGemmArgs& a, uint32_t r0, uint32_t b, WBlock<FMT>& wb,
                                             uint32_t tid) {
@@ -108,9 +110,12 @@ __device__ __forceinline__ void load_wblock(const GhGemmArgs& a, uint32_t r0, ui
     const uint32_t lr = tid % BR, part = tid / BR;
     uint64_t wbase = a.w;
     uint32_t row = r0 + lr;
-    if constexpr (PAIR) {
+    if constexpr (PAIR && BR == 96) {
         row = r0 + (lr < 64 ? lr % 32u : 32u + (lr - 64) % 16u);
         wbase = ((lr >= 32 && lr < 64) || lr >= 80) ? a.aux : a.w;
+    } else if constexpr (PAIR) {
+        row = r0 + (lr / 64) * 32 + lr % 32;
+        wbase = (lr / 32) % 2 ? a.aux : a.w;
     }
     row = min(row, a.rows - 1);
     const uint64_t blk = (uint64_t)row * nb + b;
@@ -307,7 +312,9 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     constexpr int TI = TW / 32, TJ = BR / (32 * CR), NX = WT / 8;
     constexpr int kS = 3;
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
-    static_assert(!PAIR || (BR == 96 && NC == 4 && NF == 4 && WT == 32 && CR == 1), "pair tiles: 96 rows x 128 tokens");
+    static_assert(!PAIR || (BR == 96 && NC == 4 && NF == 4 && WT == 32 && CR == 1) ||
+                      (BR == 128 && NC == 8 && NF == 4 && WT == 32 && CR == 2),
+                  "pair tiles: 96 rows (four consumers) or 128 rows (eight) x 128 tokens");
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t r0 = bx * (PAIR ? BR / 2 : BR);
     const uint32_t units = a.in_dim / 64;
@@ -450,7 +457,19 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     for (int b = 0; b < kXB - 1; ++b)
         if (u + b < u1) step(u + b, b);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past u1 have landed
-    if constexpr (PAIR) {
+    if constexpr (PAIR && BR == 128) {
+        // one split (the host's plan): the wave's tile 0 holds gate rows r0 + 32 (w % 2) + fm,
+        // tile 1 the up rows of the same lanes. out = silu_mul(f16(gate), f16(up)), as
+        // gh_gemm_reduce_swiglu computes it.
+        const uint32_t row = r0 + (rc / 64) * 32 + fm;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t t = tc + 8 * (r >> 2) + 4 * fg + (r & 3);
+            if (t < a.n && row < a.rows)
+                gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] =
+                    gh_silu_mul_h(gh_f2h(acc[0][0][r]), gh_f2h(acc[0][1][r]));
+        }
+    } else if constexpr (PAIR) {
         // one split (the host's plan): tile 0 holds gate rows r0 + fm, tile 1 the up rows of the
         // same lanes, tile 2 gate rows r0 + 32 + fm in lanes fm < 16 and the matching up rows
         // 16 lanes up. out = silu_mul(f16(gate), f16(up)), as gh_gemm_reduce_swiglu computes it.
@@ -504,6 +523,12 @@ GH_GEMM3T(gh_gemm3_q6k_r96_t128, kQ6K, 96)
 GH_KERNEL __launch_bounds__(512) void gh_gemm3_swiglu_r96_t128(GhGemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_T(96, 32)];
     gemm3_body<kQ4K, 96, 32, 4, GH_GEMM3_XB(32), 1, 4, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
+}
+// the same over 128-row tiles of 64 gate + 64 up rows, eight consumers (outputs whose 48-row
+// pairs would overfill one wave of workgroups: 14B 16384 rows, 256 tiles of 64)
+GH_KERNEL __launch_bounds__(768) void gh_gemm3_swiglu_r128_t128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_T(128, 32)];
+    gemm3_body<kQ4K, 128, 32, 8, GH_GEMM3_XB(32), 2, 4, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
 }
 // 128-token tiles of 128 rows: the activations fetched by four waves, eight consumers of 32
 // tokens x 64 rows (two per SIMD), four producers, 768 threads. Against four consumers of 32
