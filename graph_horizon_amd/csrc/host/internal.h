@@ -98,6 +98,8 @@ enum GhKernel : int {
     K_XCD_PROBE,
     K_GEMM3_SWIGLU_R96_T128,
     K_GEMM3_SWIGLU_R128_T128,
+    K_GEMM3_SWIGLU_R96,
+    K_GEMM4W_SWIGLU_R96,
     K_COUNT
 };
 

@@ -103,6 +103,17 @@ struct WBlock {
 // r0 + lr (lr < 32), up row r0 + lr - 32 (< 64), gate row r0 + lr - 32 (< 80) or up row
 // r0 + lr - 48. BR = 128: rows alternate by 32, gate rows r0 .. + 32 | up rows r0 .. + 32 |
 // gate rows r0 + 32 .. + 32 | up rows r0 + 32 .. + 32.
+template <int BR>
+__device__ __forceinline__ uint32_t pair_row(uint32_t lr, uint64_t& wbase, const GhGemmArgs& a) {
+    if constexpr (BR == 96) {
+        wbase = ((lr >= 32 && lr < 64) || lr >= 80) ? a.aux : a.w;
+        return lr < 64 ? lr % 32u : 32u + (lr - 64) % 16u;
+    } else {
+        wbase = (lr / 32) % 2 ? a.aux : a.w;
+        return (lr / 64) * 32 + lr % 32;
+    }
+}
+
 template <uint32_t FMT, int BR, bool PAIR = false>
 __device__ __forceinline__ void load_wblock(const GhGemmArgs& a, uint32_t r0, uint32_t b, WBlock<FMT>& wb,
                                             uint32_t tid) {
@@ -110,13 +121,7 @@ __device__ __forceinline__ void load_wblock(const GhGemmArgs& a, uint32_t r0, ui
     const uint32_t lr = tid % BR, part = tid / BR;
     uint64_t wbase = a.w;
     uint32_t row = r0 + lr;
-    if constexpr (PAIR && BR == 96) {
-        row = r0 + (lr < 64 ? lr % 32u : 32u + (lr - 64) % 16u);
-        wbase = ((lr >= 32 && lr < 64) || lr >= 80) ? a.aux : a.w;
-    } else if constexpr (PAIR) {
-        row = r0 + (lr / 64) * 32 + lr % 32;
-        wbase = (lr / 32) % 2 ? a.aux : a.w;
-    }
+    if constexpr (PAIR) row = r0 + pair_row<BR>(lr, wbase, a);
     row = min(row, a.rows - 1);
     const uint64_t blk = (uint64_t)row * nb + b;
     if constexpr (FMT == kQ4K) {
@@ -270,6 +275,23 @@ __device__ __forceinline__ void gemm_write(const GhGemmArgs& a, const f16v (&acc
     }
 }
 
+// The 96-row pair tiles' output (one split, the host's plan): one wave's 32 tokens from tc;
+// tile 0 holds gate rows r0 + fm, tile 1 the up rows of the same lanes, tile 2 gate rows
+// r0 + 32 + fm in lanes fm < 16 and the matching up rows 16 lanes up. out = silu_mul(f16(gate),
+// f16(up)), as gh_gemm_reduce_swiglu computes it.
+__device__ __forceinline__ void pair_write96(const GhGemmArgs& a, const f16v (&acc)[1][3], uint32_t tc, uint32_t r0,
+                                             uint32_t fm, uint32_t fg) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float up2 = __shfl_xor(acc[0][2][r], 16);
+        const uint32_t t = tc + 8 * (r >> 2) + 4 * fg + (r & 3);
+        if (t >= a.n) continue;
+        GH_GLOBAL uint16_t* o = gh_gpw<uint16_t>(a.out) + (uint64_t)t * a.rows;
+        if (r0 + fm < a.rows) o[r0 + fm] = gh_silu_mul_h(gh_f2h(acc[0][0][r]), gh_f2h(acc[0][1][r]));
+        if (fm < 16 && r0 + 32 + fm < a.rows) o[r0 + 32 + fm] = gh_silu_mul_h(gh_f2h(acc[0][2][r]), gh_f2h(up2));
+    }
+}
+
 // Warp-specialized variant for long batches: a 512-thread workgroup owns 4·WT tokens x BR rows
 // (WT = 64: 256 tokens; WT = 32: 128 tokens, for chunks of fewer than 256 rows, where split K
 // has to spread the units over many workgroups). Waves 0-3 (consumers) run the matrix cores
@@ -312,9 +334,9 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     constexpr int TI = TW / 32, TJ = BR / (32 * CR), NX = WT / 8;
     constexpr int kS = 3;
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
-    static_assert(!PAIR || (BR == 96 && NC == 4 && NF == 4 && WT == 32 && CR == 1) ||
+    static_assert(!PAIR || (BR == 96 && NC == NF && WT == 32 && CR == 1) ||
                       (BR == 128 && NC == 8 && NF == 4 && WT == 32 && CR == 2),
-                  "pair tiles: 96 rows (four consumers) or 128 rows (eight) x 128 tokens");
+                  "pair tiles: 96 rows (consumers of 32 tokens x 96 rows) or 128 rows (eight consumers)");
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t r0 = bx * (PAIR ? BR / 2 : BR);
     const uint32_t units = a.in_dim / 64;
@@ -470,18 +492,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
                     gh_silu_mul_h(gh_f2h(acc[0][0][r]), gh_f2h(acc[0][1][r]));
         }
     } else if constexpr (PAIR) {
-        // one split (the host's plan): tile 0 holds gate rows r0 + fm, tile 1 the up rows of the
-        // same lanes, tile 2 gate rows r0 + 32 + fm in lanes fm < 16 and the matching up rows
-        // 16 lanes up. out = silu_mul(f16(gate), f16(up)), as gh_gemm_reduce_swiglu computes it.
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float up2 = __shfl_xor(acc[0][2][r], 16);
-            const uint32_t t = tc + 8 * (r >> 2) + 4 * fg + (r & 3);
-            if (t >= a.n) continue;
-            GH_GLOBAL uint16_t* o = gh_gpw<uint16_t>(a.out) + (uint64_t)t * a.rows;
-            if (r0 + fm < a.rows) o[r0 + fm] = gh_silu_mul_h(gh_f2h(acc[0][0][r]), gh_f2h(acc[0][1][r]));
-            if (fm < 16 && r0 + 32 + fm < a.rows) o[r0 + 32 + fm] = gh_silu_mul_h(gh_f2h(acc[0][2][r]), gh_f2h(up2));
-        }
+        pair_write96(a, acc, tc, r0, fm, fg);
     } else {
         gemm_write<TI, TJ, true>(a, acc, tc, r0 + rc, fm, fg, bz, ps, pc);
     }
@@ -507,6 +518,13 @@ GH_GEMM3(gh_gemm3_q4k_r128, kQ4K, 128)
 GH_GEMM3(gh_gemm3_q6k_r128, kQ6K, 128)
 GH_GEMM3(gh_gemm3_q4k_r96, kQ4K, 96)
 GH_GEMM3(gh_gemm3_q6k_r96, kQ6K, 96)
+// SwiGLU's gate (a.w) and up (a.aux) Q4_K projections in one launch of 256-token tiles, each
+// 96-row tile 48 gate rows and the same 48 up rows (pair_row), K unsplit, silu_mul in the
+// epilogue (pair_write96): the gate's FP16 output is neither written nor read back
+GH_KERNEL __launch_bounds__(768) void gh_gemm3_swiglu_r96(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_C8(96)];
+    gemm3_body<kQ4K, 96, 32, 8, 2, 1, 8, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
+}
 // 128-token tiles (consumer waves of 32 tokens)
 #define GH_GEMM3T(NAME, FMT, BR)                                                                   \
     GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
@@ -556,15 +574,16 @@ GH_GEMM3T8(gh_gemm3_q6k_r128_t128, kQ6K, 128)
 // (unit u + 1 landed, every wave's reads of unit u done) unit u + 3 goes into unit u's stage.
 // The k order of every output's sum is the one gemm3_body uses: the same bits.
 #define GH_GEMM4_LDS(BR) (3 * (256 + (BR)) * 64)
-template <uint32_t FMT, int BR>
+template <uint32_t FMT, int BR, bool PAIR = false>
 __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
     static_assert(BR == 128 || BR == 96, "all-waves-MFMA tiles: 128 or 96 rows");
+    static_assert(!PAIR || BR == 96, "pair tiles of the FP16 copies: 96 rows");
     constexpr uint32_t WTOK = BR == 128 ? 64 : 32, WROW = BR == 128 ? 64 : 96;
     constexpr uint32_t NR = BR / WROW, TI = WTOK / 32, TJ = WROW / 32, NB = BR / 8;
     constexpr uint32_t kStage = (256 + BR) * 64;  // halves: A (256 token rows), then B (BR rows)
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, g = wave / NR, hr = wave % NR;
-    const uint32_t r0 = bx * BR;
+    const uint32_t r0 = bx * (PAIR ? BR / 2 : BR);
     const uint32_t units = a.in_dim / 64;
     const uint32_t per = gh_gemm_split_units(units, a.splits);
     const uint32_t u0 = bz * per, u1 = min(units, u0 + per);
@@ -587,7 +606,9 @@ __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, u
 #pragma unroll
     for (uint32_t i = 0; i < kB; ++i) {
         const uint32_t r = 8 * (wave + 8 * i) + (lane >> 3), c = (lane & 7u) ^ ((r >> 1) & 7u);
-        wa[i] = a.w + ((uint64_t)min(r0 + r, a.rows - 1) * units) * 128 + c * 16;
+        uint64_t wbase = a.w;
+        const uint32_t wr = PAIR ? pair_row<BR>(min(r, (uint32_t)BR - 1), wbase, a) : r;
+        wa[i] = wbase + ((uint64_t)min(r0 + wr, a.rows - 1) * units) * 128 + c * 16;
     }
     auto stage = [&](uint32_t st) __attribute__((always_inline)) { return lds + st * kStage; };
     auto issue = [&](uint32_t u, uint32_t st) __attribute__((always_inline)) {
@@ -686,7 +707,10 @@ __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, u
     }
     if (u < u1) step(u, f0, f1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) loads have landed
-    gemm_write<TI, TJ, true>(a, acc, by * 256 + WTOK * g, r0 + WROW * hr, fm, fg, bz, ps, pc);
+    if constexpr (PAIR)
+        pair_write96(a, acc, by * 256 + WTOK * g, r0, fm, fg);
+    else
+        gemm_write<TI, TJ, true>(a, acc, by * 256 + WTOK * g, r0 + WROW * hr, fm, fg, bz, ps, pc);
 }
 #define GH_GEMM4W(NAME, FMT, BR)                                                                   \
     GH_KERNEL __launch_bounds__(512) void NAME(GhGemmArgs a) {                                     \
@@ -697,6 +721,12 @@ GH_GEMM4W(gh_gemm4w_q4k_r128, kQ4K, 128)
 GH_GEMM4W(gh_gemm4w_q6k_r128, kQ6K, 128)
 GH_GEMM4W(gh_gemm4w_q4k_r96, kQ4K, 96)
 GH_GEMM4W(gh_gemm4w_q6k_r96, kQ6K, 96)
+// gh_gemm3_swiglu_r96 over the FP16 copies of gate (a.w) and up (a.aux): the same pair tiles,
+// the same k order
+GH_KERNEL __launch_bounds__(512) void gh_gemm4w_swiglu_r96(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM4_LDS(96)];
+    gemm4_body<kQ4K, 96, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
+}
 
 // A Q4_K / Q6_K matrix [rows][in_dim] dequantized to FP16 in the GEMM's unit order, the layout
 // gemm4_body reads: thread t handles half p = t % 2 of unit u of row r, t / 2 = r · units + u,
