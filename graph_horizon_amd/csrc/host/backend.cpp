@@ -1054,7 +1054,7 @@ int op_gemm(gh_backend* b, uint64_t out, const gh_buf* a, const gh_buf* w, uint3
         ga.norm = e->norm;
         ga.normed = e->normed;
         ga.eps = e->eps;
-        return launch(b, K_GEMM_TAIL, n, 1, 1, 256, &ga);
+        return launch(b, K_GEMM_TAIL, n, 1, 1, 1024, &ga);
     }
     if (p.splits == 1) return GH_OK;
     ga.epi = epi;

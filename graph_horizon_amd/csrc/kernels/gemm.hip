@@ -872,67 +872,55 @@ GH_KERNEL __launch_bounds__(256) void gh_gemm_reduce_seg(GhGemmArgs a) {
     }
 }
 
-// The GEMM's output row t folded into the residual stream, one 256-thread workgroup per row:
+// The GEMM's output row t folded into the residual stream, one 1024-thread workgroup per row:
 // h = f16(Σ_s part[s][t][c]) in split order (gh_gemm_reduce; with one split the GEMM's FP16
 // output), x[t][c] += f32(h) (residual_add, residual.rs:12-22), and with a norm weight the
 // row's RMSNorm f16(x · inverse · f16 w) into `normed` — gh_rmsnorm_x's arithmetic, its Σx²
-// in gh_rms_inverse_256's order (thread t: the 16-value items t, t + 256 of the row) — so the
-// three ops' bits in one pass. rows (the row width) is a multiple of 16 and at most 8192.
-GH_KERNEL __launch_bounds__(256) void gh_gemm_tail(GhGemmArgs a) {
+// in gh_rms_inverse_256's order (threads t < 256: the 16-value items t, t + 256 of the row,
+// then the four waves' sums in order) — so the three ops' bits in one pass. rows (the row
+// width) is a multiple of 16 and at most 8192. The elementwise passes run on all 1024 threads
+// (16 waves of loads in flight per row: with 256 threads, 128-token chunks held 6.9 us for
+// about 10 MB of partials).
+GH_KERNEL __launch_bounds__(1024) void gh_gemm_tail(GhGemmArgs a) {
 #pragma clang fp contract(off)
-    const uint32_t t = blockIdx.x, d = a.rows, n4 = d >> 2;
+    const uint32_t t = blockIdx.x, d = a.rows, n4 = d >> 2, tid = threadIdx.x;
     const uint64_t total = (uint64_t)a.n * d, row0 = (uint64_t)t * d;
     GH_GLOBAL float4* x = gh_gpw<float4>(a.aux) + row0 / 4;
     __shared__ float red[4];
     __shared__ float4 ys[2048];  // the updated residual row (rows <= 8192)
-    // Pass 1, coalesced: thread t takes the float4s t + 256 j (a wave's loads cover whole
-    // lines), 1024 per round. Every load of a round and a group of four splits is requested
-    // before any is summed (clamped indices, no branch around the loads); the splits are summed
-    // in order, the sum rounded to FP16, added into the residual, and the new row kept in LDS.
+    // Pass 1, coalesced: thread t takes float4 j0 + t (a wave's loads cover whole lines), 1024
+    // per round. Every load of a round and a group of four splits is requested before any is
+    // summed (clamped indices, no branch around the loads); the splits are summed in order, the
+    // sum rounded to FP16, added into the residual, and the new row kept in LDS.
     for (uint32_t j0 = 0; j0 < n4; j0 += 1024) {  // launch-uniform: one round up to 4096 rows
-        float4 s[4], xv[4];
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            s[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            xv[j] = x[min(j0 + threadIdx.x + 256 * j, n4 - 1)];
-        }
+        const uint32_t c = min(j0 + tid, n4 - 1);
+        float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 xv = x[c];
         if (a.splits > 1) {
             for (uint32_t k0 = 0; k0 < a.splits; k0 += 4) {
-                float4 p[4][4];
+                float4 p[4];
 #pragma unroll
                 for (uint32_t kk = 0; kk < 4; ++kk)
+                    p[kk] = gh_gp<float4>(a.part)[(min(k0 + kk, a.splits - 1) * total + row0) / 4 + c];
 #pragma unroll
-                    for (uint32_t j = 0; j < 4; ++j) {
-                        const uint32_t k = min(k0 + kk, a.splits - 1), c = min(j0 + threadIdx.x + 256 * j, n4 - 1);
-                        p[kk][j] = gh_gp<float4>(a.part)[(k * total + row0) / 4 + c];
+                for (uint32_t kk = 0; kk < 4; ++kk)
+                    if (k0 + kk < a.splits) {
+                        s.x += p[kk].x;
+                        s.y += p[kk].y;
+                        s.z += p[kk].z;
+                        s.w += p[kk].w;
                     }
-#pragma unroll
-                for (uint32_t kk = 0; kk < 4; ++kk)
-                    if (k0 + kk < a.splits)
-#pragma unroll
-                        for (uint32_t j = 0; j < 4; ++j) {
-                            s[j].x += p[kk][j].x;
-                            s[j].y += p[kk][j].y;
-                            s[j].z += p[kk][j].z;
-                            s[j].w += p[kk][j].w;
-                        }
             }
         } else {
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
-                const uint2 o = gh_gp<uint2>(a.out)[row0 / 4 + min(j0 + threadIdx.x + 256 * j, n4 - 1)];
-                s[j] = make_float4(gh_h2f(o.x & 0xFFFFu), gh_h2f(o.x >> 16), gh_h2f(o.y & 0xFFFFu), gh_h2f(o.y >> 16));
-            }
+            const uint2 o = gh_gp<uint2>(a.out)[row0 / 4 + c];
+            s = make_float4(gh_h2f(o.x & 0xFFFFu), gh_h2f(o.x >> 16), gh_h2f(o.y & 0xFFFFu), gh_h2f(o.y >> 16));
         }
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            const uint32_t c = j0 + threadIdx.x + 256 * j;
-            if (c >= n4) continue;
+        if (j0 + tid < n4) {
             // one split: s already holds the FP16 output; several: round their sum to FP16
-            const float4 h = a.splits > 1 ? make_float4(gh_h2f(gh_f2h(s[j].x)), gh_h2f(gh_f2h(s[j].y)),
-                                                        gh_h2f(gh_f2h(s[j].z)), gh_h2f(gh_f2h(s[j].w)))
-                                          : s[j];
-            float4 y = xv[j];
+            const float4 h = a.splits > 1 ? make_float4(gh_h2f(gh_f2h(s.x)), gh_h2f(gh_f2h(s.y)),
+                                                        gh_h2f(gh_f2h(s.z)), gh_h2f(gh_f2h(s.w)))
+                                          : s;
+            float4 y = xv;
             y.x = y.x + h.x;
             y.y = y.y + h.y;
             y.z = y.z + h.z;
@@ -943,34 +931,32 @@ GH_KERNEL __launch_bounds__(256) void gh_gemm_tail(GhGemmArgs a) {
     }
     if (!a.norm) return;  // launch-uniform
     __syncthreads();
-    // Pass 2: thread t takes the 16-value items t, t + 256 of the row back from LDS, in
-    // gh_rms_inverse_256's order, for the sum of squares and the normalized FP16 values.
-    float4 v[2][4];
+    // Pass 2: threads t < 256 take the 16-value items t, t + 256 of the row back from LDS, in
+    // gh_rms_inverse_256's order, for the sum of squares (gh_rms_finish_256's reduction, its
+    // four waves' sums in order); every thread then normalizes float4s tid + 1024 k.
     float ss = 0.0f;
+    if (tid < 256) {
 #pragma unroll
-    for (uint32_t it = 0; it < 2; ++it)
+        for (uint32_t it = 0; it < 2; ++it)
 #pragma unroll
-        for (uint32_t q = 0; q < 4; ++q) {
-            const uint32_t c = 4 * (threadIdx.x + 256 * it) + q;
-            if (c >= n4) continue;
-            v[it][q] = ys[c];
-            ss = gh_rms_add(ss, v[it][q]);
-        }
-    const float inverse = gh_rms_finish_256(ss, d, a.eps, red);
+            for (uint32_t q = 0; q < 4; ++q) {
+                const uint32_t c = 4 * (tid + 256 * it) + q;
+                if (c < n4) ss = gh_rms_add(ss, ys[c]);
+            }
+    }
+    ss = gh_wave_sum63(ss);
+    if (tid < 256 && (tid & 63) == 63) red[tid >> 6] = ss;
+    __syncthreads();
+    const float inverse = 1.0f / __builtin_sqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)d + a.eps);
     const GH_GLOBAL uint2* w = gh_gp<uint2>(a.norm);
     GH_GLOBAL uint2* out = gh_gpw<uint2>(a.normed) + row0 / 4;
-#pragma unroll
-    for (uint32_t it = 0; it < 2; ++it)
-#pragma unroll
-        for (uint32_t q = 0; q < 4; ++q) {
-            const uint32_t c = 4 * (threadIdx.x + 256 * it) + q;
-            if (c >= n4) continue;
-            const float4 xv = v[it][q];
-            const uint2 wv = w[c];
-            const uint32_t o0 = gh_f2h(xv.x * inverse * gh_h2f(wv.x & 0xFFFFu));
-            const uint32_t o1 = gh_f2h(xv.y * inverse * gh_h2f(wv.x >> 16));
-            const uint32_t o2 = gh_f2h(xv.z * inverse * gh_h2f(wv.y & 0xFFFFu));
-            const uint32_t o3 = gh_f2h(xv.w * inverse * gh_h2f(wv.y >> 16));
-            out[c] = make_uint2(o0 | (o1 << 16), o2 | (o3 << 16));
-        }
+    for (uint32_t c = tid; c < n4; c += 1024) {
+        const float4 xv = ys[c];
+        const uint2 wv = w[c];
+        const uint32_t o0 = gh_f2h(xv.x * inverse * gh_h2f(wv.x & 0xFFFFu));
+        const uint32_t o1 = gh_f2h(xv.y * inverse * gh_h2f(wv.x >> 16));
+        const uint32_t o2 = gh_f2h(xv.z * inverse * gh_h2f(wv.y & 0xFFFFu));
+        const uint32_t o3 = gh_f2h(xv.w * inverse * gh_h2f(wv.y >> 16));
+        out[c] = make_uint2(o0 | (o1 << 16), o2 | (o3 << 16));
+    }
 }
