@@ -67,6 +67,7 @@ const KernelName kKernels[] = {
     {K_XCD_PROBE, "gh_xcd_probe"},
     {K_GEMM3_SWIGLU_R96_T128, "gh_gemm3_swiglu_r96_t128"}, {K_GEMM3_SWIGLU_R128_T128, "gh_gemm3_swiglu_r128_t128"},
     {K_GEMM3_SWIGLU_R96, "gh_gemm3_swiglu_r96"},           {K_GEMM4W_SWIGLU_R96, "gh_gemm4w_swiglu_r96"},
+    {K_GEMM3_SWIGLU_R128, "gh_gemm3_swiglu_r128"},         {K_GEMM4W_SWIGLU_R128, "gh_gemm4w_swiglu_r128"},
 };
 
 const char* kModules[] = {"gh_quant", "gh_gemv", "gh_glue", "gh_attention", "gh_gemm"};
@@ -1096,15 +1097,16 @@ int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const g
         return launch(b, pair96 ? K_GEMM3_SWIGLU_R96_T128 : K_GEMM3_SWIGLU_R128_T128, pair_tiles, ceil_div(n, 128u),
                       1, pair96 ? 512 : 768, &ga);
     }
-    // Longer chunks whose separate GEMMs run K unsplit in 96-row tiles (8B at 256-1024 tokens):
-    // the same pairs in 256-token tiles, so each sum is the separate launch's, over the FP16
-    // copies when both weights have one (8B 512-token prefill 11.73 -> 11.56-11.65 ms, same
-    // box). Where the fill rule picks 128-row tiles (8B 2048 tokens) the separate launches
-    // stay: pairs of 96 rows measured 34.6 -> 36.4 ms there.
+    // Longer chunks whose separate GEMMs run K unsplit: the same pairs in 256-token tiles of the
+    // separate launches' height (96 rows: 8B at 256-1024 tokens; 128 rows where the fill rule
+    // picks them: 8B at 2048, 14B), so each sum is the separate launch's, over the FP16 copies
+    // when both weights have one (8B 512-token prefill 11.73 -> 11.56-11.65 ms, same box; 96-row
+    // pairs where the separate launches take 128 rows measured 34.6 -> 36.4 ms at 2048)
     const GemmPlan pg = plan_gemm(b, wg, n), pu = plan_gemm(b, wu, n);
     const bool r96 = pg.k == K_GEMM4W_Q4K_R96 || pg.k == K_GEMM3_Q4K_R96;
+    const bool r128 = pg.k == K_GEMM4W_Q4K_R128 || pg.k == K_GEMM3_Q4K_R128;
     if (n >= kGemmTallTokens && wg->format == GH_FMT_Q4_K && wu->format == GH_FMT_Q4_K && pg.splits == 1 &&
-        pu.splits == 1 && r96 && pu.k == pg.k) {
+        pu.splits == 1 && (r96 || r128) && pu.k == pg.k) {
         const auto cg = b->w16.find(wg->addr), cu = b->w16.find(wu->addr);
         const bool copies = cg != b->w16.end() && cu != b->w16.end();
         GhGemmArgs ga{};
@@ -1116,8 +1118,9 @@ int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const g
         ga.rows = wg->rows;
         ga.n = n;
         ga.splits = 1;
-        return launch(b, copies ? K_GEMM4W_SWIGLU_R96 : K_GEMM3_SWIGLU_R96, ceil_div(wg->rows, 48u), ceil_div(n, 256u), 1,
-                      copies ? 512 : 768, &ga);
+        const GhKernel k = r96 ? (copies ? K_GEMM4W_SWIGLU_R96 : K_GEMM3_SWIGLU_R96)
+                               : (copies ? K_GEMM4W_SWIGLU_R128 : K_GEMM3_SWIGLU_R128);
+        return launch(b, k, ceil_div(wg->rows, r96 ? 48u : 64u), ceil_div(n, 256u), 1, copies ? 512 : 768, &ga);
     }
     if (pg.splits == 1 || pu.splits != pg.splits || wg->rows % 4) {
         GemmEpi e;

@@ -100,6 +100,8 @@ enum GhKernel : int {
     K_GEMM3_SWIGLU_R128_T128,
     K_GEMM3_SWIGLU_R96,
     K_GEMM4W_SWIGLU_R96,
+    K_GEMM3_SWIGLU_R128,
+    K_GEMM4W_SWIGLU_R128,
     K_COUNT
 };
 

@@ -292,6 +292,24 @@ __device__ __forceinline__ void pair_write96(const GhGemmArgs& a, const f16v (&a
     }
 }
 
+// The 128-row pair tiles' output (one split): a wave holding 64 tile rows has gate rows
+// row0 + fm in its tile 0 and the up rows of the same lanes in tile 1, for TI token tiles of 32
+// from tc. out = silu_mul(f16(gate), f16(up)), as gh_gemm_reduce_swiglu computes it.
+template <int TI>
+__device__ __forceinline__ void pair_write128(const GhGemmArgs& a, const f16v (&acc)[TI][2], uint32_t tc,
+                                              uint32_t row0, uint32_t fm, uint32_t fg) {
+    const uint32_t row = row0 + fm;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t t = tc + 32 * i + 8 * (r >> 2) + 4 * fg + (r & 3);
+            if (t < a.n && row < a.rows)
+                gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] =
+                    gh_silu_mul_h(gh_f2h(acc[i][0][r]), gh_f2h(acc[i][1][r]));
+        }
+}
+
 // Warp-specialized variant for long batches: a 512-thread workgroup owns 4·WT tokens x BR rows
 // (WT = 64: 256 tokens; WT = 32: 128 tokens, for chunks of fewer than 256 rows, where split K
 // has to spread the units over many workgroups). Waves 0-3 (consumers) run the matrix cores
@@ -334,9 +352,8 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
     constexpr int TI = TW / 32, TJ = BR / (32 * CR), NX = WT / 8;
     constexpr int kS = 3;
     auto wstage = [&](uint32_t st) __attribute__((always_inline)) { return lds3 + st * (BR * LDK); };
-    static_assert(!PAIR || (BR == 96 && NC == NF && WT == 32 && CR == 1) ||
-                      (BR == 128 && NC == 8 && NF == 4 && WT == 32 && CR == 2),
-                  "pair tiles: 96 rows (consumers of 32 tokens x 96 rows) or 128 rows (eight consumers)");
+    static_assert(!PAIR || (BR == 96 && NC == NF && WT == 32 && CR == 1) || (BR == 128 && NC == 8 && CR == 2),
+                  "pair tiles: 96 rows (consumers of 32 tokens x 96 rows) or 128 rows (eight consumers of 64 rows)");
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t r0 = bx * (PAIR ? BR / 2 : BR);
     const uint32_t units = a.in_dim / 64;
@@ -480,17 +497,7 @@ __device__ __forceinline__ void gemm3_body(const GhGemmArgs& a, _Float16* lds3, 
         if (u + b < u1) step(u + b, b);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past u1 have landed
     if constexpr (PAIR && BR == 128) {
-        // one split (the host's plan): the wave's tile 0 holds gate rows r0 + 32 (w % 2) + fm,
-        // tile 1 the up rows of the same lanes. out = silu_mul(f16(gate), f16(up)), as
-        // gh_gemm_reduce_swiglu computes it.
-        const uint32_t row = r0 + (rc / 64) * 32 + fm;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t t = tc + 8 * (r >> 2) + 4 * fg + (r & 3);
-            if (t < a.n && row < a.rows)
-                gh_gpw<uint16_t>(a.out)[(uint64_t)t * a.rows + row] =
-                    gh_silu_mul_h(gh_f2h(acc[0][0][r]), gh_f2h(acc[0][1][r]));
-        }
+        pair_write128(a, acc, tc, r0 + (rc / 64) * 32, fm, fg);
     } else if constexpr (PAIR) {
         pair_write96(a, acc, tc, r0, fm, fg);
     } else {
@@ -524,6 +531,12 @@ GH_GEMM3(gh_gemm3_q6k_r96, kQ6K, 96)
 GH_KERNEL __launch_bounds__(768) void gh_gemm3_swiglu_r96(GhGemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_C8(96)];
     gemm3_body<kQ4K, 96, 32, 8, 2, 1, 8, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
+}
+// the same over 128-row tiles of 64 gate + 64 up rows (pair_row<128>; eight consumers of 64
+// tokens x 64 rows), where the separate launches take 128-row tiles
+GH_KERNEL __launch_bounds__(768) void gh_gemm3_swiglu_r128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM3_LDS_C8(128)];
+    gemm3_body<kQ4K, 128, 32, 8, 2, 2, 8, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
 }
 // 128-token tiles (consumer waves of 32 tokens)
 #define GH_GEMM3T(NAME, FMT, BR)                                                                   \
@@ -578,7 +591,7 @@ template <uint32_t FMT, int BR, bool PAIR = false>
 __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, uint32_t bx, uint32_t by,
                                            uint32_t bz, uint64_t ps, uint64_t pc) {
     static_assert(BR == 128 || BR == 96, "all-waves-MFMA tiles: 128 or 96 rows");
-    static_assert(!PAIR || BR == 96, "pair tiles of the FP16 copies: 96 rows");
+
     constexpr uint32_t WTOK = BR == 128 ? 64 : 32, WROW = BR == 128 ? 64 : 96;
     constexpr uint32_t NR = BR / WROW, TI = WTOK / 32, TJ = WROW / 32, NB = BR / 8;
     constexpr uint32_t kStage = (256 + BR) * 64;  // halves: A (256 token rows), then B (BR rows)
@@ -707,7 +720,9 @@ __device__ __forceinline__ void gemm4_body(const GhGemmArgs& a, _Float16* lds, u
     }
     if (u < u1) step(u, f0, f1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) loads have landed
-    if constexpr (PAIR)
+    if constexpr (PAIR && BR == 128)
+        pair_write128(a, acc, by * 256 + WTOK * g, r0 + 32 * hr, fm, fg);
+    else if constexpr (PAIR)
         pair_write96(a, acc, by * 256 + WTOK * g, r0, fm, fg);
     else
         gemm_write<TI, TJ, true>(a, acc, by * 256 + WTOK * g, r0 + WROW * hr, fm, fg, bz, ps, pc);
@@ -726,6 +741,10 @@ GH_GEMM4W(gh_gemm4w_q6k_r96, kQ6K, 96)
 GH_KERNEL __launch_bounds__(512) void gh_gemm4w_swiglu_r96(GhGemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM4_LDS(96)];
     gemm4_body<kQ4K, 96, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
+}
+GH_KERNEL __launch_bounds__(512) void gh_gemm4w_swiglu_r128(GhGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[GH_GEMM4_LDS(128)];
+    gemm4_body<kQ4K, 128, true>(a, lds, blockIdx.x, blockIdx.y, blockIdx.z, a.rows, 0);
 }
 
 // A Q4_K / Q6_K matrix [rows][in_dim] dequantized to FP16 in the GEMM's unit order, the layout
