@@ -1105,8 +1105,13 @@ int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const g
     const GemmPlan pg = plan_gemm(b, wg, n), pu = plan_gemm(b, wu, n);
     const bool r96 = pg.k == K_GEMM4W_Q4K_R96 || pg.k == K_GEMM3_Q4K_R96;
     const bool r128 = pg.k == K_GEMM4W_Q4K_R128 || pg.k == K_GEMM3_Q4K_R128;
-    if (n >= kGemmTallTokens && wg->format == GH_FMT_Q4_K && wu->format == GH_FMT_Q4_K && pg.splits == 1 &&
-        pu.splits == 1 && (r96 || r128) && pu.k == pg.k) {
+    // Where the separate launches split K (8B at 129-255 tokens: 128 tiles x 2 splits and a
+    // split reduce), 96-row pairs unsplit instead when they fill the CUs in one pass, at least
+    // half of them: the 128-token tiles' trade, in 256-token tiles
+    const uint32_t tt = ceil_div(n, 256u), p96 = ceil_div(wg->rows, 48u) * tt;
+    const bool split_pairs = pg.splits > 1 && p96 <= b->cus && 2 * p96 >= b->cus;
+    if (n >= kGemmTallTokens && wg->format == GH_FMT_Q4_K && wu->format == GH_FMT_Q4_K &&
+        ((pg.splits == 1 && pu.splits == 1 && (r96 || r128) && pu.k == pg.k) || split_pairs)) {
         const auto cg = b->w16.find(wg->addr), cu = b->w16.find(wu->addr);
         const bool copies = cg != b->w16.end() && cu != b->w16.end();
         GhGemmArgs ga{};
@@ -1118,9 +1123,10 @@ int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const g
         ga.rows = wg->rows;
         ga.n = n;
         ga.splits = 1;
-        const GhKernel k = r96 ? (copies ? K_GEMM4W_SWIGLU_R96 : K_GEMM3_SWIGLU_R96)
-                               : (copies ? K_GEMM4W_SWIGLU_R128 : K_GEMM3_SWIGLU_R128);
-        return launch(b, k, ceil_div(wg->rows, r96 ? 48u : 64u), ceil_div(n, 256u), 1, copies ? 512 : 768, &ga);
+        const bool p96t = r96 || split_pairs;
+        const GhKernel k = p96t ? (copies ? K_GEMM4W_SWIGLU_R96 : K_GEMM3_SWIGLU_R96)
+                                : (copies ? K_GEMM4W_SWIGLU_R128 : K_GEMM3_SWIGLU_R128);
+        return launch(b, k, ceil_div(wg->rows, p96t ? 48u : 64u), tt, 1, copies ? 512 : 768, &ga);
     }
     if (pg.splits == 1 || pu.splits != pg.splits || wg->rows % 4) {
         GemmEpi e;
