@@ -1108,8 +1108,9 @@ int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const g
     // Where the separate launches split K (8B at 129-255 tokens: 128 tiles x 2 splits and a
     // split reduce), 96-row pairs unsplit instead when they fill the CUs in one pass, at least
     // half of them: the 128-token tiles' trade, in 256-token tiles
-    const uint32_t tt = ceil_div(n, 256u), p96 = ceil_div(wg->rows, 48u) * tt;
-    const bool split_pairs = pg.splits > 1 && p96 <= b->cus && 2 * p96 >= b->cus;
+    const uint32_t tt = ceil_div(n, 256u), p96 = ceil_div(wg->rows, 48u) * tt, p128 = ceil_div(wg->rows, 64u) * tt;
+    const bool fits96 = p96 <= b->cus && 2 * p96 >= b->cus, fits128 = p128 <= b->cus && 2 * p128 >= b->cus;
+    const bool split_pairs = pg.splits > 1 && (fits96 || fits128);  // 128-row pairs: 14B, 256 tiles
     if (n >= kGemmTallTokens && wg->format == GH_FMT_Q4_K && wu->format == GH_FMT_Q4_K &&
         ((pg.splits == 1 && pu.splits == 1 && (r96 || r128) && pu.k == pg.k) || split_pairs)) {
         const auto cg = b->w16.find(wg->addr), cu = b->w16.find(wu->addr);
@@ -1123,7 +1124,7 @@ int op_gemm_swiglu(gh_backend* b, const gh_buf* out, const gh_buf* gate, const g
         ga.rows = wg->rows;
         ga.n = n;
         ga.splits = 1;
-        const bool p96t = r96 || split_pairs;
+        const bool p96t = split_pairs ? fits96 : r96;
         const GhKernel k = p96t ? (copies ? K_GEMM4W_SWIGLU_R96 : K_GEMM3_SWIGLU_R96)
                                 : (copies ? K_GEMM4W_SWIGLU_R128 : K_GEMM3_SWIGLU_R128);
         return launch(b, k, ceil_div(wg->rows, p96t ? 48u : 64u), tt, 1, copies ? 512 : 768, &ga);
