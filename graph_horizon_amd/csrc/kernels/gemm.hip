@@ -20,7 +20,9 @@
 //     the matrix cores; activation lines and weight rows both arrive by LDS DMA, and the k
 //     order of every sum is gemm3_body's, so the bits are the same.
 // A multi-matrix launch (gemm3_mixed, the prefill's Q/K/V) runs each row tile in its matrix's
-// format over the shared LDS block.
+// format over the shared LDS block. SwiGLU's gate and up run as one launch of pair tiles
+// (gh_gemm3/4w_swiglu_*): each tile holds matching gate and up rows (pair_row), K unsplit, and
+// the consumers apply silu_mul to their sums in registers (pair_write96 / pair_write128).
 //
 // A Q6_K unit's 64 weights are not contiguous in k (16 from each quarter of a 128-weight half
 // block); x is staged in the same permuted order, which leaves every dot product unchanged.
@@ -98,8 +100,8 @@ struct WBlock {
     uint32_t d;                       // Q6_K: d (FP16 bits)
 };
 
-// PAIR (SwiGLU's gate and up in one tile, gh_gemm3_swiglu_*_t128; the gate matrix at a.w, the up
-// matrix of the same shape at a.aux), r0 = BR / 2 · tile. BR = 96: LDS row lr holds gate row
+// PAIR (SwiGLU's gate and up in one tile, the gh_gemm3/4w_swiglu_* kernels; the gate matrix at
+// a.w, the up matrix of the same shape at a.aux), r0 = BR / 2 · tile. BR = 96: LDS row lr holds gate row
 // r0 + lr (lr < 32), up row r0 + lr - 32 (< 64), gate row r0 + lr - 32 (< 80) or up row
 // r0 + lr - 48. BR = 128: rows alternate by 32, gate rows r0 .. + 32 | up rows r0 .. + 32 |
 // gate rows r0 + 32 .. + 32 | up rows r0 + 32 .. + 32.
