@@ -201,7 +201,10 @@ __device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* 
         const float db = d * (float)(int8_t)(scw[ib >> 2] >> (8 * (ib & 3u)));
         const float na = -32.0f * da, nb = -32.0f * db;
         const uint32_t qh[4] = {ws.qh.x, ws.qh.y, ws.qh.z, ws.qh.w};
-        const uint32_t sl = 2 * part, sh = 4 + 2 * part;
+        // the two high bits of each quant moved to bits 4-5 of its byte in one shift:
+        // ((qh >> 2 part) & 3) << 4 = (qh << (4 - 2 part)) & 0x30, ((qh >> (4 + 2 part)) & 3) << 4
+        // = (qh >> 2 part) & 0x30 (part is 0 or 1)
+        const uint32_t sl = 4 - 2 * part, sh = 2 * part;
         auto w2 = [](uint32_t q4, int e, float sc, float bias) __attribute__((always_inline)) {
             typedef _Float16 hv2 __attribute__((ext_vector_type(2)));
             const float f0 = (float)((q4 >> (8 * e)) & 0xFFu), f1 = (float)((q4 >> (8 * e + 8)) & 0xFFu);
@@ -210,8 +213,8 @@ __device__ __forceinline__ void store_w(uint32_t u, const WStage& ws, _Float16* 
         };
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t qa4 = (qw[j] & 0x0F0F0F0Fu) | (((qh[j] >> sl) & 0x03030303u) << 4);
-            const uint32_t qb4 = ((qw[j] >> 4) & 0x0F0F0F0Fu) | (((qh[j] >> sh) & 0x03030303u) << 4);
+            const uint32_t qa4 = (qw[j] & 0x0F0F0F0Fu) | ((qh[j] << sl) & 0x30303030u);
+            const uint32_t qb4 = ((qw[j] >> 4) & 0x0F0F0F0Fu) | ((qh[j] >> sh) & 0x30303030u);
             lo[2 * j] = w2(qa4, 0, da, na);
             lo[2 * j + 1] = w2(qa4, 2, da, na);
             hi[2 * j] = w2(qb4, 0, db, nb);
