@@ -95,11 +95,13 @@ def test_8b_full_depth_greedy_64_matches_oracle(hip):
     assert_agreement([first] + [int(t) for t in toks], ora, "8b full depth, 64 greedy steps")
 
 
-@pytest.mark.parametrize("n", [100, 300])
+@pytest.mark.parametrize("n", [100, 160, 300])
 @pytest.mark.parametrize("name", ["8b", "14b"])
 def test_full_width_prefill_driver_matches_op_by_op(hip, name, n):
     """The driver's fused prefill at the real widths, 300 rows in one chunk (a partial second
-    256-token tile, over the FP16 weight copies) or 100 rows (one partial 128-token tile of the
+    256-token tile, over the FP16 weight copies), 160 rows (one partial 256-token tile, where
+    the separate gate/up GEMMs split K and the driver's paired gate/up launch does not) or 100
+    rows (one partial 128-token tile of the
     dequantizing kernels, no copies) — Q/K/V in one mixed-format GEMM with its RoPE split reduce writing K/V into
     the cache, the O and down projections' split sums folded into the residual and the
     RMSNorm, SiLU in the up GEMM, 16-row attention blocks — against every trait op recorded
